@@ -1,0 +1,166 @@
+// The C ABI: host-side validation, chunking and launch order, mirroring the attention parts of
+// Engine.encodeAttention (Sources/EmblaMetal/Engine.swift:743-832) and Prefill.encode
+// (Sources/EmblaMetal/Prefill.swift:290-341, 378-407).
+#include <stdlib.h>
+#include <string.h>
+#include "embla_internal.hpp"
+
+using namespace embla;
+
+namespace {
+
+constexpr size_t kCounterBytes = 1024;  // reserved (zeroed by embla_workspace_init)
+constexpr int kMaxChunks = 256;         // chunks the merge kernel takes (decode_full.hip)
+constexpr int kMaxKV = 16;
+constexpr int kPartStride = 132;        // floats a (chunk, query head) partial: acc[128], m, l, pad
+
+size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+struct Workspace {
+    uint32_t* counter;
+    uint16_t* qprep;
+    float* part;
+};
+
+size_t qprep_bytes(int n_q) { return round_up((size_t)n_q * 128 * 2, 256); }
+size_t part_bytes(int max_s, int n_q) { return (size_t)((max_s + 31) / 32) * n_q * kPartStride * 4; }
+
+Workspace carve(void* ws, int max_s, int n_q) {
+    char* p = (char*)ws;
+    Workspace w;
+    w.counter = (uint32_t*)p;
+    w.qprep = (uint16_t*)(p + kCounterBytes);
+    w.part = (float*)(p + kCounterBytes + qprep_bytes(n_q));
+    return w;
+}
+
+int env_int(const char* name, int dflt) {
+    const char* s = getenv(name);
+    if (!s || !*s) return dflt;
+    return atoi(s);
+}
+
+/// Keys a workgroup for the split decode: about EMBLA_DECODE_WG workgroups over all kv heads
+/// (default 512, two a CU on MI355X), at most kMaxChunks a kv head, at least 128 keys (one 32-key
+/// tile a wave), a multiple of 32. The reference's chunks8 makes the same choice for its GPU (Engine.swift:736-739).
+int decode_chunk(int S, int n_kv) {
+    const int target = env_int("EMBLA_DECODE_WG", 512);
+    int per_head = target / n_kv > 0 ? target / n_kv : 1;
+    if (per_head > kMaxChunks) per_head = kMaxChunks;
+    int ch = (S + per_head - 1) / per_head;
+    ch = (ch + 31) / 32 * 32;
+    return ch < 128 ? 128 : ch;
+}
+
+bool valid_act(int dt) { return dt == EMBLA_F16 || dt == EMBLA_BF16; }
+bool valid_scale(int dt) { return dt == EMBLA_F16 || dt == EMBLA_F32; }
+
+}  // namespace
+
+extern "C" {
+
+int embla_version(void) { return 1; }
+
+size_t embla_workspace_bytes(int max_s, int n_q) {
+    if (max_s <= 0 || n_q <= 0) return 0;
+    return kCounterBytes + qprep_bytes(n_q) + part_bytes(max_s, n_q);
+}
+
+int embla_workspace_init(void* ws, size_t ws_bytes, hipStream_t stream) {
+    if (!ws || ws_bytes < kCounterBytes) return EMBLA_ERR_WORKSPACE;
+    return hipMemsetAsync(ws, 0, kCounterBytes, stream) == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
+}
+
+int embla_decode_int8(const void* q, const void* kc, const void* vc, void* o, float* scores, int S,
+                      int max_s, int n_q, int n_kv, int weights, int scale_dtype, int out_dtype,
+                      int chunk, void* ws, size_t ws_bytes, hipStream_t stream) {
+    if (!q || !kc || !vc || !o) return EMBLA_ERR_INVALID;
+    if (S <= 0 || max_s <= 0 || max_s % 32 || S > max_s) return EMBLA_ERR_INVALID;
+    if (n_kv <= 0 || n_q % n_kv || n_kv > kMaxKV) return EMBLA_ERR_INVALID;
+    if (weights != EMBLA_SOFTMAX && weights != EMBLA_RELU2_SINK) return EMBLA_ERR_INVALID;
+    if (!valid_scale(scale_dtype) || !valid_act(out_dtype)) return EMBLA_ERR_INVALID;
+    if (scores && weights != EMBLA_RELU2_SINK) return EMBLA_ERR_UNSUPPORTED;
+    if (chunk < 0 || chunk % 32) return EMBLA_ERR_INVALID;
+    const int ch = chunk ? chunk : decode_chunk(S, n_kv);
+    const int C = (S + ch - 1) / ch;
+    if (C > kMaxChunks) return EMBLA_ERR_INVALID;
+    if (C > 1) {
+        if (!ws || ws_bytes < embla_workspace_bytes(max_s, n_q)) return EMBLA_ERR_WORKSPACE;
+        if ((size_t)C * n_q * kPartStride * 4 > part_bytes(max_s, n_q)) return EMBLA_ERR_WORKSPACE;
+    }
+    Workspace w = ws ? carve(ws, max_s, n_q) : Workspace{nullptr, nullptr, nullptr};
+    FullDecodeArgs a;
+    a.q = (const uint16_t*)q;
+    a.kc = (const int8_t*)kc;
+    a.vc = (const int8_t*)vc;
+    a.part = w.part;
+    a.scores = scores;
+    a.o = (uint16_t*)o;
+    a.S = S; a.CH = ch; a.C = C; a.max_s = max_s; a.n_q = n_q; a.n_kv = n_kv;
+    a.relu2 = weights == EMBLA_RELU2_SINK;
+    a.scale32 = scale_dtype == EMBLA_F32;
+    a.out_bf16 = out_dtype == EMBLA_BF16;
+    return launch_full_decode(a, stream);
+}
+
+int embla_q_prep(const void* qraw, const void* g1, const void* g2, int ng, int stride, int T,
+                 int n_q, void* out, int out_dtype, hipStream_t stream) {
+    if (!qraw || !out || T <= 0 || n_q <= 0 || ng < 0 || ng > 2 || stride < n_q * 128) return EMBLA_ERR_INVALID;
+    if ((ng >= 1 && !g1) || (ng >= 2 && !g2) || !valid_act(out_dtype)) return EMBLA_ERR_INVALID;
+    QPrepArgs a{(const uint16_t*)qraw, (const uint16_t*)g1, (const uint16_t*)g2, ng, stride, T, n_q,
+                (uint16_t*)out, out_dtype == EMBLA_BF16};
+    return launch_q_prep(a, stream);
+}
+
+int embla_attn_full8(const void* qraw, const void* g1, const void* g2, const void* kc, const void* vc,
+                     float* part, float* scores, uint32_t* counter, void* o, const EmblaAttnParams* p,
+                     hipStream_t stream) {
+    if (!p || !part || !counter) return EMBLA_ERR_INVALID;
+    if (p->S <= 0 || p->maxS <= 0 || p->maxS % 32 || p->S > p->maxS) return EMBLA_ERR_INVALID;
+    // the reference's part buffer doubles as this call's workspace: q, then the partials
+    const size_t need = embla_workspace_bytes(p->maxS, 16);
+    Workspace w = carve(part, p->maxS, 16);
+    int rc = embla_q_prep(qraw, g1, g2, p->ng, 16 * 128, 1, 16, w.qprep, EMBLA_F16, stream);
+    if (rc) return rc;
+    const int ch = p->CH > 0 ? p->CH : decode_chunk(p->S, 2);
+    if (ch % 32 || (p->S + ch - 1) / ch > kMaxChunks) return EMBLA_ERR_INVALID;
+    FullDecodeArgs a;
+    a.q = w.qprep;
+    a.kc = (const int8_t*)kc;
+    a.vc = (const int8_t*)vc;
+    a.part = w.part;
+    (void)counter;   // no counters: the partials are merged by a second kernel
+    a.scores = scores;
+    a.o = (uint16_t*)o;
+    a.S = p->S; a.CH = ch; a.C = (p->S + ch - 1) / ch; a.max_s = p->maxS; a.n_q = 16; a.n_kv = 2;
+    a.relu2 = true; a.scale32 = true; a.out_bf16 = true;
+    (void)need;
+    return launch_full_decode(a, stream);
+}
+
+int embla_kv_quant_append(const void* k, const void* v, int in_dtype, int stride, int T, int p0,
+                          int n_kv, void* kc, void* vc, int max_s, int scale_dtype, int norm_k,
+                          hipStream_t stream) {
+    if (!k || !v || !kc || !vc || T <= 0 || p0 < 0 || n_kv <= 0 || stride < n_kv * 128) return EMBLA_ERR_INVALID;
+    if (max_s <= 0 || max_s % 32 || p0 + T > max_s) return EMBLA_ERR_INVALID;
+    if (!valid_act(in_dtype) || !valid_scale(scale_dtype)) return EMBLA_ERR_INVALID;
+    KVQuantArgs a{(const uint16_t*)k, (const uint16_t*)v, stride, T, p0, n_kv, max_s,
+                  (int8_t*)kc, (int8_t*)vc, in_dtype == EMBLA_BF16, scale_dtype == EMBLA_F32, norm_k != 0};
+    return launch_kv_quant(a, stream);
+}
+
+int embla_kv_append(const void* qkv, void* cache, const EmblaKVJob* jobs, int njobs, int pm_pos,
+                    int maxS, int T, hipStream_t stream) {
+    if (!qkv || !cache || !jobs || njobs <= 0 || T <= 0) return EMBLA_ERR_INVALID;
+    for (int i = 0; i < njobs; i++) {
+        const EmblaKVJob& j = jobs[i];
+        const uint16_t* base = (const uint16_t*)qkv;
+        char* c = (char*)cache;
+        const int rc = embla_kv_quant_append(base + j.k, base + j.v, EMBLA_BF16, 4096, T, pm_pos, 2,
+                                             c + j.kc, c + j.vc, maxS, EMBLA_F32, 1, stream);
+        if (rc) return rc;
+    }
+    return EMBLA_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,122 @@
+// Shared device helpers for the gfx950 attention kernels: element types, exact int8 -> fp16
+// conversion, MFMA wrappers, wave reductions and the cache layouts every kernel agrees on.
+//
+// Cache layouts (one layer; head dim 128; the caller owns the memory). Both K and V are stored in
+// 32-key tiles "in MFMA lane order": tile (kv head h, keys 32i .. 32i+31) is 32*128*ES bytes at
+// ((h * max_s/32) + i) * 4096 * ES, and inside a tile the bytes are ordered so that load j of
+// lane l (16 bytes at (j*64 + l)*16) is exactly what lane l needs as its MFMA operand slice. Every
+// load instruction of a wave then reads 1 KB contiguous (a row-major or column-group layout makes
+// each 16-byte lane load hit its own cache line and caps a CU at ~20 GB/s).
+//   K tile: key k = 16t + m (t = 0, 1), dim d: lane l = m + 16*(d/32) holds dims 32*(d/32) .. +31
+//           of key k; byte p = (d % 32) * ES of its slice is load j = t*2ES + p/16, byte p % 16.
+//   V tile: key k = 16t + 4g + i, dim d = 8n + u: lane l = n + 16g, byte p = (8u + 4t + i) * ES
+//           of its 8*8*ES-byte slice is load j = p/16, byte p % 16.
+//   int8 regions: K (or V) tiles [n_kv][max_s/32], then scales [n_kv][max_s] (fp16 or fp32) at
+//   byte n_kv * max_s * 128, as the reference's KV8 layout places them (common.metal:53-63), so an
+//   engine's per-layer offsets and region sizes are unchanged.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace embla {
+
+constexpr int HD = 128;          // head dim
+constexpr float NEG_INF = -__builtin_huge_valf();
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 b8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef float f16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------------ scalar conversions
+__device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
+__device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+/// fp32 -> bf16 bits, round to nearest even (BFloat16.swift:4-9; NaN is not expected here).
+__device__ __forceinline__ uint16_t f2bf(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (uint16_t)((u + (((u >> 16) & 1u) + 0x7FFFu)) >> 16);
+}
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+/// A 16-bit activation (fp16 or bf16 bits) as float.
+template <bool BF> __device__ __forceinline__ float a2f(uint16_t b) { return BF ? bf2f(b) : h2f(b); }
+template <bool BF> __device__ __forceinline__ uint16_t f2a(float f) { return BF ? f2bf(f) : f2h(f); }
+
+// ------------------------------------------------------------------ int8 -> fp16, exact
+// Bytes are biased to unsigned (x ^ 0x80), placed under a 0x64 exponent byte (the fp16 value
+// 1024 + u), and 1152 is subtracted: every int8 is exact in fp16, so the result is exact.
+__device__ __forceinline__ void i8x4_to_h4(uint32_t x, uint32_t& lo, uint32_t& hi) {
+    const uint32_t u = x ^ 0x80808080u;
+    lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    const h2_t bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, lo) - bias);
+    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, hi) - bias);
+}
+/// 8 int8 (two dwords) -> 8 fp16 lanes of an MFMA operand.
+__device__ __forceinline__ h8_t i8x8_to_h8(uint32_t a, uint32_t b) {
+    uint32_t r0, r1, r2, r3;
+    i8x4_to_h4(a, r0, r1);
+    i8x4_to_h4(b, r2, r3);
+    return __builtin_bit_cast(h8_t, (u4_t){r0, r1, r2, r3});
+}
+/// 8 bf16 (four dwords) -> 8 fp16; exact for the magnitudes attention inputs take (|x| in
+/// [2^-14, 65504]); smaller values lose low bits as fp16 subnormals.
+__device__ __forceinline__ h8_t bf8_to_h8(u4_t w) {
+    h8_t r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        r[2 * i] = (_Float16)__uint_as_float(w[i] << 16);
+        r[2 * i + 1] = (_Float16)__uint_as_float(w[i] & 0xFFFF0000u);
+    }
+    return r;
+}
+
+// ------------------------------------------------------------------ MFMA (gfx950)
+// 16x16x32 f16: A lane = row + 16*(k/8), B lane = col + 16*(k/8), 8 halves a lane; D lane =
+// col + 16*(row/4), 4 floats a lane (item = row % 4). Only the pairing of A and B k-slots matters
+// for the kernels below: a lane's 8 A halves and the same lane group's 8 B halves are one k-range.
+__device__ __forceinline__ f4_t mfma16(h8_t a, h8_t b, f4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f4_t mfma16bf(b8_t a, b8_t b, f4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// ------------------------------------------------------------------ loads
+__device__ __forceinline__ u4_t ld16(const void* p) { return *reinterpret_cast<const u4_t*>(p); }
+__device__ __forceinline__ u2_t ld8(const void* p) { return *reinterpret_cast<const u2_t*>(p); }
+/// Streaming loads for data read once (KV caches): no reuse, keep them out of the way.
+__device__ __forceinline__ u4_t ld16_stream(const void* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(p));
+}
+
+// ------------------------------------------------------------------ wave helpers (wave64)
+__device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
+__device__ __forceinline__ float readlane(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+/// Byte offset of element (key j, dim d) of kv head h in a K tile region of element size ES.
+__host__ __device__ __forceinline__ size_t kt_off(int h, int max_s, int j, int d, int es) {
+    const int k = j & 31, t = k >> 4, m = k & 15, l = m + 16 * (d >> 5), p = (d & 31) * es;
+    const int jj = t * 2 * es + (p >> 4);
+    return (((size_t)h * (max_s >> 5) + (j >> 5)) * 4096 * es) + (size_t)(jj * 64 + l) * 16 + (p & 15);
+}
+/// Byte offset of element (key j, dim d) of kv head h in a V tile region of element size ES.
+__host__ __device__ __forceinline__ size_t vt_off(int h, int max_s, int j, int d, int es) {
+    const int k = j & 31, t = k >> 4, g = (k >> 2) & 3, i = k & 3, n = d >> 3, u = d & 7;
+    const int l = n + 16 * g, p = (8 * u + 4 * t + i) * es;
+    return (((size_t)h * (max_s >> 5) + (j >> 5)) * 4096 * es) + (size_t)((p >> 4) * 64 + l) * 16 + (p & 15);
+}
+/// Start of the 32-key tile holding key j.
+__host__ __device__ __forceinline__ size_t tile_base(int h, int max_s, int j, int es) {
+    return ((size_t)h * (max_s >> 5) + (j >> 5)) * 4096 * es;
+}
+
+}  // namespace embla

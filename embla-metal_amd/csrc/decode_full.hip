@@ -1,0 +1,390 @@
+// Split-K decode attention over an int8 KV cache (one query token), on gfx950 MFMA.
+//
+// Follows the reference's attn_full8 / attn_sparse8 (Sources/EmblaMetal/Kernels/attention.metal:
+// 235-363, 448-584): a workgroup takes one (chunk of keys, kv head) and writes a partial; the
+// partials are then merged (the reference's arrive_last step, common.metal:86-99, 209-220).
+// Weights: softmax (config C1/C3 and the reference's sparse layers) or ReLU² with sink
+// (`relu(q·k/√128)²`, `o = Σw·v / (√128 + Σw)`, attention.metal:143-145, 209-220).
+//
+// The MI355X design (not the reference's): a wave64 takes 32-key tiles. S^T = K·q^T runs on
+// v_mfma_i32_16x16x64_i8 straight on the cache's int8 K bytes: q is held as a 15-bit fixed point
+// per head (|error| <= absmax/64000) split exactly into two int8 halves, q = s·(256·hi + lo), which
+// sit in columns n and n + GQ of the B operand, so one MFMA gives both partial sums. A lane (head n,
+// lane group g) of the score tile then holds keys {16t + 4g + i}, which is exactly the A-operand
+// slice it needs for O += W·V (v_mfma_f32_16x16x32_f16, V bytes converted exactly to fp16), so the
+// weights never move between lanes. K and V tiles are stored in MFMA lane order (common.hpp), so
+// each of a wave's 8 loads a tile reads 1 KB contiguous. Scores and weights stay in fp32;
+// W = p·scale_v is rounded to fp16 (with a power-of-two prescale) only as the MFMA operand.
+// Chunk partials are merged by a second, wide kernel (a workgroup a (query head, 32 dims), one
+// memory round) instead of the reference's last-arriving threadgroup: on MI355X a cross-XCD
+// arrival protocol costs a chain of round trips through the coherence point (store completion,
+// counter RMW, then the loads) of ~5 us, against ~2 us for a dependent launch; the split also
+// needs no counters, so the path is graph-capturable and leaves no state behind.
+#include "common.hpp"
+#include "embla_internal.hpp"
+
+namespace embla {
+
+typedef int i4_t __attribute__((ext_vector_type(4)));
+
+constexpr float WSCALE = 64.0f;   // prescale of W into fp16's normal range; divided out at the end
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float QFIX = 32000.0f;  // q's fixed-point range: |q_int| <= 32000, so |hi| <= 125
+constexpr int PS = HD + 4;        // floats a (chunk, query head) partial: acc[128], m, l, pad
+
+/// One 32-key tile's raw bytes for a lane.
+struct Tile8 {
+    u4_t k[4];    // K: [2t + h] = half t, dims 32g + 16h .. + 15 of key 16t + n
+    u4_t v[4];    // V: [u / 2], dwords (u % 2) * 2 .. = dim 8n + u for keys {16t + 4g + i}
+    u4_t ks[2];   // scales of keys 16t + 4g .. + 3: fp16 in .xy of [t]; fp32 in [t]
+    u4_t vs[2];
+};
+
+/// The 8 scales of a lane's keys, item e = 4t + i <-> key 16t + 4g + i.
+template <bool SCALE32>
+__device__ __forceinline__ void scales8(const u4_t* r, float* out) {
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        if constexpr (SCALE32) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) out[4 * t + i] = __uint_as_float(r[t][i]);
+        } else {
+            out[4 * t + 0] = h2f((uint16_t)(r[t][0] & 0xFFFF));
+            out[4 * t + 1] = h2f((uint16_t)(r[t][0] >> 16));
+            out[4 * t + 2] = h2f((uint16_t)(r[t][1] & 0xFFFF));
+            out[4 * t + 3] = h2f((uint16_t)(r[t][1] >> 16));
+        }
+    }
+}
+
+template <int GQ, bool RELU2, bool SCALE32, bool OBF, bool SCORES>
+__global__ __launch_bounds__(256, 2) void full_decode_kernel(
+    const uint16_t* __restrict__ q,   // [n_kv * GQ][128] fp16, prepared
+    const int8_t* __restrict__ kc, const int8_t* __restrict__ vc,
+    float* __restrict__ part, float* __restrict__ scores, uint16_t* __restrict__ o, int S, int CH,
+    int C, int max_s, int n_kv, float qk_scale, float sink) {
+    static_assert(GQ == 4 || GQ == 8, "4 or 8 query heads a kv head");
+    const int c = blockIdx.x, kvh = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int n = lane & 15, g = lane >> 4;
+
+    const size_t rows = (size_t)n_kv * max_s * HD;
+    const char* ksb = (const char*)(kc + rows);
+    const char* vsb = (const char*)(vc + rows);
+    constexpr int ES = SCALE32 ? 4 : 2;
+    const int j0 = c * CH, j1 = min(S, j0 + CH);
+    const float sc = RELU2 ? qk_scale : qk_scale * LOG2E;
+
+    float m = NEG_INF, l = 0.0f;
+    f4_t O[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) O[u] = (f4_t){0, 0, 0, 0};
+
+    i4_t qb[2];
+    float qsc = 0.0f;   // the fixed point's step, per head
+    // q as a 15-bit fixed point split into int8 halves: column n < GQ holds hi of head n, column
+    // GQ + n holds lo; lane (n, g), MFMA b: dims 32g + 16b .. + 15 (the K slice's dims).
+    auto setup_q = [&]() {
+        const int hn = n % GQ;
+        const bool live = n < 2 * GQ, is_lo = n >= GQ;
+        const uint16_t* qr = q + ((size_t)kvh * GQ + hn) * HD + 32 * g;
+        float qf[32];
+        float am = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const u4_t r = ld16(qr + 8 * u);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                qf[8 * u + 2 * i] = h2f((uint16_t)(r[i] & 0xFFFF));
+                qf[8 * u + 2 * i + 1] = h2f((uint16_t)(r[i] >> 16));
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < 32; d++) am = fmaxf(am, fabsf(qf[d]));
+        am = fmaxf(am, shfl_xor(am, 16));
+        am = fmaxf(am, shfl_xor(am, 32));
+        const float inv = am > 0.0f ? QFIX / am : 0.0f;
+        qsc = am / QFIX;
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                uint32_t word = 0;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int qi = (int)rintf(qf[16 * b + 4 * k + e] * inv);
+                    const int hi = (qi + 128) >> 8, lo = qi - hi * 256;
+                    const int byte = live ? (is_lo ? lo : hi) : 0;
+                    word |= (uint32_t)(byte & 0xFF) << (8 * e);
+                }
+                qb[b][k] = (int)word;
+            }
+        }
+    };
+
+    auto load_tile = [&](int t0, Tile8& T) {
+        const int8_t* pk = kc + tile_base(kvh, max_s, t0, 1) + lane * 16;
+        const int8_t* pv = vc + tile_base(kvh, max_s, t0, 1) + lane * 16;
+#pragma unroll
+        for (int j = 0; j < 4; j++) { T.k[j] = ld16(pk + 1024 * j); T.v[j] = ld16(pv + 1024 * j); }
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const size_t si = ((size_t)kvh * max_s + t0 + 16 * t + 4 * g) * ES;
+            if constexpr (SCALE32) { T.ks[t] = ld16(ksb + si); T.vs[t] = ld16(vsb + si); }
+            else {
+                const u2_t a = ld8(ksb + si), b = ld8(vsb + si);
+                T.ks[t] = (u4_t){a[0], a[1], 0, 0};
+                T.vs[t] = (u4_t){b[0], b[1], 0, 0};
+            }
+        }
+    };
+
+    auto compute_tile = [&](int t0, const Tile8& T) {
+        const bool full = t0 + 32 <= j1;
+        float ks[8], vs[8];
+        scales8<SCALE32>(T.ks, ks);
+        scales8<SCALE32>(T.vs, vs);
+        // S^T (int32) of the two 16-key halves: lane (n, g) item i of half t = key t0 + 16t + 4g + i
+        float x[8];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            i4_t st = {0, 0, 0, 0};
+            st = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i4_t, T.k[2 * t]), qb[0], st, 0, 0, 0);
+            st = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i4_t, T.k[2 * t + 1]), qb[1], st, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int lo = __shfl_xor(st[i], GQ, 64);
+                x[4 * t + i] = (float)(st[i] * 256 + lo) * qsc * ks[4 * t + i];
+            }
+        }
+        bool valid[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) valid[e] = full || t0 + 16 * (e >> 2) + 4 * g + (e & 3) < j1;
+        if constexpr (SCORES) {
+            // max over the kv head's query heads of the dequantised q·k (attention.metal:295-305)
+            float smx[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                float v = n < GQ ? x[e] : NEG_INF;
+                v = fmaxf(v, shfl_xor(v, 1));
+                v = fmaxf(v, shfl_xor(v, 2));
+                v = fmaxf(v, shfl_xor(v, 4));
+                smx[e] = v;
+            }
+            if (n == 0) {
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    if (valid[e]) scores[(size_t)kvh * max_s + t0 + 16 * (e >> 2) + 4 * g + (e & 3)] = smx[e];
+            }
+        }
+        h8_t wa;
+        if constexpr (RELU2) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float a = fmaxf(x[e] * sc, 0.0f);
+                const float wt = valid[e] ? a * a : 0.0f;
+                l += wt;
+                wa[e] = (_Float16)(wt * vs[e] * WSCALE);
+            }
+        } else {
+            float mt = NEG_INF;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                x[e] = valid[e] ? x[e] * sc : NEG_INF;
+                mt = fmaxf(mt, x[e]);
+            }
+            mt = fmaxf(mt, shfl_xor(mt, 16));
+            mt = fmaxf(mt, shfl_xor(mt, 32));
+            const float mn = fmaxf(m, mt);
+            // rescale only when some head's maximum grew (rare once the maxima settle); nothing to
+            // rescale while m is still -inf
+            if (__any(n < GQ && mn > m)) {
+                if (__any(n < GQ && m != NEG_INF)) {
+                    const float corr = m == NEG_INF ? 0.0f : exp2f(m - mn);
+                    l *= corr;
+                    float cf[4];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const float c0 = readlane(corr, i);
+                        if constexpr (GQ == 8) {
+                            const float c1 = readlane(corr, 4 + i);
+                            cf[i] = g == 1 ? c1 : c0;
+                        } else {
+                            cf[i] = c0;
+                        }
+                    }
+#pragma unroll
+                    for (int u = 0; u < 8; u++)
+#pragma unroll
+                        for (int i = 0; i < 4; i++) O[u][i] *= cf[i];
+                }
+                m = mn;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float p = exp2f(x[e] - m);   // x = -inf -> 0; m finite once a key is valid
+                l += p;
+                wa[e] = (_Float16)(p * vs[e] * WSCALE);
+            }
+        }
+        // O += W V: MFMA u covers dims 8n + u (column n), rows = heads 4g + i
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const u4_t r = T.v[u >> 1];
+            const h8_t b = (u & 1) ? i8x8_to_h8(r[2], r[3]) : i8x8_to_h8(r[0], r[1]);
+            O[u] = mfma16(wa, b, O[u]);
+        }
+    };
+
+    // two tiles in flight a wave: tile i+2's loads go out before tile i+1 is computed
+    {
+        constexpr int step = 32 * 4;
+        const int t0 = j0 + 32 * w;
+        Tile8 A, B;
+        if (t0 < j1) load_tile(t0, A);
+        if (t0 + step < j1) load_tile(t0 + step, B);
+        setup_q();   // after the first loads are out: the q math overlaps their latency
+        for (int t = t0; t < j1; t += 2 * step) {
+            compute_tile(t, A);
+            if (t + 2 * step < j1) load_tile(t + 2 * step, A);
+            if (t + step < j1) {
+                compute_tile(t + step, B);
+                if (t + 3 * step < j1) load_tile(t + 3 * step, B);
+            }
+        }
+    }
+
+    // ---- merge the 4 waves (LDS)
+    __shared__ float om[4][GQ][HD];
+    __shared__ float mm[4][GQ], ll[4][GQ];
+    l += shfl_xor(l, 16);
+    l += shfl_xor(l, 32);
+    if (g == 0 && n < GQ) { mm[w][n] = m; ll[w][n] = l; }
+#pragma unroll
+    for (int u = 0; u < 8; u++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (4 * g + i < GQ) om[w][4 * g + i][8 * n + u] = O[u][i];
+    __syncthreads();
+
+    constexpr int PER = GQ * HD / 256;   // outputs a thread: 2 or 4 (one head, consecutive dims)
+    const int oh = tid * PER / HD, od = tid * PER % HD;
+    float acc[PER], M, L;
+    if constexpr (RELU2) {
+        M = 0.0f;
+        L = ll[0][oh] + ll[1][oh] + ll[2][oh] + ll[3][oh];
+#pragma unroll
+        for (int e = 0; e < PER; e++) acc[e] = om[0][oh][od + e] + om[1][oh][od + e] + om[2][oh][od + e] + om[3][oh][od + e];
+    } else {
+        M = fmaxf(fmaxf(mm[0][oh], mm[1][oh]), fmaxf(mm[2][oh], mm[3][oh]));
+        float f[4];
+        L = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < 4; ww++) {
+            f[ww] = mm[ww][oh] == NEG_INF ? 0.0f : exp2f(mm[ww][oh] - M);
+            L += ll[ww][oh] * f[ww];
+        }
+#pragma unroll
+        for (int e = 0; e < PER; e++) {
+            float a = 0.0f;
+#pragma unroll
+            for (int ww = 0; ww < 4; ww++) a += om[ww][oh][od + e] * f[ww];
+            acc[e] = a;
+        }
+    }
+    const int hq = kvh * GQ + oh;
+    if (C == 1) {
+        const float rr = RELU2 ? 1.0f / (WSCALE * (sink + L)) : 1.0f / (WSCALE * L);
+#pragma unroll
+        for (int e = 0; e < PER; e++) o[(size_t)hq * HD + od + e] = f2a<OBF>(acc[e] * rr);
+        return;
+    }
+    float* pp = part + ((size_t)c * n_kv * GQ + hq) * PS;
+#pragma unroll
+    for (int e = 0; e < PER; e++) pp[od + e] = acc[e];
+    if (od == 0) { pp[HD] = M; pp[HD + 1] = L; }
+}
+
+/// Merges the C chunk partials of query head blockIdx.x, dims 32 * blockIdx.y .. + 31: thread
+/// (slice s of 4 dims, chunk group r) loads its chunks' slices, maxima and sums in one round.
+template <bool RELU2, bool OBF>
+__global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ part, uint16_t* __restrict__ o,
+                                                           int C, int n_q, float sink) {
+    constexpr int NR = 32, MAXK = 8;   // chunk groups; chunks a thread (C <= 256)
+    const int h = blockIdx.x, d0 = 32 * blockIdx.y;
+    const int tid = threadIdx.x, sl = tid & 7, r = tid >> 3;
+    const int d = d0 + 4 * sl;
+    u4_t v[MAXK];
+    float mk[MAXK], lk[MAXK];
+#pragma unroll
+    for (int k = 0; k < MAXK; k++) {
+        const int cc = r + NR * k;
+        if (cc < C) {
+            const float* p = part + ((size_t)cc * n_q + h) * PS;
+            v[k] = ld16(p + d);
+            mk[k] = p[HD];
+            lk[k] = p[HD + 1];
+        }
+    }
+    __shared__ float sm[NR], sl_[NR];
+    __shared__ f4_t sa[NR][8];
+    float M = RELU2 ? 0.0f : NEG_INF;
+    if constexpr (!RELU2) {
+#pragma unroll
+        for (int k = 0; k < MAXK; k++)
+            if (r + NR * k < C) M = fmaxf(M, mk[k]);
+        if (sl == 0) sm[r] = M;
+        __syncthreads();
+        M = NEG_INF;
+        for (int i = 0; i < NR; i++) M = fmaxf(M, sm[i]);
+    }
+    f4_t A = {0, 0, 0, 0};
+    float Lr = 0.0f;
+#pragma unroll
+    for (int k = 0; k < MAXK; k++) {
+        if (r + NR * k < C) {
+            const float f = RELU2 ? 1.0f : (mk[k] == NEG_INF ? 0.0f : exp2f(mk[k] - M));
+            Lr += lk[k] * f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) A[i] += __uint_as_float(v[k][i]) * f;
+        }
+    }
+    sa[r][sl] = A;
+    if (sl == 0) sl_[r] = Lr;
+    __syncthreads();
+    if (tid >= 8) return;
+    f4_t T = {0, 0, 0, 0};
+    float L = 0.0f;
+    for (int i = 0; i < NR; i++) { T += sa[i][sl]; L += sl_[i]; }
+    const float inv = 1.0f / (RELU2 ? WSCALE * (sink + L) : WSCALE * L);
+#pragma unroll
+    for (int i = 0; i < 4; i++) o[(size_t)h * HD + d + i] = f2a<OBF>(T[i] * inv);
+}
+
+// ------------------------------------------------------------------ host launch
+int launch_full_decode(const FullDecodeArgs& a, hipStream_t st) {
+    const dim3 grid(a.C, a.n_kv), block(256);
+    const float qs = 0.08838834764831845f;   // 1/sqrt(128)
+    const float sink = 11.313708498984761f;   // sqrt(128)
+#define EMBLA_FD(GQ, R, S32, OBF, SC)                                                              \
+    hipLaunchKernelGGL((full_decode_kernel<GQ, R, S32, OBF, SC>), grid, block, 0, st, a.q, a.kc, a.vc, \
+                       a.part, a.scores, a.o, a.S, a.CH, a.C, a.max_s, a.n_kv, qs, sink)
+    const int gq = a.n_q / a.n_kv;
+    if (gq == 4 && !a.relu2 && !a.scale32 && !a.out_bf16 && !a.scores) EMBLA_FD(4, false, false, false, false);
+    else if (gq == 4 && !a.relu2 && a.scale32 && a.out_bf16 && !a.scores) EMBLA_FD(4, false, true, true, false);
+    else if (gq == 8 && a.relu2 && a.scale32 && a.out_bf16 && !a.scores) EMBLA_FD(8, true, true, true, false);
+    else if (gq == 8 && a.relu2 && a.scale32 && a.out_bf16 && a.scores) EMBLA_FD(8, true, true, true, true);
+    else if (gq == 8 && !a.relu2 && a.scale32 && a.out_bf16 && !a.scores) EMBLA_FD(8, false, true, true, false);
+    else if (gq == 8 && !a.relu2 && !a.scale32 && !a.out_bf16 && !a.scores) EMBLA_FD(8, false, false, false, false);
+    else return EMBLA_ERR_UNSUPPORTED;
+#undef EMBLA_FD
+    if (a.C > 1) {
+        const dim3 mg(a.n_q, HD / 32);
+        if (a.relu2 && a.out_bf16) hipLaunchKernelGGL((decode_merge_kernel<true, true>), mg, block, 0, st, a.part, a.o, a.C, a.n_q, sink);
+        else if (!a.relu2 && a.out_bf16) hipLaunchKernelGGL((decode_merge_kernel<false, true>), mg, block, 0, st, a.part, a.o, a.C, a.n_q, sink);
+        else hipLaunchKernelGGL((decode_merge_kernel<false, false>), mg, block, 0, st, a.part, a.o, a.C, a.n_q, sink);
+    }
+    return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
+}
+
+}  // namespace embla

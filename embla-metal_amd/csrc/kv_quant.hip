@@ -1,0 +1,108 @@
+// int8 quantise-and-append of K/V rows, and the reference's query preparation (RMS head norm
+// with gains), one wave64 a (token, kv head, K or V) / a (token, head).
+//
+// Quantisation follows write_row8 (Sources/EmblaMetal/Kernels/common.metal:72-84) with kv_append /
+// kv_append_b as callers (attention.metal:113-140, prefill.metal:182-212):
+//   v_i = x_i (bf16-rounded when the input is bf16: the reference's bf()),
+//   a = max |v_i|, q_i = rint(v_i * (127 / a)) (0 when a = 0), scale = a / 127
+// stored as fp32 (reference) or fp16 (config). With norm_k the K row is first RMS-normed without
+// gains (head_norm with ng = 0, common.metal:13-26): r = 1 / sqrt(Σx² / 128 + 2^-23).
+// Bit-exactness: the squares are summed in a fixed butterfly (lane pairs xor 32, 16, .., 1 over
+// per-lane sums of two squares) that the oracle restates; no fma contraction anywhere here.
+#include "common.hpp"
+#include "embla_internal.hpp"
+
+#pragma clang fp contract(off)
+
+namespace embla {
+
+constexpr float EPS32 = 1.1920929e-07f;
+
+__device__ __forceinline__ float wave_sum_bfly(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = v + shfl_xor(v, m);
+    return v;
+}
+__device__ __forceinline__ float wave_max_bfly(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor(v, m));
+    return v;
+}
+
+/// RMS factor of a head held two dims a lane, in the fixed order the oracle restates.
+__device__ __forceinline__ float rms_factor(float x0, float x1) {
+    const float s0 = x0 * x0, s1 = x1 * x1;
+    const float ss = wave_sum_bfly(s0 + s1);
+    return 1.0f / sqrtf(ss / 128.0f + EPS32);
+}
+
+/// One wave a (token, kv head, K or V): two dims a lane, quantised, then stored at their places
+/// in the MFMA lane-order tiles (common.hpp); K's two bytes are adjacent, V's are not.
+__global__ __launch_bounds__(64) void kv_quant_kernel(KVQuantArgs a) {
+    const int lane = threadIdx.x;
+    const int t = blockIdx.x, h = blockIdx.y;
+    const bool is_v = blockIdx.z == 1;
+    const int pos = a.p0 + t;
+    const uint16_t* src = is_v ? a.v : a.k;
+    int8_t* rows = is_v ? a.vc : a.kc;
+    const size_t nrow = (size_t)a.n_kv * a.max_s * HD;
+
+    const uint32_t raw = *(const uint32_t*)(src + (size_t)t * a.stride + h * HD + 2 * lane);
+    float x0 = a.in_bf16 ? bf2f(raw & 0xFFFF) : h2f(raw & 0xFFFF);
+    float x1 = a.in_bf16 ? bf2f(raw >> 16) : h2f(raw >> 16);
+    if (!is_v && a.norm_k) {
+        const float r = rms_factor(x0, x1);
+        x0 = x0 * r;
+        x1 = x1 * r;
+    }
+    if (a.in_bf16) { x0 = bf2f(f2bf(x0)); x1 = bf2f(f2bf(x1)); }
+    const float am = wave_max_bfly(fmaxf(fabsf(x0), fabsf(x1)));
+    const float inv = am > 0.0f ? 127.0f / am : 0.0f;
+    const int q0 = (int)rintf(x0 * inv), q1 = (int)rintf(x1 * inv);
+    if (lane == 0) {
+        const size_t si = (size_t)h * a.max_s + pos;
+        if (a.scale32) ((float*)(rows + nrow))[si] = am / 127.0f;
+        else ((uint16_t*)(rows + nrow))[si] = f2h(am / 127.0f);
+    }
+    if (!is_v) {
+        *(uint16_t*)(rows + kt_off(h, a.max_s, pos, 2 * lane, 1)) = (uint16_t)((q0 & 0xFF) | ((q1 & 0xFF) << 8));
+    } else {
+        rows[vt_off(h, a.max_s, pos, 2 * lane, 1)] = (int8_t)q0;
+        rows[vt_off(h, a.max_s, pos, 2 * lane + 1, 1)] = (int8_t)q1;
+    }
+}
+
+int launch_kv_quant(const KVQuantArgs& a, hipStream_t st) {
+    hipLaunchKernelGGL(kv_quant_kernel, dim3(a.T, a.n_kv, 2), dim3(64), 0, st, a);
+    return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
+}
+
+/// Query rows normed with the gains (head_norm, common.metal:13-26), bf16-rounded as the
+/// reference does before its attention (attention.metal:168-169; prefill.metal:406-426).
+__global__ __launch_bounds__(64) void q_prep_kernel(QPrepArgs a) {
+    const int lane = threadIdx.x, h = blockIdx.x, t = blockIdx.y;
+    const uint32_t raw = *(const uint32_t*)(a.qraw + (size_t)t * a.stride + h * HD + 2 * lane);
+    float x0 = bf2f(raw & 0xFFFF), x1 = bf2f(raw >> 16);
+    const float r = rms_factor(x0, x1);
+    float g0 = r, g1 = r;
+    if (a.ng >= 1) {
+        g0 = g0 * (1.0f + bf2f(a.g1[2 * lane]));
+        g1 = g1 * (1.0f + bf2f(a.g1[2 * lane + 1]));
+    }
+    if (a.ng >= 2) {
+        g0 = g0 * (1.0f + bf2f(a.g2[2 * lane]));
+        g1 = g1 * (1.0f + bf2f(a.g2[2 * lane + 1]));
+    }
+    x0 = bf2f(f2bf(x0 * g0));
+    x1 = bf2f(f2bf(x1 * g1));
+    uint16_t* out = a.out + ((size_t)t * a.n_q + h) * HD + 2 * lane;
+    out[0] = a.out_bf16 ? f2bf(x0) : f2h(x0);
+    out[1] = a.out_bf16 ? f2bf(x1) : f2h(x1);
+}
+
+int launch_q_prep(const QPrepArgs& a, hipStream_t st) {
+    hipLaunchKernelGGL(q_prep_kernel, dim3(a.n_q, a.T), dim3(64), 0, st, a);
+    return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
+}
+
+}  // namespace embla

@@ -1,0 +1,72 @@
+"""Torch-facing wrappers over the C ABI: device tensors in, device tensors out, launched on the
+current torch stream. Torch supplies device memory and the stream; every computation is the HIP
+library's.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from . import _lib
+from ._lib import BF16, F16, F32, RELU2_SINK, SOFTMAX, call, lib
+
+_DT = {F16: torch.float16, BF16: torch.bfloat16}
+
+
+def _p(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def stream_handle(stream=None) -> C.c_void_p:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return C.c_void_p(s.cuda_stream)
+
+
+class Workspace:
+    """Split-K partials and counters for decode calls up to max_s keys and n_q heads."""
+
+    def __init__(self, max_s: int, n_q: int = 16, device="cuda"):
+        self.nbytes = int(lib().embla_workspace_bytes(max_s, n_q))
+        if self.nbytes == 0:
+            raise ValueError("invalid workspace shape")
+        self.buf = torch.empty(self.nbytes, dtype=torch.uint8, device=device)
+        call("embla_workspace_init", _p(self.buf), self.nbytes, stream_handle())
+
+    @property
+    def ptr(self):
+        return _p(self.buf)
+
+
+def decode_int8(q, kc, vc, S, max_s, n_kv, weights=SOFTMAX, scale_dtype=F16, out_dtype=F16,
+                chunk=0, ws: Workspace | None = None, scores=None, out=None, stream=None):
+    """Split-K decode of fp16 q [n_q][128] over an int8 layer cache (K region kc, V region vc)."""
+    n_q = q.shape[0]
+    if out is None:
+        out = torch.empty((n_q, 128), dtype=_DT[out_dtype], device=q.device)
+    call("embla_decode_int8", _p(q), _p(kc), _p(vc), _p(out), _p(scores), S, max_s, n_q, n_kv,
+         weights, scale_dtype, out_dtype, chunk, ws.ptr if ws else None, ws.nbytes if ws else 0,
+         stream_handle(stream))
+    return out
+
+
+def kv_quant_append(k, v, T, p0, n_kv, kc, vc, max_s, in_dtype=BF16, scale_dtype=F16, norm_k=False,
+                    stride=None, stream=None):
+    stride = stride if stride is not None else n_kv * 128
+    call("embla_kv_quant_append", _p(k), _p(v), in_dtype, stride, T, p0, n_kv, _p(kc), _p(vc), max_s,
+         scale_dtype, int(norm_k), stream_handle(stream))
+
+
+def q_prep(qraw, g1, g2, ng, T, n_q, out_dtype=F16, stride=None, stream=None):
+    stride = stride if stride is not None else n_q * 128
+    out = torch.empty((T, n_q, 128), dtype=_DT[out_dtype], device=qraw.device)
+    call("embla_q_prep", _p(qraw), _p(g1), _p(g2), ng, stride, T, n_q, _p(out), out_dtype,
+         stream_handle(stream))
+    return out
+
+
+def attn_full8(qraw, g1, g2, kc, vc, part, scores, counter, o, S, maxS, ng=2, CH=0, stream=None):
+    """Reference-signature full layer (attention.metal:235-363)."""
+    p = _lib.AttnParams(S, CH, 0, maxS, S - 1, ng, 0, 0)
+    call("embla_attn_full8", _p(qraw), _p(g1), _p(g2), _p(kc), _p(vc), _p(part), _p(scores),
+         _p(counter), _p(o), C.byref(p), stream_handle(stream))

@@ -1,0 +1,73 @@
+"""Seeded synthetic inputs of the benchmark configurations (SplitMix64, as the reference's tests
+seed their fixtures: Tests/EmblaMetalTests/GEMV4Tests.swift:35-46).
+
+Draws, in a fixed order per configuration:
+  uniform  u = (z >> 11) * 2^-53
+  normal   Box-Muller on consecutive uniform pairs (u1, u2): sqrt(-2 ln(1 - u1)) cos(2π u2), in
+           fp64, then rounded (RNE) to fp16 or bf16
+  int8     (z mod 255) - 127, in [-127, 127]
+"""
+from __future__ import annotations
+
+import numpy as np
+
+GOLD = np.uint64(0x9E3779B97F4A7C15)
+M1 = np.uint64(0xBF58476D1CE4E5B9)
+M2 = np.uint64(0x94D049BB133111EB)
+
+
+class SplitMix64:
+    def __init__(self, seed: int):
+        self.state = np.uint64(seed & 0xFFFFFFFFFFFFFFFF)
+
+    def next(self, n: int) -> np.ndarray:
+        with np.errstate(over="ignore"):
+            z = self.state + np.arange(1, n + 1, dtype=np.uint64) * GOLD
+            self.state = self.state + np.uint64(n) * GOLD
+            z = (z ^ (z >> np.uint64(30))) * M1
+            z = (z ^ (z >> np.uint64(27))) * M2
+            return z ^ (z >> np.uint64(31))
+
+    def uniform(self, n: int) -> np.ndarray:
+        return (self.next(n) >> np.uint64(11)).astype(np.float64) * (2.0 ** -53)
+
+    def normal(self, n: int) -> np.ndarray:
+        u = self.uniform(2 * n)
+        u1, u2 = u[0::2], u[1::2]
+        return np.sqrt(-2.0 * np.log1p(-u1)) * np.cos(2.0 * np.pi * u2)
+
+    def int8(self, n: int) -> np.ndarray:
+        return ((self.next(n) % np.uint64(255)).astype(np.int16) - 127).astype(np.int8)
+
+
+def f16_bits(x: np.ndarray) -> np.ndarray:
+    """fp64/fp32 -> fp16 bits (RNE, via numpy's IEEE conversion)."""
+    return np.asarray(x, dtype=np.float64).astype(np.float16).view(np.uint16)
+
+
+def f16_val(bits: np.ndarray) -> np.ndarray:
+    return np.asarray(bits, dtype=np.uint16).view(np.float16).astype(np.float32)
+
+
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    """-> bf16 bits, RNE from the fp32 value (BFloat16.swift:4-9)."""
+    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = (u + ((u >> np.uint64(16)) & np.uint64(1)) + np.uint64(0x7FFF)) >> np.uint64(16)
+    return r.astype(np.uint16)
+
+
+def bf16_val(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+def decode_int8_case(seed: int, S: int, n_q: int = 16, n_kv: int = 4, lo: float = 0.005,
+                     hi: float = 0.02) -> dict:
+    """Configs 1 and 3: q fp16 N(0,1); K, V int8 U{-127..127}; fp16 scales U[lo, hi].
+    Draw order: q, K, K scales, V, V scales."""
+    g = SplitMix64(seed)
+    q = f16_bits(g.normal(n_q * 128)).reshape(n_q, 128)
+    K = g.int8(n_kv * S * 128).reshape(n_kv, S, 128)
+    ks = f16_bits(lo + (hi - lo) * g.uniform(n_kv * S)).reshape(n_kv, S)
+    V = g.int8(n_kv * S * 128).reshape(n_kv, S, 128)
+    vs = f16_bits(lo + (hi - lo) * g.uniform(n_kv * S)).reshape(n_kv, S)
+    return dict(q=q, K=K, ks=ks, V=V, vs=vs, S=S, n_q=n_q, n_kv=n_kv)

@@ -1,0 +1,119 @@
+/* embla_attn.h — C ABI of the MI355X (gfx950) attention hot path.
+ *
+ * Every entry point takes device pointers the caller owns, a hipStream_t, and returns 0 or a
+ * negative EMBLA_ERR_* code. Arguments are validated on the host before any launch; nothing
+ * throws or aborts across this boundary, nothing allocates, nothing synchronises the host.
+ * Calls are stream-ordered and asynchronous. A workspace (split-K partials) is thread-compatible,
+ * not thread-safe: one in-flight call per workspace. Calls keep no state in it between calls, so
+ * they can be captured in a HIP graph.
+ *
+ * Head dim is 128. Cache layouts (one layer): an int8 K (or V) region is the 32-key tiles of
+ * every kv head, [n_kv][max_s/32][4096] bytes, then the scales [n_kv][max_s] (fp16 or fp32).
+ * Inside a tile the bytes are in MFMA lane order, so a wave reads each tile as contiguous 1 KB
+ * runs (element (key k, dim d) of a tile; ES = element size):
+ *   K: k = 16t + m: byte ((t*2ES + p/16) * 64 + m + 16*(d/32)) * 16 + p%16, p = (d%32)*ES
+ *   V: k = 16t + 4g + i, d = 8n + u: byte ((p/16) * 64 + n + 16g) * 16 + p%16, p = (8u+4t+i)*ES
+ * A region has the byte size and scale offset of the reference's KV8 layout
+ * (Sources/EmblaMetal/Kernels/common.metal:53-63; Engine.swift:277-281), so an engine's per-layer
+ * offsets hold. max_s must be a multiple of 32. 16-bit rings use the same tiles with ES = 2.
+ */
+#ifndef EMBLA_ATTN_H
+#define EMBLA_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* hipStream_t;
+
+#define EMBLA_OK 0
+#define EMBLA_ERR_INVALID (-1)     /* an argument out of range (checked on the host) */
+#define EMBLA_ERR_UNSUPPORTED (-2) /* a combination no kernel is built for */
+#define EMBLA_ERR_HIP (-3)         /* the HIP runtime reported an error at launch */
+#define EMBLA_ERR_WORKSPACE (-4)   /* workspace missing or too small */
+
+/* element types */
+#define EMBLA_F16 0
+#define EMBLA_BF16 1
+#define EMBLA_F32 2
+
+/* attention weights */
+#define EMBLA_SOFTMAX 0    /* softmax(q·k / sqrt(128)) */
+#define EMBLA_RELU2_SINK 1 /* w = relu(q·k / sqrt(128))^2, o = Σ w v / (sqrt(128) + Σ w) */
+
+/* Mirrors AttnParams (Sources/EmblaMetal/Kernels/attention.metal:8-16; Engine.swift:37-39)
+ * field for field. CH = 0 lets the library choose the chunking. */
+typedef struct EmblaAttnParams {
+    int32_t S, CH, C, maxS, pos, ng, pad0, pad1;
+} EmblaAttnParams;
+
+/* Mirrors KVJob (attention.metal:108-111; Engine.swift:35): element offsets of k and v in qkv
+ * and byte offsets of the layer's K and V regions in the cache. */
+typedef struct EmblaKVJob {
+    uint32_t k, v, kc, vc;
+} EmblaKVJob;
+
+/* Library version, for a host to check it loaded what it was built against. */
+int embla_version(void);
+
+/* Bytes of workspace for decode calls with up to max_s keys and n_q query heads. */
+size_t embla_workspace_bytes(int max_s, int n_q);
+/* Zeroes a workspace's reserved header (optional; kept for engines that initialise buffers). */
+int embla_workspace_init(void* ws, size_t ws_bytes, hipStream_t stream);
+
+/* ---------------------------------------------------------------- decode, int8 cache
+ * One query token attends keys 0 .. S-1 of an int8 layer cache, split over chunks of keys whose
+ * partials a second kernel merges (one launch when a single chunk covers S). Replaces the dispatches of attn_full8 and
+ * attn_sparse8 without selection (attention.metal:235-363, 448-584) made by
+ * Engine.encodeAttention (Engine.swift:795-818).
+ *   q       fp16 [n_q][128], prepared (normed/gained where the model does that)
+ *   o       [n_q][128] in out_dtype (EMBLA_F16 or EMBLA_BF16)
+ *   scores  optional [n_kv][max_s] fp32: max over a kv head's query heads of q·k·scale_k
+ *           (the reference's SCORES output, attention.metal:295-305); only with RELU2_SINK
+ *   weights EMBLA_SOFTMAX or EMBLA_RELU2_SINK; scale_dtype EMBLA_F16 or EMBLA_F32
+ *   chunk   keys a workgroup (multiple of 32), 0 = library's choice */
+int embla_decode_int8(const void* q, const void* kc, const void* vc, void* o, float* scores,
+                      int S, int max_s, int n_q, int n_kv, int weights, int scale_dtype,
+                      int out_dtype, int chunk, void* ws, size_t ws_bytes, hipStream_t stream);
+
+/* Reference-signature full layer (attn_full8, attention.metal:235-363; bound at Engine.swift:
+ * 800-818): raw bf16 q [16][128] normed with p->ng gains g1, g2 (common.metal:13-26) and rounded
+ * to bf16, ReLU² with sink over the int8 cache of 2 kv heads with fp32 scales; o bf16 [16][128].
+ * scores may be NULL (the SCORES=0 pipeline). part: a workspace of embla_workspace_bytes(maxS, 16)
+ * bytes; `counter` (the reference's split-K counters) is accepted and not used: the chunk
+ * partials are merged by a second kernel. */
+int embla_attn_full8(const void* qraw, const void* g1, const void* g2, const void* kc,
+                     const void* vc, float* part, float* scores, uint32_t* counter, void* o,
+                     const EmblaAttnParams* p, hipStream_t stream);
+
+/* ---------------------------------------------------------------- quantise-and-append
+ * T new positions p0 .. p0+T-1 of K and V rows into an int8 layer cache (write_row8,
+ * common.metal:72-84; kv_append / kv_append_b, attention.metal:113-140, prefill.metal:182-212):
+ * a = max|x|, q = rint(x * 127 / a), scale = a / 127 stored in scale_dtype. k and v point at row 0
+ * head 0; row t head h is at (t * stride + h * 128) elements; in_dtype EMBLA_BF16 or EMBLA_F16
+ * (bf16 inputs are rounded to bf16 after the norm, as the reference's bf()). norm_k: RMS-norm K
+ * rows first (no gains, eps 2^-23), as the reference's full layers. */
+int embla_kv_quant_append(const void* k, const void* v, int in_dtype, int stride, int T, int p0,
+                          int n_kv, void* kc, void* vc, int max_s, int scale_dtype, int norm_k,
+                          hipStream_t stream);
+
+/* Reference-signature kv_append (attention.metal:113-140 / prefill.metal:182-212, bound at
+ * Engine.swift:782-793, Prefill.swift:315-322): T tokens of qkv rows (4096 bf16 each, position
+ * pm_pos + t), njobs jobs of 2 kv heads, int8 cache with fp32 scales at byte offsets
+ * jobs[i].kc / .vc of cache; maxS rows a kv head. */
+int embla_kv_append(const void* qkv, void* cache, const EmblaKVJob* jobs, int njobs, int pm_pos,
+                    int maxS, int T, hipStream_t stream);
+
+/* Query preparation (head_norm with ng gains + bf16 rounding; attention.metal:167-169,
+ * prefill.metal:406-426): qraw bf16 rows of `stride` elements, n_q heads, T tokens ->
+ * out [T][n_q][128] in out_dtype. */
+int embla_q_prep(const void* qraw, const void* g1, const void* g2, int ng, int stride, int T,
+                 int n_q, void* out, int out_dtype, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* EMBLA_ATTN_H */

@@ -1,0 +1,57 @@
+"""The C ABI library loads, exports every entry point include/embla_attn.h declares, and rejects
+invalid arguments on the host (no GPU needed: validation precedes any HIP call)."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from embla_attn import _lib
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "embla_attn.h"
+
+
+def declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(embla_\w+)\s*\(", text)))
+
+
+def test_header_symbols_exported():
+    L = _lib.lib()
+    names = declared()
+    assert len(names) >= 8
+    for n in names:
+        assert hasattr(L, n), n
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+
+
+def test_version_and_workspace():
+    L = _lib.lib()
+    assert L.embla_version() >= 1
+    assert L.embla_workspace_bytes(32768, 16) > 1024 * 16 * 130 * 4
+    assert L.embla_workspace_bytes(0, 16) == 0
+
+
+@pytest.mark.parametrize("S,max_s,n_q,n_kv", [(0, 1024, 16, 4), (2000, 1024, 16, 4), (10, 1000, 16, 4),
+                                                (10, 1024, 16, 3)])
+def test_decode_rejects_bad_shapes(S, max_s, n_q, n_kv):
+    L = _lib.lib()
+    d = C.c_void_p(16)
+    rc = L.embla_decode_int8(d, d, d, d, None, S, max_s, n_q, n_kv, 0, 0, 0, 0, None, 0, None)
+    assert rc == _lib.EMBLA_ERR_INVALID
+
+
+def test_decode_rejects_missing_workspace_and_nulls():
+    L = _lib.lib()
+    d = C.c_void_p(16)
+    assert L.embla_decode_int8(d, d, d, d, None, 4096, 4096, 16, 4, 0, 0, 0, 128, None, 0, None) == _lib.EMBLA_ERR_WORKSPACE
+    assert L.embla_decode_int8(None, d, d, d, None, 64, 64, 16, 4, 0, 0, 0, 0, None, 0, None) == _lib.EMBLA_ERR_INVALID
+    # SCORES only with the reference's ReLU² layers
+    assert L.embla_decode_int8(d, d, d, d, d, 64, 64, 16, 4, 0, 0, 0, 0, None, 0, None) == _lib.EMBLA_ERR_UNSUPPORTED
+
+
+def test_kv_append_rejects_out_of_range():
+    L = _lib.lib()
+    d = C.c_void_p(16)
+    assert L.embla_kv_quant_append(d, d, 1, 512, 10, 1020, 4, d, d, 1024, 0, 0, None) == _lib.EMBLA_ERR_INVALID
+    assert L.embla_kv_quant_append(d, d, 1, 100, 1, 0, 4, d, d, 1024, 0, 0, None) == _lib.EMBLA_ERR_INVALID

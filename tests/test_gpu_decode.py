@@ -1,0 +1,97 @@
+"""Parity of the int8 split-K decode (configs C1 and C3; the reference's attn_full8 / attn_sparse8
+math) against the C oracle on the same seeded inputs."""
+import numpy as np
+import pytest
+
+from conftest import gpu_available
+from gpu_util import assert_close, dev, f16_host, bf16_host, say, upload_int8_case
+from embla_attn import layout, synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch_gpu():
+    if not gpu_available():
+        pytest.skip("no GPU")
+    import torch
+    return torch
+
+
+def run_cfg_decode(torch, c, max_s, chunk=0, ws=None):
+    from embla_attn import ops
+    kc, vc = upload_int8_case(c, max_s)
+    q = dev(c["q"], torch.float16)
+    ws = ws or ops.Workspace(max_s, c["n_q"])
+    o = ops.decode_int8(q, kc, vc, c["S"], max_s, c["n_kv"], chunk=chunk, ws=ws)
+    torch.cuda.synchronize()
+    return f16_host(o)
+
+
+def oracle_cfg(orc, c, weights=0):
+    return orc.decode_int8(synth.f16_val(c["q"]), c["K"], synth.f16_val(c["ks"]), c["V"], synth.f16_val(c["vs"]),
+                           weights=weights)
+
+
+@pytest.mark.parametrize("S,max_s,seed", [(1024, 1024, 0), (1000, 1024, 5), (33, 64, 6), (1, 32, 7), (4096, 4096, 2),
+                                          (16384, 16384, 2), (32768, 32768, 2)])
+def test_decode_softmax_int8_matches_oracle(torch_gpu, orc, S, max_s, seed):
+    say(f"decode softmax int8 S={S} max_s={max_s} seed={seed}")
+    c = synth.decode_int8_case(seed=seed, S=S)
+    got = run_cfg_decode(torch_gpu, c, max_s)
+    assert_close(got, oracle_cfg(orc, c), what=f"S={S}")
+
+
+@pytest.mark.parametrize("chunk", [128, 256, 512, 2048, 4096])
+def test_decode_independent_of_split(torch_gpu, orc, chunk):
+    say(f"decode split chunk={chunk}")
+    c = synth.decode_int8_case(seed=0, S=4000)
+    ref = oracle_cfg(orc, c)
+    got = run_cfg_decode(torch_gpu, c, 4096, chunk=chunk)
+    assert_close(got, ref, what=f"chunk={chunk}")
+
+
+def test_decode_repeated_calls_leave_counters_zero(torch_gpu, orc):
+    from embla_attn import ops
+    say("decode repeated calls, one workspace")
+    ws = ops.Workspace(8192, 16)
+    for seed, S in [(1, 8192), (2, 3000), (3, 8000)]:
+        c = synth.decode_int8_case(seed=seed, S=S)
+        got = run_cfg_decode(torch_gpu, c, 8192, ws=ws)
+        assert_close(got, oracle_cfg(orc, c), what=f"call S={S}")
+    torch_gpu.cuda.synchronize()
+    assert not ws.buf[:256].cpu().numpy().any()
+
+
+def test_full8_reference_mode(torch_gpu, orc):
+    """attn_full8: raw bf16 q with two gains, 2 kv heads, ReLU² + sink, fp32 scales, SCORES."""
+    import torch
+    from embla_attn import ops
+    say("attn_full8 reference mode")
+    S, max_s = 3000, 4096
+    g = synth.SplitMix64(40)
+    qraw = synth.bf16_bits(g.normal(16 * 128) * 2)
+    g1 = synth.bf16_bits(g.normal(128) * 0.2)
+    g2 = synth.bf16_bits(g.normal(128) * 0.2)
+    # a cache as kv_append writes it: normed rows, int8, fp32 scales
+    K = g.int8(2 * S * 128).reshape(2, S, 128)
+    V = g.int8(2 * S * 128).reshape(2, S, 128)
+    ks = (0.02 + 0.01 * g.uniform(2 * S)).astype(np.float32).reshape(2, S)
+    vs = (0.02 + 0.01 * g.uniform(2 * S)).astype(np.float32).reshape(2, S)
+    kc = dev(layout.pack_region(K, ks, max_s, "k"))
+    vc = dev(layout.pack_region(V, vs, max_s, "v"))
+    from embla_attn import _lib
+    part = torch.zeros(_lib.lib().embla_workspace_bytes(max_s, 16), dtype=torch.uint8, device="cuda")
+    counter = torch.zeros(2, dtype=torch.int32, device="cuda")
+    scores = torch.full((2, max_s), -1.0, dtype=torch.float32, device="cuda")
+    o = torch.empty((16, 128), dtype=torch.bfloat16, device="cuda")
+    ops.attn_full8(dev(qraw, torch.bfloat16), dev(g1, torch.bfloat16), dev(g2, torch.bfloat16), kc, vc, part, scores,
+                   counter, o, S, max_s, ng=2)
+    torch.cuda.synchronize()
+    qn = np.stack([orc.head_norm(synth.bf16_val(qraw.reshape(16, 128)[h]), synth.bf16_val(g1), synth.bf16_val(g2), 2)
+                   for h in range(16)])
+    ref, ref_sc = orc.decode_int8(qn, K, ks, V, vs, weights=1, want_scores=True)
+    assert_close(bf16_host(o), ref, what="full8 o")
+    # scores carry q's 15-bit fixed point (|q error| <= absmax(q)/64000): 1e-3 of their scale
+    assert_close(scores.cpu().numpy()[:, :S], ref_sc, atol=1e-3 * np.abs(ref_sc).max(), rtol=0, what="full8 scores")
+    assert not counter.cpu().numpy().any()
