@@ -12,7 +12,9 @@ namespace {
 constexpr size_t kCounterBytes = 1024;  // reserved (zeroed by embla_workspace_init)
 constexpr int kMaxChunks = 256;         // chunks the merge kernel takes (decode_full.hip)
 constexpr int kMaxKV = 16;
-constexpr int kPartStride = 132;        // floats a (chunk, query head) partial: acc[128], m, l, pad
+constexpr int kPartStride = 132;
+constexpr int kRefWindow = 128;         // the reference's sliding window (Engine.swift:9)
+constexpr int kRefRing = 4096;          // the reference's ring (attention.metal:6)        // floats a (chunk, query head) partial: acc[128], m, l, pad
 
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
@@ -161,6 +163,50 @@ int embla_kv_append(const void* qkv, void* cache, const EmblaKVJob* jobs, int nj
         if (rc) return rc;
     }
     return EMBLA_OK;
+}
+
+int embla_sliding_decode(const void* q, const void* k_new, const void* v_new, void* kring, void* vring,
+                         void* o, int pos, int window, int ring, int n_q, int n_kv, int dtype, int chunk,
+                         void* ws, size_t ws_bytes, hipStream_t stream) {
+    if (!q || !k_new || !v_new || !kring || !vring || !o) return EMBLA_ERR_INVALID;
+    if (pos < 0 || window <= 0 || ring <= 0 || ring % 32 || window > ring || !valid_act(dtype)) return EMBLA_ERR_INVALID;
+    if (n_kv <= 0 || n_q % n_kv || n_kv > kMaxKV) return EMBLA_ERR_INVALID;
+    if (n_q / n_kv != 4) return EMBLA_ERR_UNSUPPORTED;
+    if (chunk < 0 || chunk % 32) return EMBLA_ERR_INVALID;
+    const int lo = pos - window + 1 > 0 ? pos - window + 1 : 0;
+    const int span = pos - (lo & ~31);   // ring keys from the first tile on (the current key is extra)
+    const int ch = chunk ? chunk : env_int("EMBLA_SLIDING_CH", 128);
+    int C = (span + ch - 1) / ch;
+    if (C < 1) C = 1;
+    if (C > kMaxChunks) return EMBLA_ERR_INVALID;
+    if (C > 1 && (!ws || ws_bytes < embla_workspace_bytes(ring, n_q))) return EMBLA_ERR_WORKSPACE;
+    RingArgs a;
+    a.q = (const uint16_t*)q; a.q_stride = 128;
+    a.k_new = (const uint16_t*)k_new; a.v_new = (const uint16_t*)v_new;
+    a.qg = nullptr; a.kg = nullptr;
+    a.kring = (uint16_t*)kring; a.vring = (uint16_t*)vring;
+    a.part = ws ? carve(ws, ring, n_q).part : nullptr;
+    a.o = (uint16_t*)o;
+    a.pos = pos; a.W = window; a.R = ring; a.CH = ch; a.C = C; a.n_q = n_q; a.n_kv = n_kv;
+    a.bf16 = dtype == EMBLA_BF16; a.preops = false;
+    return launch_ring_decode(a, stream);
+}
+
+int embla_attn_sliding(const void* qkv, const void* qg, const void* kg, void* kc, void* vc, void* o,
+                       int pos, hipStream_t stream) {
+    if (!qkv || !qg || !kg || !kc || !vc || !o || pos < 0) return EMBLA_ERR_INVALID;
+    const uint16_t* row = (const uint16_t*)qkv;
+    RingArgs a;
+    a.q = row; a.q_stride = 128;
+    a.k_new = row + 16 * 128; a.v_new = row + 20 * 128;
+    a.qg = (const uint16_t*)qg; a.kg = (const uint16_t*)kg;
+    a.kring = (uint16_t*)kc; a.vring = (uint16_t*)vc;
+    a.part = nullptr;
+    a.o = (uint16_t*)o;
+    a.pos = pos; a.W = kRefWindow; a.R = kRefRing; a.CH = kRefWindow + 32; a.C = 1; a.n_q = 16; a.n_kv = 4;
+    // one chunk: at most 127 ring keys counted from a 32-aligned tile fit in kRefWindow + 32
+    a.bf16 = true; a.preops = true;
+    return launch_ring_decode(a, stream);
 }
 
 }  // extern "C"

@@ -309,7 +309,7 @@ __global__ __launch_bounds__(256, 2) void full_decode_kernel(
 /// (slice s of 4 dims, chunk group r) loads its chunks' slices, maxima and sums in one round.
 template <bool RELU2, bool OBF>
 __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ part, uint16_t* __restrict__ o,
-                                                           int C, int n_q, float sink) {
+                                                           int C, int n_q, float sink, float oscale) {
     constexpr int NR = 32, MAXK = 8;   // chunk groups; chunks a thread (C <= 256)
     const int h = blockIdx.x, d0 = 32 * blockIdx.y;
     const int tid = threadIdx.x, sl = tid & 7, r = tid >> 3;
@@ -356,7 +356,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
     f4_t T = {0, 0, 0, 0};
     float L = 0.0f;
     for (int i = 0; i < NR; i++) { T += sa[i][sl]; L += sl_[i]; }
-    const float inv = 1.0f / (RELU2 ? WSCALE * (sink + L) : WSCALE * L);
+    const float inv = 1.0f / (RELU2 ? oscale * (sink + L) : oscale * L);
 #pragma unroll
     for (int i = 0; i < 4; i++) o[(size_t)h * HD + d + i] = f2a<OBF>(T[i] * inv);
 }
@@ -378,12 +378,18 @@ int launch_full_decode(const FullDecodeArgs& a, hipStream_t st) {
     else if (gq == 8 && !a.relu2 && !a.scale32 && !a.out_bf16 && !a.scores) EMBLA_FD(8, false, false, false, false);
     else return EMBLA_ERR_UNSUPPORTED;
 #undef EMBLA_FD
-    if (a.C > 1) {
-        const dim3 mg(a.n_q, HD / 32);
-        if (a.relu2 && a.out_bf16) hipLaunchKernelGGL((decode_merge_kernel<true, true>), mg, block, 0, st, a.part, a.o, a.C, a.n_q, sink);
-        else if (!a.relu2 && a.out_bf16) hipLaunchKernelGGL((decode_merge_kernel<false, true>), mg, block, 0, st, a.part, a.o, a.C, a.n_q, sink);
-        else hipLaunchKernelGGL((decode_merge_kernel<false, false>), mg, block, 0, st, a.part, a.o, a.C, a.n_q, sink);
-    }
+    if (a.C > 1) return launch_decode_merge(a.part, a.o, a.C, a.n_q, a.relu2, a.out_bf16, WSCALE, st);
+    return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
+}
+
+int launch_decode_merge(const float* part, uint16_t* o, int C, int n_q, bool relu2, bool out_bf16, float oscale,
+                        hipStream_t st) {
+    const dim3 mg(n_q, HD / 32), block(256);
+    const float sink = 11.313708498984761f;   // sqrt(128)
+    if (relu2 && out_bf16) hipLaunchKernelGGL((decode_merge_kernel<true, true>), mg, block, 0, st, part, o, C, n_q, sink, oscale);
+    else if (!relu2 && out_bf16) hipLaunchKernelGGL((decode_merge_kernel<false, true>), mg, block, 0, st, part, o, C, n_q, sink, oscale);
+    else if (!relu2) hipLaunchKernelGGL((decode_merge_kernel<false, false>), mg, block, 0, st, part, o, C, n_q, sink, oscale);
+    else return EMBLA_ERR_UNSUPPORTED;
     return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
 }
 

@@ -18,6 +18,25 @@ struct FullDecodeArgs {
     bool relu2, scale32, out_bf16;
 };
 int launch_full_decode(const FullDecodeArgs& a, hipStream_t st);
+/// Merges C chunk partials [C][n_q][132] into o [n_q][128]; the partials' sums carry a factor oscale.
+int launch_decode_merge(const float* part, uint16_t* o, int C, int n_q, bool relu2, bool out_bf16, float oscale,
+                        hipStream_t st);
+
+struct RingArgs {
+    const uint16_t* q;       // head h's row at q + h * q_stride
+    int q_stride;
+    const uint16_t* k_new;   // kv head h at + h * 128
+    const uint16_t* v_new;
+    const uint16_t* qg;      // gains (pre-ops only)
+    const uint16_t* kg;
+    uint16_t* kring;         // [n_kv][R/32] tiles, ES = 2
+    uint16_t* vring;
+    float* part;
+    uint16_t* o;
+    int pos, W, R, CH, C, n_q, n_kv;
+    bool bf16, preops;
+};
+int launch_ring_decode(const RingArgs& a, hipStream_t st);
 
 struct KVQuantArgs {
     const uint16_t* k;   // [T] rows of k, row stride `stride` elements, kv head h at h * 128

@@ -47,6 +47,8 @@ SIGNATURES = {
     "embla_kv_quant_append": (i32, [vp, vp, i32, i32, i32, i32, i32, vp, vp, i32, i32, i32, vp]),
     "embla_kv_append": (i32, [vp, vp, C.POINTER(KVJob), i32, i32, i32, i32, vp]),
     "embla_q_prep": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, i32, vp]),
+    "embla_sliding_decode": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp, sz, vp]),
+    "embla_attn_sliding": (i32, [vp, vp, vp, vp, vp, vp, i32, vp]),
 }
 
 _lib = None

@@ -70,3 +70,19 @@ def attn_full8(qraw, g1, g2, kc, vc, part, scores, counter, o, S, maxS, ng=2, CH
     p = _lib.AttnParams(S, CH, 0, maxS, S - 1, ng, 0, 0)
     call("embla_attn_full8", _p(qraw), _p(g1), _p(g2), _p(kc), _p(vc), _p(part), _p(scores),
          _p(counter), _p(o), C.byref(p), stream_handle(stream))
+
+
+def sliding_decode(q, k_new, v_new, kring, vring, pos, window, ring, n_kv, dtype=F16, chunk=0,
+                   ws: Workspace | None = None, out=None, stream=None):
+    """One decode step over a 16-bit ring: appends (k_new, v_new) at pos, attends the window."""
+    n_q = q.shape[0]
+    if out is None:
+        out = torch.empty((n_q, 128), dtype=_DT[dtype], device=q.device)
+    call("embla_sliding_decode", _p(q), _p(k_new), _p(v_new), _p(kring), _p(vring), _p(out), pos, window, ring,
+         n_q, n_kv, dtype, chunk, ws.ptr if ws else None, ws.nbytes if ws else 0, stream_handle(stream))
+    return out
+
+
+def attn_sliding(qkv, qg, kg, kc, vc, o, pos, stream=None):
+    """Reference-signature sliding layer (attention.metal:26-102)."""
+    call("embla_attn_sliding", _p(qkv), _p(qg), _p(kg), _p(kc), _p(vc), _p(o), pos, stream_handle(stream))

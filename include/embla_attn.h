@@ -89,6 +89,25 @@ int embla_attn_full8(const void* qraw, const void* g1, const void* g2, const voi
                      const void* vc, float* part, float* scores, uint32_t* counter, void* o,
                      const EmblaAttnParams* p, hipStream_t stream);
 
+/* ---------------------------------------------------------------- sliding window over a ring
+ * One query token attends the last min(pos + 1, window) positions, the current one included, of
+ * a 16-bit ring of `ring` slots a kv head (position p at slot p % ring; K and V in the tile layout
+ * with ES = 2); the current k, v are written into slot pos % ring. Softmax, scale 1/sqrt(128).
+ * q [n_q][128], k_new, v_new [n_kv][128], o [n_q][128], all in dtype (EMBLA_F16 or EMBLA_BF16).
+ * window <= ring, ring a multiple of 32; chunk: ring keys a workgroup (0 = library's choice);
+ * ws as embla_decode_int8 (sized for max_s = ring), unused when one chunk covers the window.
+ * The BASELINE config C2 (fp16 ring of 8192, window 1024) runs through this. */
+int embla_sliding_decode(const void* q, const void* k_new, const void* v_new, void* kring, void* vring,
+                         void* o, int pos, int window, int ring, int n_q, int n_kv, int dtype, int chunk,
+                         void* ws, size_t ws_bytes, hipStream_t stream);
+
+/* Reference-signature sliding layer (attn_sliding, attention.metal:26-102; bound at
+ * Engine.swift:771-780): qkv bf16 [q 16*128 | k 4*128 | v 4*128]; q and k RMS-normed with gains
+ * qg / kg (ng = 1) and rotated (RoPE, common.metal:39-47), rounded to bf16; window 128 over a bf16
+ * ring of 4096 (kc, vc in the tile layout); o bf16 [16][128]. */
+int embla_attn_sliding(const void* qkv, const void* qg, const void* kg, void* kc, void* vc, void* o,
+                       int pos, hipStream_t stream);
+
 /* ---------------------------------------------------------------- quantise-and-append
  * T new positions p0 .. p0+T-1 of K and V rows into an int8 layer cache (write_row8,
  * common.metal:72-84; kv_append / kv_append_b, attention.metal:113-140, prefill.metal:182-212):
