@@ -9,7 +9,8 @@ the 256 MB MALL, so every layer streams from HBM). A step is the 16 layers' atte
 `value` is algorithmic HBM bytes a step / time (1040·L + 8192 bytes a layer).
 
 Also reported: the C3 context sweep (4096, 16384, 32768; µs a layer), C2 sliding-window decode
-(512 steps over an fp16 ring of 8192, window 1024), and the CPU baseline: the C oracle
+(512 steps over an fp16 ring of 8192, window 1024), C4 sparse-layer decode at 32k (indexer, exact
+top-k, attention over 1152 gathered rows), and the CPU baseline: the C oracle
 (oracle/oracle.c, a scalar fp32 restatement) timed on a bounded sample on this host.
 """
 from __future__ import annotations
@@ -126,6 +127,25 @@ def bench_c2(torch, n_steps=512, reps=5):
                 gbs_cache_resident=2 * W * n_kv * 128 * 2 / (us * 1e-6) / 1e9)
 
 
+def bench_c4(torch, reps=20):
+    """Config C4: one sparse-layer decode step at context 32768 (index scores, exact top-1024 +
+    latest 128, attention over the 1152 gathered fp16 rows); one graph of the step."""
+    from embla_attn import ops, synth
+    c = synth.sparse_case(seed=3, ctx=32768)
+    dev = lambda a, dt=None: (torch.from_numpy(a).cuda().view(dt) if dt is not None else torch.from_numpy(a).cuda())
+    q, qi, w, ki = dev(c["q"], torch.float16), dev(c["qi"], torch.float16), dev(c["w"]), dev(c["ki"], torch.float16)
+    K, V = dev(c["K"], torch.float16), dev(c["V"], torch.float16)
+    ws = ops.SparseWorkspace(32768, 16)
+    out = torch.empty(16, 128, dtype=torch.float16, device="cuda")
+
+    def run():
+        ops.sparse_layer_decode(q, qi, w, ki, K, V, 32768, 32768, 4, ws, out=out)
+    wall, ms = time_graph(torch, run, reps, 3)
+    nbytes = 32768 * 64 * 2 + 1152 * 4 * 2 * 128 * 2
+    return dict(us_per_layer=ms * 1000, tokens_per_s=1e3 / ms, algorithmic_bytes=nbytes,
+                gbs=nbytes / (ms * 1e-3) / 1e9)
+
+
 def cpu_baseline(case, L, budget_s=10.0):
     """The C oracle (scalar fp32 restatement, one thread) on whole C3 layers at context L."""
     sys.path.insert(0, str(ROOT / "oracle"))
@@ -171,6 +191,7 @@ def main():
     L = 32768
     res, case, out0, _ = bench_c3(torch, args.steps, args.warmup)
     c2 = bench_c2(torch)
+    c4 = bench_c4(torch)
     head = res[L]
     line = {
         "metric": METRIC,
@@ -202,6 +223,7 @@ def main():
         "c3_sweep_us_per_layer": {str(k): round(v["us_per_layer"], 3) for k, v in res.items()},
         "c3_sweep_gbs": {str(k): round(v["gbs"], 1) for k, v in res.items()},
         "c2_sliding": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in c2.items()},
+        "c4_sparse": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in c4.items()},
     }
     if not args.no_cpu:
         cb, ref = cpu_baseline(case, L)

@@ -14,7 +14,8 @@ constexpr int kMaxChunks = 256;         // chunks the merge kernel takes (decode
 constexpr int kMaxKV = 16;
 constexpr int kPartStride = 132;
 constexpr int kRefWindow = 128;         // the reference's sliding window (Engine.swift:9)
-constexpr int kRefRing = 4096;          // the reference's ring (attention.metal:6)        // floats a (chunk, query head) partial: acc[128], m, l, pad
+constexpr int kRefRing = 4096;          // the reference's ring (attention.metal:6)
+constexpr int kTopK = 1024, kRecent = 128;   // Engine.swift:9 (topk, recent)        // floats a (chunk, query head) partial: acc[128], m, l, pad
 
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
@@ -207,6 +208,71 @@ int embla_attn_sliding(const void* qkv, const void* qg, const void* kg, void* kc
     // one chunk: at most 127 ring keys counted from a 32-aligned tile fit in kRefWindow + 32
     a.bf16 = true; a.preops = true;
     return launch_ring_decode(a, stream);
+}
+
+int embla_index_scores(const void* qi, const float* w, const void* ki, float* scores, int n, int n_ih,
+                       hipStream_t stream) {
+    if (!qi || !w || !ki || !scores || n <= 0) return EMBLA_ERR_INVALID;
+    if (n_ih != 1 && n_ih != 2 && n_ih != 4) return EMBLA_ERR_UNSUPPORTED;
+    return launch_index_scores((const uint16_t*)qi, w, (const uint16_t*)ki, scores, n, n_ih, stream);
+}
+
+int embla_select_topk(const float* scores, int score_stride, uint32_t* idx, int idx_stride, int S, int n_sets,
+                      int topk, int recent, hipStream_t stream) {
+    if (!scores || !idx || n_sets <= 0 || topk <= 0 || recent < 0) return EMBLA_ERR_INVALID;
+    if (S <= topk + recent) return EMBLA_ERR_INVALID;   // the reference selects only past topk + recent keys
+    if (n_sets > 1 && (score_stride < S || idx_stride < topk + recent)) return EMBLA_ERR_INVALID;
+    return launch_select_topk(scores, score_stride, idx, idx_stride, S, n_sets, topk, recent, stream);
+}
+
+int embla_select_keys(const float* scores, uint32_t* idx, int S, int maxS, hipStream_t stream) {
+    return embla_select_topk(scores, maxS, idx, kTopK + kRecent, S, 2, kTopK, kRecent, stream);
+}
+
+int embla_sparse_decode(const void* q, const void* kc, const void* vc, const uint32_t* idx, int idx_stride,
+                        int nsel, void* o, int max_s, int n_q, int n_kv, int dtype, int chunk, void* ws,
+                        size_t ws_bytes, hipStream_t stream) {
+    if (!q || !kc || !vc || !o || nsel <= 0 || max_s <= 0 || idx_stride < 0) return EMBLA_ERR_INVALID;
+    if (!idx && nsel > max_s) return EMBLA_ERR_INVALID;
+    if (n_kv <= 0 || n_q % n_kv || n_kv > kMaxKV || !valid_act(dtype)) return EMBLA_ERR_INVALID;
+    if (n_q / n_kv != 4 && n_q / n_kv != 8) return EMBLA_ERR_UNSUPPORTED;
+    if (chunk < 0 || chunk % 32) return EMBLA_ERR_INVALID;
+    const int ch = chunk ? chunk : env_int("EMBLA_SPARSE_CH", 128);
+    const int C = (nsel + ch - 1) / ch;
+    if (C > kMaxChunks) return EMBLA_ERR_INVALID;
+    if (C > 1 && (!ws || ws_bytes < embla_workspace_bytes(32 * C, n_q))) return EMBLA_ERR_WORKSPACE;
+    SparseArgs a;
+    a.q = (const uint16_t*)q; a.kc = (const uint16_t*)kc; a.vc = (const uint16_t*)vc;
+    a.idx = idx; a.idx_stride = idx_stride; a.nsel = nsel;
+    a.part = ws ? carve(ws, 32 * C, n_q).part : nullptr;
+    a.o = (uint16_t*)o;
+    a.CH = ch; a.C = C; a.max_s = max_s; a.n_q = n_q; a.n_kv = n_kv; a.bf16 = dtype == EMBLA_BF16;
+    return launch_sparse_decode(a, stream);
+}
+
+size_t embla_sparse_workspace_bytes(int max_s, int n_q) {
+    if (max_s <= 0 || n_q <= 0) return 0;
+    return round_up((size_t)max_s * 4, 256) + round_up((size_t)(kTopK + kRecent) * 4, 256) +
+           embla_workspace_bytes(kTopK + kRecent, n_q);
+}
+
+int embla_sparse_layer_decode(const void* q, const void* qi, const float* w, const void* ki, const void* kc,
+                              const void* vc, void* o, int S, int max_s, int n_q, int n_kv, int n_ih, int dtype,
+                              void* ws, size_t ws_bytes, hipStream_t stream) {
+    if (!q || !qi || !w || !ki || !kc || !vc || !o || S <= 0 || S > max_s) return EMBLA_ERR_INVALID;
+    if (!ws || ws_bytes < embla_sparse_workspace_bytes(max_s, n_q)) return EMBLA_ERR_WORKSPACE;
+    char* p = (char*)ws;
+    float* scores = (float*)p;
+    uint32_t* idx = (uint32_t*)(p + round_up((size_t)max_s * 4, 256));
+    void* aws = p + round_up((size_t)max_s * 4, 256) + round_up((size_t)(kTopK + kRecent) * 4, 256);
+    const size_t abytes = embla_workspace_bytes(kTopK + kRecent, n_q);
+    if (S <= kTopK + kRecent)   // every key (Engine.swift:796-799: no selection yet)
+        return embla_sparse_decode(q, kc, vc, nullptr, 0, S, o, max_s, n_q, n_kv, dtype, 0, aws, abytes, stream);
+    int rc = embla_index_scores(qi, w, ki, scores, S - kRecent, n_ih, stream);
+    if (rc) return rc;
+    rc = embla_select_topk(scores, 0, idx, 0, S, 1, kTopK, kRecent, stream);
+    if (rc) return rc;
+    return embla_sparse_decode(q, kc, vc, idx, 0, kTopK + kRecent, o, max_s, n_q, n_kv, dtype, 0, aws, abytes, stream);
 }
 
 }  // extern "C"

@@ -1,0 +1,190 @@
+// Sparse-layer decode: softmax attention over a gathered set of cache rows (16-bit K/V), one query.
+//
+// Follows attn_sparse / attn_sparse8 with SEL (Sources/EmblaMetal/Kernels/attention.metal:370-441,
+// 448-584): keys are the rows idx[kv head][j] (or one set shared by every kv head, as the BASELINE
+// config C4's selection), split into chunks whose partials are merged afterwards
+// (decode_merge_kernel, decode_full.hip).
+//
+// MI355X design: the rows are gathered by a wave 32 at a time (each 16-byte load of the wave covers
+// four whole 256-byte rows) into a wave-private LDS tile with a padded row stride; the MFMA A
+// operand of S^T = K q^T is read back from it as 16-byte rows, and the V operand of O += W V is
+// assembled from eight 16-byte row reads a lane (a register transpose), so both products run on
+// v_mfma_f32_16x16x32_{f16,bf16}.
+#include "common.hpp"
+#include "embla_internal.hpp"
+
+namespace embla {
+
+constexpr int SROW = HD + 8;   // LDS row stride in 16-bit elements (272 bytes: conflict-free rows)
+constexpr int SPS = HD + 4;    // partial record stride, as decode_full.hip
+
+template <bool BF>
+__device__ __forceinline__ f4_t mfma16s(u4_t a, u4_t b, f4_t c) {
+    if constexpr (BF) return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8_t, a), __builtin_bit_cast(b8_t, b), c, 0, 0, 0);
+    else return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, a), __builtin_bit_cast(h8_t, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int GQ, bool BF>
+__global__ __launch_bounds__(256) void sparse_decode_kernel(SparseArgs a) {
+    const int c = blockIdx.x, kvh = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int n = lane & 15, g = lane >> 4;
+    const int j0 = c * a.CH, j1 = min(a.nsel, j0 + a.CH);
+    const uint32_t* rows = a.idx ? a.idx + (size_t)kvh * a.idx_stride : nullptr;   // null: rows 0 .. nsel-1
+    const uint16_t* kb = a.kc + (size_t)kvh * a.max_s * HD;
+    const uint16_t* vb = a.vc + (size_t)kvh * a.max_s * HD;
+
+    __shared__ uint16_t stage[4][2][32 * SROW];
+    uint16_t* Ks = stage[w][0];
+    uint16_t* Vs = stage[w][1];
+
+    // q^T, B operand: lane (head n, group g), MFMA u: dims 32g + 8u .. + 7
+    u4_t qb[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const u4_t r = ld16(a.q + (size_t)(kvh * GQ + (n < GQ ? n : 0)) * HD + 32 * g + 8 * u);
+        qb[u] = n < GQ ? r : (u4_t){0, 0, 0, 0};
+    }
+    const float sc = 0.08838834764831845f * 1.4426950408889634f;
+    float m = NEG_INF, l = 0.0f;
+    f4_t O[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) O[u] = (f4_t){0, 0, 0, 0};
+
+    for (int t0 = j0 + 32 * w; t0 < j1; t0 += 128) {
+        // gather: load j covers rows 4j .. 4j + 3, lane l: row 4j + l / 16, dims 8 (l % 16) ..
+        u4_t kr[8], vr[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int p = t0 + 4 * j + (lane >> 4);
+            const size_t row = p < j1 ? (size_t)min(rows ? (int)rows[p] : p, a.max_s - 1) : 0;   // rows clamped in range
+            kr[j] = ld16(kb + row * HD + 8 * n);
+            vr[j] = ld16(vb + row * HD + 8 * n);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int r = 4 * j + (lane >> 4);
+            *(u4_t*)(Ks + r * SROW + 8 * n) = kr[j];
+            *(u4_t*)(Vs + r * SROW + 8 * n) = vr[j];
+        }
+        wave_lds_sync();
+        // S^T: lane (head n, group g) item i of half t = key 16t + 4g + i
+        float x[8];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            f4_t st = {0, 0, 0, 0};
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                st = mfma16s<BF>(*(const u4_t*)(Ks + (16 * t + n) * SROW + 32 * g + 8 * u), qb[u], st);
+#pragma unroll
+            for (int i = 0; i < 4; i++) x[4 * t + i] = t0 + 16 * t + 4 * g + i < j1 ? st[i] * sc : NEG_INF;
+        }
+        float mt = NEG_INF;
+#pragma unroll
+        for (int e = 0; e < 8; e++) mt = fmaxf(mt, x[e]);
+        mt = fmaxf(mt, shfl_xor(mt, 16));
+        mt = fmaxf(mt, shfl_xor(mt, 32));
+        const float mn = fmaxf(m, mt);
+        if (__any(n < GQ && mn > m)) {
+            if (__any(n < GQ && m != NEG_INF)) {
+                const float corr = m == NEG_INF ? 0.0f : exp2f(m - mn);
+                l *= corr;
+                float cf[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float c0 = readlane(corr, i);
+                    if constexpr (GQ == 8) cf[i] = g == 1 ? readlane(corr, 4 + i) : c0;
+                    else cf[i] = c0;
+                }
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) O[u][i] *= cf[i];
+            }
+            m = mn;
+        }
+        u4_t wb;
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            const float p0 = exp2f(x[e] - m), p1 = exp2f(x[e + 1] - m);
+            l += p0 + p1;
+            wb[e / 2] = (uint32_t)f2a<BF>(p0) | ((uint32_t)f2a<BF>(p1) << 16);
+        }
+        // V operand: lane (dim column n, group g), MFMA u = dim 8n + u, item e = key 16t + 4g + i
+        u4_t vrow[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) vrow[e] = *(const u4_t*)(Vs + (16 * (e >> 2) + 4 * g + (e & 3)) * SROW + 8 * n);
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            u4_t b;
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                const uint32_t lo = (vrow[e][u >> 1] >> (16 * (u & 1))) & 0xFFFF;
+                const uint32_t hi = (vrow[e + 1][u >> 1] >> (16 * (u & 1))) & 0xFFFF;
+                b[e / 2] = lo | (hi << 16);
+            }
+            O[u] = mfma16s<BF>(wb, b, O[u]);
+        }
+        wave_lds_sync();   // the next tile's stores come after every lane's reads
+    }
+
+    // ---- merge the 4 waves (LDS), then this chunk's partial (or o with one chunk)
+    __shared__ float om[4][GQ][HD];
+    __shared__ float mm[4][GQ], ll[4][GQ];
+    l += shfl_xor(l, 16);
+    l += shfl_xor(l, 32);
+    if (g == 0 && n < GQ) { mm[w][n] = m; ll[w][n] = l; }
+#pragma unroll
+    for (int u = 0; u < 8; u++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (4 * g + i < GQ) om[w][4 * g + i][8 * n + u] = O[u][i];
+    __syncthreads();
+    constexpr int PER = GQ * HD / 256;
+    const int oh = tid * PER / HD, od = tid * PER % HD;
+    const float M = fmaxf(fmaxf(mm[0][oh], mm[1][oh]), fmaxf(mm[2][oh], mm[3][oh]));
+    float f[4], L = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ww++) {
+        f[ww] = mm[ww][oh] == NEG_INF ? 0.0f : exp2f(mm[ww][oh] - M);
+        L += ll[ww][oh] * f[ww];
+    }
+    float acc[PER];
+#pragma unroll
+    for (int e = 0; e < PER; e++) {
+        float s = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < 4; ww++) s += om[ww][oh][od + e] * f[ww];
+        acc[e] = s;
+    }
+    const int hq = kvh * GQ + oh;
+    if (a.C == 1) {
+#pragma unroll
+        for (int e = 0; e < PER; e++) a.o[(size_t)hq * HD + od + e] = f2a<BF>(acc[e] / L);
+        return;
+    }
+    float* pp = a.part + ((size_t)c * a.n_kv * GQ + hq) * SPS;
+#pragma unroll
+    for (int e = 0; e < PER; e++) pp[od + e] = acc[e];
+    if (od == 0) { pp[HD] = M; pp[HD + 1] = L; }
+}
+
+int launch_sparse_decode(const SparseArgs& a, hipStream_t st) {
+    const dim3 grid(a.C, a.n_kv), block(256);
+    const int gq = a.n_q / a.n_kv;
+    if (gq == 4 && !a.bf16) hipLaunchKernelGGL((sparse_decode_kernel<4, false>), grid, block, 0, st, a);
+    else if (gq == 4 && a.bf16) hipLaunchKernelGGL((sparse_decode_kernel<4, true>), grid, block, 0, st, a);
+    else if (gq == 8 && a.bf16) hipLaunchKernelGGL((sparse_decode_kernel<8, true>), grid, block, 0, st, a);
+    else if (gq == 8 && !a.bf16) hipLaunchKernelGGL((sparse_decode_kernel<8, false>), grid, block, 0, st, a);
+    else return EMBLA_ERR_UNSUPPORTED;
+    if (a.C > 1) return launch_decode_merge(a.part, a.o, a.C, a.n_q, false, a.bf16, 1.0f, st);
+    return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
+}
+
+}  // namespace embla

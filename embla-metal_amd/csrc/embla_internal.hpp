@@ -38,6 +38,23 @@ struct RingArgs {
 };
 int launch_ring_decode(const RingArgs& a, hipStream_t st);
 
+struct SparseArgs {
+    const uint16_t* q;       // [n_q][128]
+    const uint16_t* kc;      // 16-bit rows [n_kv][max_s][128]
+    const uint16_t* vc;
+    const uint32_t* idx;     // rows of kv head h at idx + h * idx_stride (stride 0: one set); null: 0 .. nsel-1
+    int idx_stride, nsel;
+    float* part;
+    uint16_t* o;
+    int CH, C, max_s, n_q, n_kv;
+    bool bf16;
+};
+int launch_sparse_decode(const SparseArgs& a, hipStream_t st);
+int launch_select_topk(const float* scores, int score_stride, uint32_t* idx, int idx_stride, int S, int n_sets,
+                       int topk, int recent, hipStream_t st);
+int launch_index_scores(const uint16_t* qi, const float* w, const uint16_t* ki, float* scores, int n, int n_ih,
+                        hipStream_t st);
+
 struct KVQuantArgs {
     const uint16_t* k;   // [T] rows of k, row stride `stride` elements, kv head h at h * 128
     const uint16_t* v;

@@ -49,6 +49,12 @@ SIGNATURES = {
     "embla_q_prep": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, i32, vp]),
     "embla_sliding_decode": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp, sz, vp]),
     "embla_attn_sliding": (i32, [vp, vp, vp, vp, vp, vp, i32, vp]),
+    "embla_index_scores": (i32, [vp, vp, vp, vp, i32, i32, vp]),
+    "embla_select_topk": (i32, [vp, i32, vp, i32, i32, i32, i32, i32, vp]),
+    "embla_select_keys": (i32, [vp, vp, i32, i32, vp]),
+    "embla_sparse_decode": (i32, [vp, vp, vp, vp, i32, i32, vp, i32, i32, i32, i32, i32, vp, sz, vp]),
+    "embla_sparse_workspace_bytes": (sz, [i32, i32]),
+    "embla_sparse_layer_decode": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, sz, vp]),
 }
 
 _lib = None

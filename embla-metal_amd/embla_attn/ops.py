@@ -86,3 +86,53 @@ def sliding_decode(q, k_new, v_new, kring, vring, pos, window, ring, n_kv, dtype
 def attn_sliding(qkv, qg, kg, kc, vc, o, pos, stream=None):
     """Reference-signature sliding layer (attention.metal:26-102)."""
     call("embla_attn_sliding", _p(qkv), _p(qg), _p(kg), _p(kc), _p(vc), _p(o), pos, stream_handle(stream))
+
+
+def index_scores(qi, w, ki, n, stream=None):
+    scores = torch.empty(n, dtype=torch.float32, device=qi.device)
+    call("embla_index_scores", _p(qi), _p(w), _p(ki), _p(scores), n, qi.shape[0], stream_handle(stream))
+    return scores
+
+
+def select_topk(scores, S, n_sets=1, topk=1024, recent=128, score_stride=0, stream=None):
+    idx = torch.empty((n_sets, topk + recent), dtype=torch.int32, device=scores.device)
+    call("embla_select_topk", _p(scores), score_stride, _p(idx), topk + recent, S, n_sets, topk, recent,
+         stream_handle(stream))
+    return idx
+
+
+def select_keys(scores, S, maxS, stream=None):
+    """Reference-signature select_keys: 2 sets of [maxS] scores -> idx [2][1152]."""
+    idx = torch.empty((2, 1152), dtype=torch.int32, device=scores.device)
+    call("embla_select_keys", _p(scores), _p(idx), S, maxS, stream_handle(stream))
+    return idx
+
+
+def sparse_decode(q, kc, vc, idx, nsel, max_s, n_kv, idx_stride=0, dtype=F16, chunk=0, ws=None, out=None,
+                  stream=None):
+    n_q = q.shape[0]
+    if out is None:
+        out = torch.empty((n_q, 128), dtype=_DT[dtype], device=q.device)
+    call("embla_sparse_decode", _p(q), _p(kc), _p(vc), _p(idx), idx_stride, nsel, _p(out), max_s, n_q, n_kv, dtype,
+         chunk, ws.ptr if ws else None, ws.nbytes if ws else 0, stream_handle(stream))
+    return out
+
+
+class SparseWorkspace:
+    def __init__(self, max_s: int, n_q: int = 16, device="cuda"):
+        self.nbytes = int(lib().embla_sparse_workspace_bytes(max_s, n_q))
+        self.buf = torch.zeros(self.nbytes, dtype=torch.uint8, device=device)
+
+    @property
+    def ptr(self):
+        return _p(self.buf)
+
+
+def sparse_layer_decode(q, qi, w, ki, kc, vc, S, max_s, n_kv, ws: SparseWorkspace, dtype=F16, out=None,
+                        stream=None):
+    n_q = q.shape[0]
+    if out is None:
+        out = torch.empty((n_q, 128), dtype=_DT[dtype], device=q.device)
+    call("embla_sparse_layer_decode", _p(q), _p(qi), _p(w), _p(ki), _p(kc), _p(vc), _p(out), S, max_s, n_q, n_kv,
+         qi.shape[0], dtype, ws.ptr, ws.nbytes, stream_handle(stream))
+    return out

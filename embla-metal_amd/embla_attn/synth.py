@@ -71,3 +71,17 @@ def decode_int8_case(seed: int, S: int, n_q: int = 16, n_kv: int = 4, lo: float 
     V = g.int8(n_kv * S * 128).reshape(n_kv, S, 128)
     vs = f16_bits(lo + (hi - lo) * g.uniform(n_kv * S)).reshape(n_kv, S)
     return dict(q=q, K=K, ks=ks, V=V, vs=vs, S=S, n_q=n_q, n_kv=n_kv)
+
+
+def sparse_case(seed: int, ctx: int, n_q: int = 16, n_kv: int = 4, n_ih: int = 4) -> dict:
+    """Config C4: index heads qi fp16 [n_ih][64] N(0,1), weights w U(0,1) fp32 [n_ih], index keys
+    ki fp16 [ctx][64] N(0,1), q fp16 [n_q][128] N(0,1), K, V fp16 [n_kv][ctx][128] N(0,1).
+    Draw order: qi, w, ki, q, K, V."""
+    g = SplitMix64(seed)
+    qi = f16_bits(g.normal(n_ih * 64)).reshape(n_ih, 64)
+    w = g.uniform(n_ih).astype(np.float32)
+    ki = f16_bits(g.normal(ctx * 64)).reshape(ctx, 64)
+    q = f16_bits(g.normal(n_q * 128)).reshape(n_q, 128)
+    K = f16_bits(g.normal(n_kv * ctx * 128)).reshape(n_kv, ctx, 128)
+    V = f16_bits(g.normal(n_kv * ctx * 128)).reshape(n_kv, ctx, 128)
+    return dict(qi=qi, w=w, ki=ki, q=q, K=K, V=V, S=ctx, n_q=n_q, n_kv=n_kv)

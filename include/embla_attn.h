@@ -108,6 +108,44 @@ int embla_sliding_decode(const void* q, const void* k_new, const void* v_new, vo
 int embla_attn_sliding(const void* qkv, const void* qg, const void* kg, void* kc, void* vc, void* o,
                        int pos, hipStream_t stream);
 
+/* ---------------------------------------------------------------- sparse layers: selection
+ * Index scores (the BASELINE configs' indexer): scores[j] = Σ_h w_h relu(qi_h·ki_j)² for
+ * j < n, qi fp16 [n_ih][64], w fp32 [n_ih], ki fp16 [n][64], n_ih in {1, 2, 4}. The fp32 order
+ * is fixed (so the top-k is reproducible): 8 fma chains over dims 8k .. 8k+7, combined as
+ * ((c0+c1)+(c2+c3))+((c4+c5)+(c6+c7)); r = max(dot, 0); s = fma(w_h, r*r, s) from h = 0. */
+int embla_index_scores(const void* qi, const float* w, const void* ki, float* scores, int n, int n_ih,
+                       hipStream_t stream);
+
+/* Exact top-k (select_keys, attention.metal:647-744), n_sets sets: among keys [0, S - recent) of
+ * set i (scores + i * score_stride) the topk largest (order-preserving float bits; ties go to the
+ * lower index), written to idx + i * idx_stride as: keys above the topk-th value in index order,
+ * then the first keys equal to it in index order, then S - recent .. S - 1. Requires
+ * S > topk + recent and S - recent <= 33024. */
+int embla_select_topk(const float* scores, int score_stride, uint32_t* idx, int idx_stride, int S, int n_sets,
+                      int topk, int recent, hipStream_t stream);
+
+/* Reference-signature select_keys (attention.metal:680-744, bound at Engine.swift:819-827):
+ * 2 sets, scores [2][maxS], idx [2][1152], topk 1024, recent 128. */
+int embla_select_keys(const float* scores, uint32_t* idx, int S, int maxS, hipStream_t stream);
+
+/* Softmax decode over gathered 16-bit rows (attn_sparse with SEL, attention.metal:370-441): kv head
+ * h attends rows idx[h * idx_stride + j], j < nsel (idx_stride 0: one set for every kv head; idx
+ * NULL: rows 0 .. nsel-1) of row-major caches kc, vc [n_kv][max_s][128] in dtype; q, o
+ * [n_q][128]. ws: embla_workspace_bytes(32 * chunks, n_q), unused with one chunk. */
+int embla_sparse_decode(const void* q, const void* kc, const void* vc, const uint32_t* idx, int idx_stride,
+                        int nsel, void* o, int max_s, int n_q, int n_kv, int dtype, int chunk, void* ws,
+                        size_t ws_bytes, hipStream_t stream);
+
+/* Bytes of workspace for embla_sparse_layer_decode. */
+size_t embla_sparse_workspace_bytes(int max_s, int n_q);
+
+/* One sparse-layer decode step (config C4): with S > 1152 keys, index scores of keys
+ * [0, S - 128), the top 1024 plus the latest 128, then attention over those 1152 rows; with
+ * S <= 1152 attention over every key (Engine.swift:796-818). */
+int embla_sparse_layer_decode(const void* q, const void* qi, const float* w, const void* ki, const void* kc,
+                              const void* vc, void* o, int S, int max_s, int n_q, int n_kv, int n_ih, int dtype,
+                              void* ws, size_t ws_bytes, hipStream_t stream);
+
 /* ---------------------------------------------------------------- quantise-and-append
  * T new positions p0 .. p0+T-1 of K and V rows into an int8 layer cache (write_row8,
  * common.metal:72-84; kv_append / kv_append_b, attention.metal:113-140, prefill.metal:182-212):

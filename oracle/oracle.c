@@ -257,9 +257,11 @@ void orc_select_keys(const float* sc, int S, int topk, int recent, uint32_t* out
 }
 
 /* ------------------------------------------------------------------ index scorer (C4/C5)
- * score_j = Σ_h w_h relu(q_h·k_j)², fp16 q [n_ih][64], k [n][64], w [n_ih] fp32, in the fixed
- * order both sides implement: dot = fma chain over d = 0..63 from 0 (fp16 products are exact in
- * fp32, so each step is one rounding), r = max(dot, 0), then s = fma(w_h, r*r, s) over h from 0. */
+ * score_j = Σ_h w_h relu(q_h·k_j)², fp16 q [n_ih][64], k [n][64], w [n_ih] fp32, in the fixed fp32
+ * order the spec gives (and the GPU kernel, select.hip, implements): 8 partial dots c_k, each an
+ * fma chain over dims 8k .. 8k+7 from 0 (fp16 products are exact in fp32, so each step is one
+ * rounding); dot = ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)); r = max(dot, 0); then
+ * s = fma(w_h, r * r, s) over h = 0 .. from s = 0. */
 void orc_index_scores(const uint16_t* qi, const float* w, const uint16_t* ki, int n, int n_ih,
                       float* out) {
     float qf[16 * 64];
@@ -269,8 +271,15 @@ void orc_index_scores(const uint16_t* qi, const float* w, const uint16_t* ki, in
         for (int d = 0; d < 64; d++) kf[d] = orc_f16_to_f32(ki[(size_t)j * 64 + d]);
         float s = 0.0f;
         for (int h = 0; h < n_ih; h++) {
-            float dot = 0.0f;
-            for (int d = 0; d < 64; d++) dot = fmaf(qf[h * 64 + d], kf[d], dot);
+            float c[8];
+            for (int k = 0; k < 8; k++) {
+                float acc = 0.0f;
+                for (int d = 8 * k; d < 8 * k + 8; d++) acc = fmaf(qf[h * 64 + d], kf[d], acc);
+                c[k] = acc;
+            }
+            const float s01 = c[0] + c[1], s23 = c[2] + c[3], s45 = c[4] + c[5], s67 = c[6] + c[7];
+            const float s03 = s01 + s23, s47 = s45 + s67;
+            const float dot = s03 + s47;
             const float r = fmaxf(dot, 0.0f);
             const float r2 = r * r;
             s = fmaf(w[h], r2, s);

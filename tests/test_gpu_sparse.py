@@ -1,0 +1,102 @@
+"""Sparse layers (config C4): the index scorer and the radix top-k are bit-exact with the oracle;
+attention over the selected rows matches within tolerance; the whole layer end to end."""
+import numpy as np
+import pytest
+
+from conftest import gpu_available
+from gpu_util import assert_close, dev, f16_host, say
+from embla_attn import synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch_gpu():
+    if not gpu_available():
+        pytest.skip("no GPU")
+    import torch
+    return torch
+
+
+@pytest.fixture(scope="module")
+def c4():
+    return synth.sparse_case(seed=3, ctx=32768)
+
+
+def test_index_scores_bit_exact(torch_gpu, orc, c4):
+    from embla_attn import ops
+    torch = torch_gpu
+    n = 32768 - 128
+    say("index scores n=32640")
+    got = ops.index_scores(dev(c4["qi"], torch.float16), dev(c4["w"]), dev(c4["ki"], torch.float16), n)
+    ref = orc.index_scores(c4["qi"], c4["w"], c4["ki"][:n])
+    np.testing.assert_array_equal(got.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("case", ["c4", "ties", "all_equal", "negative", "small"])
+def test_select_topk_bit_exact(torch_gpu, orc, c4, case):
+    from embla_attn import ops
+    torch = torch_gpu
+    S = 32768 if case != "small" else 1153
+    if case == "c4":
+        sc = orc.index_scores(c4["qi"], c4["w"], c4["ki"][:S - 128])
+    else:
+        g = synth.SplitMix64(99)
+        sc = g.normal(S - 128).astype(np.float32)
+        if case == "ties":
+            sc = np.round(sc * 3) / 3
+        elif case == "all_equal":
+            sc = np.full(S - 128, 1.25, np.float32)
+        elif case == "negative":
+            sc = -np.abs(sc) - 1
+    sc = sc.astype(np.float32)
+    say(f"select topk case={case}")
+    idx = ops.select_topk(dev(sc), S)
+    ref = orc.select_keys(np.concatenate([sc, np.zeros(128, np.float32)]), S)
+    np.testing.assert_array_equal(idx.cpu().numpy()[0].astype(np.uint32), ref)
+
+
+def test_select_keys_reference_two_sets(torch_gpu, orc):
+    from embla_attn import ops
+    torch = torch_gpu
+    maxS, S = 8192, 5000
+    g = synth.SplitMix64(5)
+    sc = (np.round(g.normal(2 * maxS) * 8) / 8).astype(np.float32).reshape(2, maxS)
+    say("select_keys reference two sets")
+    idx = ops.select_keys(dev(sc), S, maxS)
+    for h in range(2):
+        np.testing.assert_array_equal(idx.cpu().numpy()[h].astype(np.uint32), orc.select_keys(sc[h], S))
+
+
+@pytest.mark.parametrize("nsel,chunk", [(1152, 0), (1152, 1152), (37, 0), (300, 64)])
+def test_sparse_decode_gathered(torch_gpu, orc, c4, nsel, chunk):
+    from embla_attn import ops
+    torch = torch_gpu
+    say(f"sparse decode gathered nsel={nsel} chunk={chunk}")
+    rng = np.random.default_rng(nsel)
+    idx = np.sort(rng.choice(32768, nsel, replace=False)).astype(np.uint32)
+    rng.shuffle(idx)
+    ws = ops.Workspace(32 * ((nsel + 31) // 32) + 4096, 16)
+    o = ops.sparse_decode(dev(c4["q"], torch.float16), dev(c4["K"], torch.float16), dev(c4["V"], torch.float16),
+                          dev(idx.view(np.int32)), nsel, 32768, 4, chunk=chunk, ws=ws)
+    ref = orc.decode_rows(synth.f16_val(c4["q"]), synth.f16_val(c4["K"]), synth.f16_val(c4["V"]), idx.astype(np.int32))
+    assert_close(f16_host(o), ref, what=f"nsel={nsel}")
+
+
+@pytest.mark.parametrize("S", [32768, 1000, 1153])
+def test_sparse_layer_end_to_end(torch_gpu, orc, c4, S):
+    from embla_attn import ops
+    torch = torch_gpu
+    say(f"sparse layer end to end S={S}")
+    ws = ops.SparseWorkspace(32768, 16)
+    K = dev(c4["K"], torch.float16)
+    V = dev(c4["V"], torch.float16)
+    o = ops.sparse_layer_decode(dev(c4["q"], torch.float16), dev(c4["qi"], torch.float16), dev(c4["w"]),
+                                dev(c4["ki"], torch.float16), K, V, S, 32768, 4, ws)
+    if S > 1152:
+        sc = orc.index_scores(c4["qi"], c4["w"], c4["ki"][:S - 128])
+        sel = orc.select_keys(np.concatenate([sc, np.zeros(128, np.float32)]), S).astype(np.int32)
+    else:
+        sel = np.arange(S, dtype=np.int32)
+    ref = orc.decode_rows(synth.f16_val(c4["q"]), synth.f16_val(c4["K"]), synth.f16_val(c4["V"]), sel)
+    assert_close(f16_host(o), ref, what=f"S={S}")
