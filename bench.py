@@ -146,6 +146,40 @@ def bench_c4(torch, reps=20):
                 gbs=nbytes / (ms * 1e-3) / 1e9)
 
 
+def prefill_flops(p0: int, T: int, n_q: int = 16, window: int = 0) -> float:
+    """Algorithmic FLOPs of causal prefill attention: 4·128 a (query row, key) pair (QK and PV)."""
+    pairs = 0
+    for i in range(T):
+        n = p0 + i + 1
+        pairs += min(n, window) if window else n
+    return pairs * n_q * 4 * 128
+
+
+def bench_c5(torch, reps=10):
+    """Config C5 full layer: a 2048-token chunk after 30720 cached int8 positions: the fused
+    quantise-and-append + causal attention, and the attention alone."""
+    from embla_attn import ops
+    p0, T, max_s, n_kv = 30720, 2048, 32768, 4
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4)
+    nrow = n_kv * max_s * 128
+    kc = torch.empty(nrow + n_kv * max_s * 2, dtype=torch.uint8, device="cuda")
+    vc = torch.empty_like(kc)
+    for t in (kc, vc):
+        t[:nrow].random_(0, 256, generator=g)
+        t[nrow:].view(torch.float16).uniform_(0.005, 0.02, generator=g)
+    q = torch.randn(T, 16, 128, generator=g, device="cuda").bfloat16()
+    kn = torch.randn(T, n_kv, 128, generator=g, device="cuda").bfloat16()
+    vn = torch.randn(T, n_kv, 128, generator=g, device="cuda").bfloat16()
+    out = torch.empty(T, 16, 128, dtype=torch.bfloat16, device="cuda")
+    flops = prefill_flops(p0, T)
+    _, ms_fused = time_graph(torch, lambda: ops.prefill_full(q, kn, vn, kc, vc, T, p0, max_s, n_kv, out=out), reps, 2)
+    _, ms_attn = time_graph(torch, lambda: ops.prefill_int8(q, kc, vc, T, p0, max_s, n_kv, out=out), reps, 2)
+    return dict(gflop=flops / 1e9, ms_attention=ms_attn, tflops_attention=flops / (ms_attn * 1e-3) / 1e12,
+                mfma_util_attention=flops / (ms_attn * 1e-3) / 2.5e15, ms_fused=ms_fused,
+                tflops_fused=flops / (ms_fused * 1e-3) / 1e12, tokens_per_s=T / (ms_fused * 1e-3))
+
+
 def cpu_baseline(case, L, budget_s=10.0):
     """The C oracle (scalar fp32 restatement, one thread) on whole C3 layers at context L."""
     sys.path.insert(0, str(ROOT / "oracle"))
@@ -192,6 +226,7 @@ def main():
     res, case, out0, _ = bench_c3(torch, args.steps, args.warmup)
     c2 = bench_c2(torch)
     c4 = bench_c4(torch)
+    c5 = bench_c5(torch)
     head = res[L]
     line = {
         "metric": METRIC,
@@ -224,6 +259,7 @@ def main():
         "c3_sweep_gbs": {str(k): round(v["gbs"], 1) for k, v in res.items()},
         "c2_sliding": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in c2.items()},
         "c4_sparse": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in c4.items()},
+        "c5_prefill_full": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c5.items()},
     }
     if not args.no_cpu:
         cb, ref = cpu_baseline(case, L)

@@ -275,4 +275,37 @@ int embla_sparse_layer_decode(const void* q, const void* qi, const float* w, con
     return embla_sparse_decode(q, kc, vc, idx, 0, kTopK + kRecent, o, max_s, n_q, n_kv, dtype, 0, aws, abytes, stream);
 }
 
+int embla_prefill_int8(const void* q, int q_dtype, long q_tok_stride, long q_head_stride, const void* kc,
+                       const void* vc, void* o, int o_dtype, long o_tok_stride, long o_head_stride, int T, int p0,
+                       int max_s, int n_q, int n_kv, int weights, int scale_dtype, int window, hipStream_t stream) {
+    if (!q || !kc || !vc || !o || T <= 0 || p0 < 0 || max_s <= 0 || max_s % 32 || p0 + T > max_s) return EMBLA_ERR_INVALID;
+    if (!valid_act(q_dtype) || !valid_act(o_dtype) || !valid_scale(scale_dtype) || window < 0) return EMBLA_ERR_INVALID;
+    if (weights != EMBLA_SOFTMAX && weights != EMBLA_RELU2_SINK) return EMBLA_ERR_INVALID;
+    if (n_kv <= 0 || n_q % n_kv) return EMBLA_ERR_INVALID;
+    PrefillArgs a;
+    a.q = (const uint16_t*)q; a.q_tok_stride = q_tok_stride; a.q_head_stride = q_head_stride;
+    a.kc = (const int8_t*)kc; a.vc = (const int8_t*)vc;
+    a.o = (uint16_t*)o; a.o_tok_stride = o_tok_stride; a.o_head_stride = o_head_stride;
+    a.T = T; a.p0 = p0; a.max_s = max_s; a.n_q = n_q; a.n_kv = n_kv; a.window = window;
+    a.relu2 = weights == EMBLA_RELU2_SINK; a.scale32 = scale_dtype == EMBLA_F32;
+    a.q_bf16 = q_dtype == EMBLA_BF16; a.out_bf16 = o_dtype == EMBLA_BF16;
+    return launch_prefill_int8(a, stream);
+}
+
+int embla_prefill_full(const void* q, const void* k, const void* v, void* kc, void* vc, void* o, int T, int p0,
+                       int max_s, int n_q, int n_kv, hipStream_t stream) {
+    int rc = embla_kv_quant_append(k, v, EMBLA_BF16, n_kv * 128, T, p0, n_kv, kc, vc, max_s, EMBLA_F16, 0, stream);
+    if (rc) return rc;
+    return embla_prefill_int8(q, EMBLA_BF16, (long)n_q * 128, 128, kc, vc, o, EMBLA_BF16, (long)n_q * 128, 128, T,
+                              p0, max_s, n_q, n_kv, EMBLA_SOFTMAX, EMBLA_F16, 0, stream);
+}
+
+int embla_relu2_prefill(const void* qn, const void* kc, const void* vc, void* o, int Tq, int Tk, int maxS,
+                        hipStream_t stream) {
+    if (Tk < Tq) return EMBLA_ERR_INVALID;
+    // q [16][Tq][128] head-major (q_prep_b), out token-major [Tq][2048] (attn_nax.metal:358)
+    return embla_prefill_int8(qn, EMBLA_BF16, 128, (long)Tq * 128, kc, vc, o, EMBLA_BF16, 2048, 128, Tq, Tk - Tq,
+                              maxS, 16, 2, EMBLA_RELU2_SINK, EMBLA_F32, 0, stream);
+}
+
 }  // extern "C"

@@ -52,6 +52,18 @@ struct SparseArgs {
 int launch_sparse_decode(const SparseArgs& a, hipStream_t st);
 int launch_select_topk(const float* scores, int score_stride, uint32_t* idx, int idx_stride, int S, int n_sets,
                        int topk, int recent, hipStream_t st);
+struct PrefillArgs {
+    const uint16_t* q;       // row (token t, head h) at q + t * q_tok_stride + h * q_head_stride
+    long q_tok_stride, q_head_stride;
+    const int8_t* kc;        // int8 regions (tiles, then scales)
+    const int8_t* vc;
+    uint16_t* o;             // row (t, h) at o + t * o_tok_stride + h * o_head_stride
+    long o_tok_stride, o_head_stride;
+    int T, p0, max_s, n_q, n_kv, window;
+    bool relu2, scale32, q_bf16, out_bf16;
+};
+int launch_prefill_int8(const PrefillArgs& a, hipStream_t st);
+
 int launch_index_scores(const uint16_t* qi, const float* w, const uint16_t* ki, float* scores, int n, int n_ih,
                         hipStream_t st);
 

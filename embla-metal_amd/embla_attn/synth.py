@@ -85,3 +85,19 @@ def sparse_case(seed: int, ctx: int, n_q: int = 16, n_kv: int = 4, n_ih: int = 4
     K = f16_bits(g.normal(n_kv * ctx * 128)).reshape(n_kv, ctx, 128)
     V = f16_bits(g.normal(n_kv * ctx * 128)).reshape(n_kv, ctx, 128)
     return dict(qi=qi, w=w, ki=ki, q=q, K=K, V=V, S=ctx, n_q=n_q, n_kv=n_kv)
+
+
+def prefill_case(seed: int, p0: int, T: int, n_q: int = 16, n_kv: int = 4, lo: float = 0.005,
+                 hi: float = 0.02) -> dict:
+    """Config C5: an int8 prefix of p0 positions (K, V int8 U{-127..127}, fp16 scales U[lo, hi],
+    as C3) and a chunk of T tokens: bf16 Q [T][n_q][128], K, V [T][n_kv][128] drawn from N(0,1).
+    Draw order: prefix K, K scales, V, V scales, then Q, K, V of the chunk."""
+    g = SplitMix64(seed)
+    K = g.int8(n_kv * p0 * 128).reshape(n_kv, p0, 128)
+    ks = f16_bits(lo + (hi - lo) * g.uniform(n_kv * p0)).reshape(n_kv, p0)
+    V = g.int8(n_kv * p0 * 128).reshape(n_kv, p0, 128)
+    vs = f16_bits(lo + (hi - lo) * g.uniform(n_kv * p0)).reshape(n_kv, p0)
+    q = bf16_bits(g.normal(T * n_q * 128).astype(np.float32)).reshape(T, n_q, 128)
+    kn = bf16_bits(g.normal(T * n_kv * 128).astype(np.float32)).reshape(T, n_kv, 128)
+    vn = bf16_bits(g.normal(T * n_kv * 128).astype(np.float32)).reshape(T, n_kv, 128)
+    return dict(K=K, ks=ks, V=V, vs=vs, q=q, kn=kn, vn=vn, p0=p0, T=T, n_q=n_q, n_kv=n_kv)

@@ -146,6 +146,28 @@ int embla_sparse_layer_decode(const void* q, const void* qi, const float* w, con
                               const void* vc, void* o, int S, int max_s, int n_q, int n_kv, int n_ih, int dtype,
                               void* ws, size_t ws_bytes, hipStream_t stream);
 
+/* ---------------------------------------------------------------- batched prefill, int8 cache
+ * T tokens at positions p0 .. p0+T-1 attend keys 0 .. their position (window > 0: only the last
+ * `window` positions, the own one included) of an int8 layer cache that already holds them.
+ * Query row (t, h) at q + t * q_tok_stride + h * q_head_stride (elements, q_dtype), output row at
+ * o + t * o_tok_stride + h * o_head_stride (o_dtype). weights: EMBLA_SOFTMAX, or EMBLA_RELU2_SINK
+ * (threshold 0, sink sqrt(128), as relu2_prefill_nax, attn_nax.metal:61-364). n_q / n_kv in {4, 8}. */
+int embla_prefill_int8(const void* q, int q_dtype, long q_tok_stride, long q_head_stride, const void* kc,
+                       const void* vc, void* o, int o_dtype, long o_tok_stride, long o_head_stride, int T, int p0,
+                       int max_s, int n_q, int n_kv, int weights, int scale_dtype, int window, hipStream_t stream);
+
+/* Full-layer prefill chunk (config C5 full): the chunk's bf16 K and V [T][n_kv][128] quantised into
+ * the int8 cache (fp16 per-token absmax scales) at p0 .., then causal softmax attention of the bf16
+ * queries [T][n_q][128] over keys 0 .. p0 + t; o bf16 [T][n_q][128]. Two launches. */
+int embla_prefill_full(const void* q, const void* k, const void* v, void* kc, void* vc, void* o, int T, int p0,
+                       int max_s, int n_q, int n_kv, hipStream_t stream);
+
+/* Reference-signature relu2_prefill_nax (attn_nax.metal:61-364, bound at Prefill.swift:389-406):
+ * qn bf16 [16][Tq][128] from q_prep_b, the int8 cache of 2 kv heads (fp32 scales), keys 0 .. Tk-1,
+ * the chunk being the last Tq of them; out bf16 token-major [Tq][2048]. */
+int embla_relu2_prefill(const void* qn, const void* kc, const void* vc, void* o, int Tq, int Tk, int maxS,
+                        hipStream_t stream);
+
 /* ---------------------------------------------------------------- quantise-and-append
  * T new positions p0 .. p0+T-1 of K and V rows into an int8 layer cache (write_row8,
  * common.metal:72-84; kv_append / kv_append_b, attention.metal:113-140, prefill.metal:182-212):

@@ -1,0 +1,111 @@
+"""Batched prefill over the int8 cache (config C5 full layer; the reference's relu2_prefill_nax)
+against the oracle: whole small chunks, and sampled rows of the full-size chunk (prefill row i
+equals decode at position p0 + i, Prefill.swift:10-13)."""
+import numpy as np
+import pytest
+
+from conftest import gpu_available
+from gpu_util import assert_close, bf16_host, dev, say
+from embla_attn import layout, synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch_gpu():
+    if not gpu_available():
+        pytest.skip("no GPU")
+    import torch
+    return torch
+
+
+def quant_rows(orc, x):   # [n][128] float -> int8, fp32 scale
+    q = np.empty(x.shape, np.int8)
+    s = np.empty(x.shape[0], np.float32)
+    for i in range(x.shape[0]):
+        q[i], s[i] = orc.quant_row(x[i], round_bf=True)
+    return q, s
+
+
+def cache_after_chunk(orc, c):
+    """The logical int8 cache after the chunk's quantise-and-append (fp16 scales), as the oracle
+    defines it."""
+    n_kv, p0, T = c["n_kv"], c["p0"], c["T"]
+    K = np.concatenate([c["K"], np.zeros((n_kv, T, 128), np.int8)], 1)
+    V = np.concatenate([c["V"], np.zeros((n_kv, T, 128), np.int8)], 1)
+    ks = np.concatenate([synth.f16_val(c["ks"]), np.zeros((n_kv, T), np.float32)], 1)
+    vs = np.concatenate([synth.f16_val(c["vs"]), np.zeros((n_kv, T), np.float32)], 1)
+    for h in range(n_kv):
+        qk, sk = quant_rows(orc, synth.bf16_val(c["kn"][:, h]))
+        qv, sv = quant_rows(orc, synth.bf16_val(c["vn"][:, h]))
+        K[h, p0:], V[h, p0:] = qk, qv
+        ks[h, p0:] = synth.f16_val(synth.f16_bits(sk))
+        vs[h, p0:] = synth.f16_val(synth.f16_bits(sv))
+    return K, ks, V, vs
+
+
+def upload_prefix(c, max_s):
+    kc = dev(layout.pack_region(c["K"], c["ks"], max_s, "k"))
+    vc = dev(layout.pack_region(c["V"], c["vs"], max_s, "v"))
+    return kc, vc
+
+
+@pytest.mark.parametrize("p0,T,window", [(1000, 96, 0), (0, 64, 0), (517, 70, 0), (300, 100, 40), (40, 33, 0)])
+def test_prefill_full_small(torch_gpu, orc, p0, T, window):
+    """Fused quantise-and-append + causal softmax prefill vs the oracle on every row."""
+    from embla_attn import ops
+    torch = torch_gpu
+    say(f"prefill small p0={p0} T={T} window={window}")
+    c = synth.prefill_case(seed=4, p0=p0, T=T)
+    max_s = ((p0 + T + 31) // 32) * 32
+    kc, vc = upload_prefix(c, max_s)
+    q = dev(c["q"], torch.bfloat16)
+    if window == 0:
+        o = ops.prefill_full(q, dev(c["kn"], torch.bfloat16), dev(c["vn"], torch.bfloat16), kc, vc, T, p0, max_s, 4)
+    else:
+        ops.kv_quant_append(dev(c["kn"], torch.bfloat16), dev(c["vn"], torch.bfloat16), T, p0, 4, kc, vc, max_s)
+        o = ops.prefill_int8(q, kc, vc, T, p0, max_s, 4, window=window)
+    K, ks, V, vs = cache_after_chunk(orc, c)
+    ref = orc.prefill_int8(synth.bf16_val(c["q"]), K, ks, V, vs, p0, weights=0, window=window)
+    assert_close(bf16_host(o), ref, what=f"p0={p0} T={T} w={window}")
+
+
+def test_prefill_c5_full_size_sampled_rows(torch_gpu, orc):
+    """Config C5 at full size (T = 2048 after 30720 cached), rows checked against decode-at-position."""
+    from embla_attn import ops
+    torch = torch_gpu
+    p0, T, max_s = 30720, 2048, 32768
+    say("prefill C5 full size")
+    c = synth.prefill_case(seed=4, p0=p0, T=T)
+    kc, vc = upload_prefix(c, max_s)
+    o = ops.prefill_full(dev(c["q"], torch.bfloat16), dev(c["kn"], torch.bfloat16), dev(c["vn"], torch.bfloat16),
+                         kc, vc, T, p0, max_s, 4)
+    got = bf16_host(o)
+    K, ks, V, vs = cache_after_chunk(orc, c)
+    # the chunk's int8 bytes are bit-exact with the oracle's quantisation
+    Kr, Ks = layout.unpack_region(kc.cpu().numpy(), 4, max_s, "k", np.uint16)
+    np.testing.assert_array_equal(Kr[:, p0:], K[:, p0:])
+    for i in (0, 1, 31, 32, 777, 1500, 2046, 2047):
+        pos = p0 + i
+        ref = orc.decode_int8(synth.bf16_val(c["q"][i]), K[:, :pos + 1], ks[:, :pos + 1], V[:, :pos + 1], vs[:, :pos + 1])
+        assert_close(got[i], ref, what=f"row {i}")
+
+
+def test_relu2_prefill_reference_mode(torch_gpu, orc):
+    """relu2_prefill_nax: q [16][Tq][128] head-major, 2 kv heads, fp32 scales, ReLU² with sink."""
+    from embla_attn import ops
+    torch = torch_gpu
+    Tq, Tk, maxS = 80, 600, 640
+    say("relu2 prefill reference")
+    g = synth.SplitMix64(44)
+    K = g.int8(2 * Tk * 128).reshape(2, Tk, 128)
+    V = g.int8(2 * Tk * 128).reshape(2, Tk, 128)
+    ks = (0.02 + 0.02 * g.uniform(2 * Tk)).astype(np.float32).reshape(2, Tk)
+    vs = (0.02 + 0.02 * g.uniform(2 * Tk)).astype(np.float32).reshape(2, Tk)
+    qn = synth.bf16_bits((g.normal(16 * Tq * 128) * 2).astype(np.float32)).reshape(16, Tq, 128)
+    kc = dev(layout.pack_region(K, ks, maxS, "k"))
+    vc = dev(layout.pack_region(V, vs, maxS, "v"))
+    o = ops.relu2_prefill(dev(qn, torch.bfloat16), kc, vc, Tq, Tk, maxS)
+    got = bf16_host(o).reshape(Tq, 16, 128)
+    ref = orc.prefill_int8(synth.bf16_val(qn).transpose(1, 0, 2), K, ks, V, vs, Tk - Tq, weights=1)
+    assert_close(got, ref, what="relu2 prefill")
