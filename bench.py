@@ -173,8 +173,9 @@ def bench_c5(torch, reps=10):
     vn = torch.randn(T, n_kv, 128, generator=g, device="cuda").bfloat16()
     out = torch.empty(T, 16, 128, dtype=torch.bfloat16, device="cuda")
     flops = prefill_flops(p0, T)
-    _, ms_fused = time_graph(torch, lambda: ops.prefill_full(q, kn, vn, kc, vc, T, p0, max_s, n_kv, out=out), reps, 2)
-    _, ms_attn = time_graph(torch, lambda: ops.prefill_int8(q, kc, vc, T, p0, max_s, n_kv, out=out), reps, 2)
+    ws = ops.PrefillWorkspace(T, 16)
+    _, ms_fused = time_graph(torch, lambda: ops.prefill_full(q, kn, vn, kc, vc, T, p0, max_s, n_kv, out=out, ws=ws), reps, 2)
+    _, ms_attn = time_graph(torch, lambda: ops.prefill_int8(q, kc, vc, T, p0, max_s, n_kv, out=out, ws=ws), reps, 2)
     return dict(gflop=flops / 1e9, ms_attention=ms_attn, tflops_attention=flops / (ms_attn * 1e-3) / 1e12,
                 mfma_util_attention=flops / (ms_attn * 1e-3) / 2.5e15, ms_fused=ms_fused,
                 tflops_fused=flops / (ms_fused * 1e-3) / 1e12, tokens_per_s=T / (ms_fused * 1e-3))

@@ -15,7 +15,8 @@ constexpr int kMaxKV = 16;
 constexpr int kPartStride = 132;
 constexpr int kRefWindow = 128;         // the reference's sliding window (Engine.swift:9)
 constexpr int kRefRing = 4096;          // the reference's ring (attention.metal:6)
-constexpr int kTopK = 1024, kRecent = 128;   // Engine.swift:9 (topk, recent)        // floats a (chunk, query head) partial: acc[128], m, l, pad
+constexpr int kTopK = 1024, kRecent = 128;   // Engine.swift:9 (topk, recent)
+constexpr int kPrefillSplits = 2;       // key-range splits of a prefill chunk (two waves a SIMD)        // floats a (chunk, query head) partial: acc[128], m, l, pad
 
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
@@ -275,9 +276,15 @@ int embla_sparse_layer_decode(const void* q, const void* qi, const float* w, con
     return embla_sparse_decode(q, kc, vc, idx, 0, kTopK + kRecent, o, max_s, n_q, n_kv, dtype, 0, aws, abytes, stream);
 }
 
+size_t embla_prefill_workspace_bytes(int T, int n_q) {
+    if (T <= 0 || n_q <= 0) return 0;
+    return (size_t)kPrefillSplits * T * n_q * kPartStride * 4;
+}
+
 int embla_prefill_int8(const void* q, int q_dtype, long q_tok_stride, long q_head_stride, const void* kc,
                        const void* vc, void* o, int o_dtype, long o_tok_stride, long o_head_stride, int T, int p0,
-                       int max_s, int n_q, int n_kv, int weights, int scale_dtype, int window, hipStream_t stream) {
+                       int max_s, int n_q, int n_kv, int weights, int scale_dtype, int window, void* ws,
+                       size_t ws_bytes, hipStream_t stream) {
     if (!q || !kc || !vc || !o || T <= 0 || p0 < 0 || max_s <= 0 || max_s % 32 || p0 + T > max_s) return EMBLA_ERR_INVALID;
     if (!valid_act(q_dtype) || !valid_act(o_dtype) || !valid_scale(scale_dtype) || window < 0) return EMBLA_ERR_INVALID;
     if (weights != EMBLA_SOFTMAX && weights != EMBLA_RELU2_SINK) return EMBLA_ERR_INVALID;
@@ -287,17 +294,23 @@ int embla_prefill_int8(const void* q, int q_dtype, long q_tok_stride, long q_hea
     a.kc = (const int8_t*)kc; a.vc = (const int8_t*)vc;
     a.o = (uint16_t*)o; a.o_tok_stride = o_tok_stride; a.o_head_stride = o_head_stride;
     a.T = T; a.p0 = p0; a.max_s = max_s; a.n_q = n_q; a.n_kv = n_kv; a.window = window;
+    // two key-range splits when a workspace is given and the blocks are too few to fill the GPU
+    // with two waves a SIMD (the split partials cost one merge pass)
+    const int blocks = (T + 31) / 32 * n_kv;
+    a.nsplit = ws && ws_bytes >= embla_prefill_workspace_bytes(T, n_q) && blocks < 512 && p0 + T > 2048
+                   ? kPrefillSplits : 1;
+    a.part = (float*)ws;
     a.relu2 = weights == EMBLA_RELU2_SINK; a.scale32 = scale_dtype == EMBLA_F32;
     a.q_bf16 = q_dtype == EMBLA_BF16; a.out_bf16 = o_dtype == EMBLA_BF16;
     return launch_prefill_int8(a, stream);
 }
 
 int embla_prefill_full(const void* q, const void* k, const void* v, void* kc, void* vc, void* o, int T, int p0,
-                       int max_s, int n_q, int n_kv, hipStream_t stream) {
+                       int max_s, int n_q, int n_kv, void* ws, size_t ws_bytes, hipStream_t stream) {
     int rc = embla_kv_quant_append(k, v, EMBLA_BF16, n_kv * 128, T, p0, n_kv, kc, vc, max_s, EMBLA_F16, 0, stream);
     if (rc) return rc;
     return embla_prefill_int8(q, EMBLA_BF16, (long)n_q * 128, 128, kc, vc, o, EMBLA_BF16, (long)n_q * 128, 128, T,
-                              p0, max_s, n_q, n_kv, EMBLA_SOFTMAX, EMBLA_F16, 0, stream);
+                              p0, max_s, n_q, n_kv, EMBLA_SOFTMAX, EMBLA_F16, 0, ws, ws_bytes, stream);
 }
 
 int embla_relu2_prefill(const void* qn, const void* kc, const void* vc, void* o, int Tq, int Tk, int maxS,
@@ -305,7 +318,7 @@ int embla_relu2_prefill(const void* qn, const void* kc, const void* vc, void* o,
     if (Tk < Tq) return EMBLA_ERR_INVALID;
     // q [16][Tq][128] head-major (q_prep_b), out token-major [Tq][2048] (attn_nax.metal:358)
     return embla_prefill_int8(qn, EMBLA_BF16, 128, (long)Tq * 128, kc, vc, o, EMBLA_BF16, 2048, 128, Tq, Tk - Tq,
-                              maxS, 16, 2, EMBLA_RELU2_SINK, EMBLA_F32, 0, stream);
+                              maxS, 16, 2, EMBLA_RELU2_SINK, EMBLA_F32, 0, nullptr, 0, stream);
 }
 
 }  // extern "C"

@@ -60,6 +60,8 @@ struct PrefillArgs {
     uint16_t* o;             // row (t, h) at o + t * o_tok_stride + h * o_head_stride
     long o_tok_stride, o_head_stride;
     int T, p0, max_s, n_q, n_kv, window;
+    int nsplit;              // key-range splits (> 1: partial rows in part, then a merge)
+    float* part;             // [nsplit][T][n_q][132]
     bool relu2, scale32, q_bf16, out_bf16;
 };
 int launch_prefill_int8(const PrefillArgs& a, hipStream_t st);

@@ -12,11 +12,14 @@
 // query rows as MFMA columns: lane (row r = l % 32, half h = l / 32) then holds one query row's 16
 // scores a 32-key block, so the online softmax state (m, l) and the output O^T rows live in that
 // lane: the row maximum needs one cross-lane step (xor 32) and rescaling O needs none. O^T += V^T·P^T
-// takes P^T straight from the score registers (its k-slots match the score items) and V^T from
-// LDS, where V is staged transposed. K and V tiles are double-buffered in LDS: the next 64 keys'
+// takes P^T straight from the score registers (its k-slots are chosen to match the score items)
+// and V^T from LDS, where V is staged as an fp16 copy of its global lane-order tile, which already
+// holds 8 keys of one dim contiguous. K and V tiles are double-buffered in LDS: the next 64 keys'
 // global loads are in flight while the current ones are multiplied.
 #include "common.hpp"
 #include "embla_internal.hpp"
+
+#include <type_traits>
 
 namespace embla {
 
@@ -24,20 +27,26 @@ typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 
 constexpr int PBK = 64;            // keys a staged tile
 constexpr int KROW = HD + 8;       // LDS row stride of K (fp16 elements): conflict-free 16 B reads
-constexpr int VROW = PBK + 8;      // LDS row stride of V^T
+// V is staged as an fp16 copy of its global tile order: a 32-key tile is 8 rows u (dim % 8) of 64
+// lane slots (n + 16g) of 16 bytes, each slot the 8 keys {16t + 4g + i} of dim 8n + u. Rows are
+// padded by 16 bytes so the A-operand reads (8 lanes, rows u = 0..7) hit distinct banks.
+constexpr int VUROW = 64 * 8 + 8;  // fp16 elements a padded row u
+constexpr int VTILE = 8 * VUROW;   // fp16 elements a staged 32-key V tile
 
 __device__ __forceinline__ f16_t mfma32(h8v a, h8v b, f16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-struct PrefillSmem {
+struct __attribute__((aligned(16))) PrefillSmem {
     _Float16 k[2][PBK * KROW];
-    _Float16 vt[2][HD * VROW];
+    _Float16 vt[2][2 * VTILE];
     float ks[2][PBK], vs[2][PBK];
 };
 
+constexpr int PPS = HD + 4;        // floats a split partial row: O[128], m, l, pad
+
 template <int GQ, bool RELU2, bool SCALE32, bool QBF, bool OBF>
-__global__ __launch_bounds__(64 * GQ) void prefill_int8_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(64 * GQ, 2) void prefill_int8_kernel(PrefillArgs a) {
     constexpr int NT = 64 * GQ;
     __shared__ PrefillSmem sm;
     const int tb = blockIdx.x, kvh = blockIdx.y;
@@ -51,9 +60,14 @@ __global__ __launch_bounds__(64 * GQ) void prefill_int8_kernel(PrefillArgs a) {
     const int hi = a.p0 + last_tok;                            // last key the block needs
     int lo = 0;
     if (a.window > 0) lo = max(0, a.p0 + tok0 - a.window + 1);
-    const int kstart = lo & ~(PBK - 1);
-    const int ntiles = (hi - kstart) / PBK + 1;
+    const int kfirst = lo & ~(PBK - 1);
+    const int ntot = (hi - kfirst) / PBK + 1;
+    // split z of nsplit takes an equal share of the block's key tiles (the prefix splits evenly)
+    const int z = blockIdx.z, t_lo = ntot * z / a.nsplit, t_hi = ntot * (z + 1) / a.nsplit;
+    const int kstart = kfirst + t_lo * PBK;
+    const int ntiles = t_hi - t_lo;
 
+    const float c = RELU2 ? 0.08838834764831845f : 0.08838834764831845f * 1.4426950408889634f;
     const size_t nrow = (size_t)a.n_kv * a.max_s * HD;
     const char* ksb = (const char*)(a.kc + nrow);
     const char* vsb = (const char*)(a.vc + nrow);
@@ -91,23 +105,18 @@ __global__ __launch_bounds__(64 * GQ) void prefill_int8_kernel(PrefillArgs a) {
                 *(h8_t*)(sm.k[b] + key * KROW + d0) = lo8;
                 *(h8_t*)(sm.k[b] + key * KROW + d0 + 8) = hi8;
             }
-            // V piece (j, l): dims 8 (l % 16) + 2j + {0, 1}, each with keys {16t + 4 (l / 16) + i}
+            // V piece (j, l): rows u = 2j, 2j + 1 of slot l, 8 keys each: straight copies as fp16
             {
-                const int n = l & 15, g = l >> 4;
-#pragma unroll
-                for (int uu = 0; uu < 2; uu++) {
-                    const h8_t v8 = i8x8_to_h8(vr[i][2 * uu], vr[i][2 * uu + 1]);   // items e = 4t + i
-                    const int dim = 8 * n + 2 * j + uu;
-                    _Float16* row = sm.vt[b] + dim * VROW + 32 * gt + 4 * g;
-                    *(h4_t*)(row) = (h4_t){v8[0], v8[1], v8[2], v8[3]};
-                    *(h4_t*)(row + 16) = (h4_t){v8[4], v8[5], v8[6], v8[7]};
-                }
+                _Float16* base = sm.vt[b] + gt * VTILE + l * 8;
+                *(h8_t*)(base + (2 * j) * VUROW) = i8x8_to_h8(vr[i][0], vr[i][1]);
+                *(h8_t*)(base + (2 * j + 1) * VUROW) = i8x8_to_h8(vr[i][2], vr[i][3]);
             }
         }
         if (tid < 2 * PBK) {
             const float v = SCALE32 ? __uint_as_float(sr) : h2f((uint16_t)sr);
-            if (tid < PBK) sm.ks[b][tid] = v;
-            else sm.vs[b][tid - PBK] = v;
+            // scores: scale_k * (1/sqrt(128)) [* log2 e]; weights: scale_v [* 64 into fp16's range]
+            if (tid < PBK) sm.ks[b][tid] = v * c;
+            else sm.vs[b][tid - PBK] = RELU2 ? v : v * 64.0f;
         }
     };
 
@@ -121,8 +130,6 @@ __global__ __launch_bounds__(64 * GQ) void prefill_int8_kernel(PrefillArgs a) {
             qb[s] = QBF ? __builtin_bit_cast(h8v, bf8_to_h8(raw)) : __builtin_bit_cast(h8v, raw);
         }
     }
-    const float c = RELU2 ? 0.08838834764831845f : 0.08838834764831845f * 1.4426950408889634f;
-
     float m = NEG_INF, lsum = 0.0f;
     f16_t O[4];
 #pragma unroll
@@ -130,50 +137,68 @@ __global__ __launch_bounds__(64 * GQ) void prefill_int8_kernel(PrefillArgs a) {
 #pragma unroll
         for (int e = 0; e < 16; e++) O[i][e] = 0.0f;
 
-    gload(kstart);
-    sstore(0);
+    if (ntiles > 0) {
+        gload(kstart);
+        sstore(0);
+    }
     __syncthreads();
     for (int it = 0; it < ntiles; it++) {
         const int b = it & 1, k0 = kstart + it * PBK;
         if (it + 1 < ntiles) gload(k0 + PBK);   // in flight during this tile's products
         const bool full_tile = k0 + PBK - 1 <= a.p0 + tok0 && (a.window == 0 || k0 >= a.p0 + last_tok - a.window + 1);
+        // keys above kmax or at/below kmin are masked; a tile every row sees whole masks nothing
+        const int kmax = full_tile ? 0x7FFFFFFF : pos;
+        const int kmin = (full_tile || a.window == 0) ? -0x7FFFFFFF : pos - a.window;
+        auto run_block = [&](int kb) {
+            // S^T for keys k0 + 32kb + {8b + 4h + i}: the lane's 16 items e = 4b + i
+            const h8v* krow = (const h8v*)(sm.k[b] + (32 * kb + r) * KROW) + h;
+            f16_t st = mfma32(krow[0], qb[0], (f16_t){});
 #pragma unroll
-        for (int kb = 0; kb < 2; kb++) {
-            // S^T for keys k0 + 32kb + {8 (e / 4) + 4h + e % 4}: lane's 16 items
-            f16_t st;
-#pragma unroll
-            for (int e = 0; e < 16; e++) st[e] = 0.0f;
-#pragma unroll
-            for (int s = 0; s < 8; s++) {
-                const h8v kv = *(const h8v*)(sm.k[b] + (32 * kb + r) * KROW + 16 * s + 8 * h);
-                st = mfma32(kv, qb[s], st);
-            }
-            float x[16];
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const int kk = 32 * kb + 8 * (e >> 2) + 4 * h + (e & 3);
-                const int key = k0 + kk;
-                const bool ok = full_tile || (key <= pos && (a.window == 0 || key > pos - a.window));
-                x[e] = ok ? st[e] * sm.ks[b][kk] * c : NEG_INF;
-            }
-            h8v pb[2];   // P^T B operands of the two 16-key k-steps (items 8s .. 8s + 7)
+            for (int s = 1; s < 8; s++) st = mfma32(krow[2 * s], qb[s], st);
+            const f4_t* ks4 = (const f4_t*)(sm.ks[b] + 32 * kb + 4 * h);   // [2b]: keys 8b + 4h ..
+            const f4_t* vs4 = (const f4_t*)(sm.vs[b] + 32 * kb + 4 * h);
+            h8v pb[2];   // P^T B operands of the two 16-key k-steps: step s = items b = s, b = 2 + s
             if constexpr (RELU2) {
 #pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    const int kk = 32 * kb + 8 * (e >> 2) + 4 * h + (e & 3);
-                    const float t = fmaxf(x[e], 0.0f);
-                    const float p = x[e] == NEG_INF ? 0.0f : t * t;
-                    lsum += p;
-                    pb[e >> 3][e & 7] = (_Float16)(p * sm.vs[b][kk]);
+                for (int bb = 0; bb < 4; bb++) {
+                    const f4_t kq = ks4[2 * bb], vq = vs4[2 * bb];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int e = 4 * bb + i;
+                        const int key = k0 + 32 * kb + 8 * bb + 4 * h + i;
+                        const bool ok = key <= kmax && key > kmin;
+                        const float t = fmaxf(st[e] * kq[i], 0.0f);
+                        const float p = ok ? t * t : 0.0f;
+                        lsum += p;
+                        pb[bb & 1][((bb >> 1) << 2) | i] = (_Float16)(p * vq[i]);
+                    }
                 }
             } else {
-                float mt = NEG_INF;
+                float x[16];
 #pragma unroll
-                for (int e = 0; e < 16; e++) mt = fmaxf(mt, x[e]);
+                for (int bb = 0; bb < 4; bb++) {
+                    const f4_t kq = ks4[2 * bb];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        x[4 * bb + i] = st[4 * bb + i] * kq[i];
+                    }
+                }
+                if (!full_tile) {   // uniform: only the diagonal (and window-edge) tiles
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        const int key = k0 + 32 * kb + 8 * (e >> 2) + 4 * h + (e & 3);
+                        x[e] = key <= kmax && key > kmin ? x[e] : NEG_INF;
+                    }
+                }
+                float mt = fmaxf(x[0], x[1]);
+#pragma unroll
+                for (int e = 2; e < 16; e += 2) mt = fmaxf(mt, fmaxf(x[e], x[e + 1]));
                 mt = fmaxf(mt, shfl_xor(mt, 32));
-                const float mn = fmaxf(m, mt);
-                if (__any(mn > m)) {
-                    const float corr = m == NEG_INF ? 0.0f : exp2f(m - mn);
+                // the running maximum moves only when a row's grows by more than 2^8: weights stay
+                // <= 256 (fp16-safe after the 64 * scale_v prescale), O and l share the stale m
+                if (__any(mt > m + 8.0f)) {
+                    const float mn = fmaxf(m, mt);
+                    const float corr = m == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
                     lsum *= corr;
 #pragma unroll
                     for (int i = 0; i < 4; i++)
@@ -181,26 +206,35 @@ __global__ __launch_bounds__(64 * GQ) void prefill_int8_kernel(PrefillArgs a) {
                         for (int e = 0; e < 16; e++) O[i][e] *= corr;
                     m = mn;
                 }
+                // a masked key gives exp2(-inf) = 0; a row whose every key so far is masked keeps
+                // m = -inf: subtracting +inf instead keeps its weights 0 (not exp2(-inf + inf))
+                const float msub = m == NEG_INF ? -NEG_INF : m;
 #pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    const int kk = 32 * kb + 8 * (e >> 2) + 4 * h + (e & 3);
-                    const float p = x[e] == NEG_INF ? 0.0f : exp2f(x[e] - m);
-                    lsum += p;
-                    pb[e >> 3][e & 7] = (_Float16)(p * sm.vs[b][kk] * 64.0f);
+                for (int bb = 0; bb < 4; bb++) {
+                    const f4_t vq = vs4[2 * bb];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const float p = __builtin_amdgcn_exp2f(x[4 * bb + i] - msub);
+                        lsum += p;
+                        pb[bb & 1][((bb >> 1) << 2) | i] = (_Float16)(p * vq[i]);
+                    }
                 }
             }
-            // O^T (dims 32i + {8 (e / 4) + 4h + e % 4}) += V^T P^T over the two 16-key k-steps
+            // O^T (dims 32i + {8b + 4h + i}) += V^T P^T over two 16-key k-steps: in step s lane
+            // (dim 32i + r, h) takes slot (n = dim / 8, g = 2s + h) of row u = dim % 8, whose 8 keys
+            // {8s + 4h + i, 16 + 8s + 4h + i} are the P^T items b = s and b = 2 + s
+            const h8v* vt = (const h8v*)(sm.vt[b] + kb * VTILE);
 #pragma unroll
             for (int s = 0; s < 2; s++) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const _Float16* vrow = sm.vt[b] + (32 * i + r) * VROW + 32 * kb + 16 * s + 4 * h;
-                    const h4_t v0 = *(const h4_t*)vrow, v1 = *(const h4_t*)(vrow + 8);
-                    const h8v av = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-                    O[i] = mfma32(av, pb[s], O[i]);
+                    const int dim = 32 * i + r;
+                    O[i] = mfma32(vt[(dim & 7) * (VUROW / 8) + (dim >> 3) + 16 * (2 * s + h)], pb[s], O[i]);
                 }
             }
-        }
+        };
+        run_block(0);
+        run_block(1);
         if (it + 1 < ntiles) {
             __syncthreads();          // every wave is done with buffer b ^ 1 (its previous tile)
             sstore(b ^ 1);
@@ -211,7 +245,17 @@ __global__ __launch_bounds__(64 * GQ) void prefill_int8_kernel(PrefillArgs a) {
     // ---- normalise and store: lane (row r, half h) holds dims 32i + 8b + 4h .. + 3
     lsum += shfl_xor(lsum, 32);
     if (!row_ok) return;
-    const float inv = RELU2 ? 1.0f / (0.0f + (11.313708498984761f + lsum)) : 1.0f / (64.0f * lsum);
+    if (a.nsplit > 1) {   // this split's partial row: unnormalised O, m, l
+        float* pp = a.part + (((size_t)z * a.T + tok) * a.n_q + hq) * PPS;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int bb = 0; bb < 4; bb++)
+                *(f4_t*)(pp + 32 * i + 8 * bb + 4 * h) = (f4_t){O[i][4 * bb], O[i][4 * bb + 1], O[i][4 * bb + 2], O[i][4 * bb + 3]};
+        if (h == 0) { pp[HD] = m; pp[HD + 1] = lsum; }
+        return;
+    }
+    const float inv = RELU2 ? 1.0f / (11.313708498984761f + lsum) : 1.0f / (64.0f * lsum);
     uint16_t* orow = a.o + (size_t)tok * a.o_tok_stride + (size_t)hq * a.o_head_stride;
 #pragma unroll
     for (int i = 0; i < 4; i++)
@@ -225,9 +269,32 @@ __global__ __launch_bounds__(64 * GQ) void prefill_int8_kernel(PrefillArgs a) {
         }
 }
 
+/// Merges the nsplit partial rows of (token, head) = (blockIdx.x * 4 + wave, blockIdx.y): a wave
+/// a row, two dims a lane.
+template <bool RELU2, bool OBF>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
+    const int lane = threadIdx.x & 63, tok = blockIdx.x * 4 + (threadIdx.x >> 6), hq = blockIdx.y;
+    if (tok >= a.T) return;
+    float M = RELU2 ? 0.0f : NEG_INF;
+    if constexpr (!RELU2)
+        for (int z = 0; z < a.nsplit; z++) M = fmaxf(M, a.part[(((size_t)z * a.T + tok) * a.n_q + hq) * PPS + HD]);
+    float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+    for (int z = 0; z < a.nsplit; z++) {
+        const float* pp = a.part + (((size_t)z * a.T + tok) * a.n_q + hq) * PPS;
+        const float mz = pp[HD];
+        const float f = RELU2 ? 1.0f : (mz == NEG_INF ? 0.0f : exp2f(mz - M));
+        L += pp[HD + 1] * f;
+        o0 += pp[2 * lane] * f;
+        o1 += pp[2 * lane + 1] * f;
+    }
+    const float inv = RELU2 ? 1.0f / (11.313708498984761f + L) : 1.0f / (64.0f * L);
+    uint16_t* orow = a.o + (size_t)tok * a.o_tok_stride + (size_t)hq * a.o_head_stride;
+    *(uint32_t*)(orow + 2 * lane) = (uint32_t)f2a<OBF>(o0 * inv) | ((uint32_t)f2a<OBF>(o1 * inv) << 16);
+}
+
 int launch_prefill_int8(const PrefillArgs& a, hipStream_t st) {
     const int gq = a.n_q / a.n_kv;
-    const dim3 grid((a.T + 31) / 32, a.n_kv);
+    const dim3 grid((a.T + 31) / 32, a.n_kv, a.nsplit);
 #define EMBLA_PF(GQ, R, S32, QBF, OBF) \
     hipLaunchKernelGGL((prefill_int8_kernel<GQ, R, S32, QBF, OBF>), grid, dim3(64 * GQ), 0, st, a)
     if (gq == 4 && !a.relu2 && !a.scale32 && a.q_bf16 && a.out_bf16) EMBLA_PF(4, false, false, true, true);
@@ -236,6 +303,12 @@ int launch_prefill_int8(const PrefillArgs& a, hipStream_t st) {
     else if (gq == 8 && !a.relu2 && a.scale32 && a.q_bf16 && a.out_bf16) EMBLA_PF(8, false, true, true, true);
     else return EMBLA_ERR_UNSUPPORTED;
 #undef EMBLA_PF
+    if (a.nsplit > 1) {
+        const dim3 mg((a.T + 3) / 4, a.n_q);
+        if (a.relu2) hipLaunchKernelGGL((prefill_merge_kernel<true, true>), mg, dim3(256), 0, st, a);
+        else if (a.out_bf16) hipLaunchKernelGGL((prefill_merge_kernel<false, true>), mg, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((prefill_merge_kernel<false, false>), mg, dim3(256), 0, st, a);
+    }
     return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
 }
 

@@ -138,8 +138,18 @@ def sparse_layer_decode(q, qi, w, ki, kc, vc, S, max_s, n_kv, ws: SparseWorkspac
     return out
 
 
+class PrefillWorkspace:
+    def __init__(self, T: int, n_q: int = 16, device="cuda"):
+        self.nbytes = int(lib().embla_prefill_workspace_bytes(T, n_q))
+        self.buf = torch.empty(self.nbytes, dtype=torch.uint8, device=device)
+
+    @property
+    def ptr(self):
+        return _p(self.buf)
+
+
 def prefill_int8(q, kc, vc, T, p0, max_s, n_kv, weights=SOFTMAX, scale_dtype=F16, window=0, q_dtype=BF16,
-                 out_dtype=BF16, q_strides=None, out=None, out_strides=None, stream=None):
+                 out_dtype=BF16, q_strides=None, out=None, out_strides=None, ws=None, stream=None):
     """Prefill attention of T query rows over an int8 layer cache holding keys 0 .. p0 + T - 1."""
     n_q = q.shape[1] if q_strides is None else q.shape[0]
     qs = q_strides or (n_q * 128, 128)
@@ -147,16 +157,17 @@ def prefill_int8(q, kc, vc, T, p0, max_s, n_kv, weights=SOFTMAX, scale_dtype=F16
         out = torch.empty((T, n_q, 128), dtype=_DT[out_dtype], device=q.device)
     os_ = out_strides or (n_q * 128, 128)
     call("embla_prefill_int8", _p(q), q_dtype, qs[0], qs[1], _p(kc), _p(vc), _p(out), out_dtype, os_[0], os_[1], T, p0,
-         max_s, n_q, n_kv, weights, scale_dtype, window, stream_handle(stream))
+         max_s, n_q, n_kv, weights, scale_dtype, window, ws.ptr if ws else None, ws.nbytes if ws else 0,
+         stream_handle(stream))
     return out
 
 
-def prefill_full(q, k, v, kc, vc, T, p0, max_s, n_kv, out=None, stream=None):
+def prefill_full(q, k, v, kc, vc, T, p0, max_s, n_kv, out=None, ws=None, stream=None):
     n_q = q.shape[1]
     if out is None:
         out = torch.empty((T, n_q, 128), dtype=torch.bfloat16, device=q.device)
     call("embla_prefill_full", _p(q), _p(k), _p(v), _p(kc), _p(vc), _p(out), T, p0, max_s, n_q, n_kv,
-         stream_handle(stream))
+         ws.ptr if ws else None, ws.nbytes if ws else 0, stream_handle(stream))
     return out
 
 

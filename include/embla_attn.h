@@ -151,16 +151,22 @@ int embla_sparse_layer_decode(const void* q, const void* qi, const float* w, con
  * `window` positions, the own one included) of an int8 layer cache that already holds them.
  * Query row (t, h) at q + t * q_tok_stride + h * q_head_stride (elements, q_dtype), output row at
  * o + t * o_tok_stride + h * o_head_stride (o_dtype). weights: EMBLA_SOFTMAX, or EMBLA_RELU2_SINK
- * (threshold 0, sink sqrt(128), as relu2_prefill_nax, attn_nax.metal:61-364). n_q / n_kv in {4, 8}. */
+ * (threshold 0, sink sqrt(128), as relu2_prefill_nax, attn_nax.metal:61-364). n_q / n_kv in {4, 8}.
+ * ws (optional, embla_prefill_workspace_bytes(T, n_q)): lets the key range split in two (partial
+ * rows merged by a second launch) so the GPU holds two waves a SIMD; NULL: one pass. */
 int embla_prefill_int8(const void* q, int q_dtype, long q_tok_stride, long q_head_stride, const void* kc,
                        const void* vc, void* o, int o_dtype, long o_tok_stride, long o_head_stride, int T, int p0,
-                       int max_s, int n_q, int n_kv, int weights, int scale_dtype, int window, hipStream_t stream);
+                       int max_s, int n_q, int n_kv, int weights, int scale_dtype, int window, void* ws,
+                       size_t ws_bytes, hipStream_t stream);
+
+/* Bytes of the optional prefill workspace for T tokens and n_q query heads. */
+size_t embla_prefill_workspace_bytes(int T, int n_q);
 
 /* Full-layer prefill chunk (config C5 full): the chunk's bf16 K and V [T][n_kv][128] quantised into
  * the int8 cache (fp16 per-token absmax scales) at p0 .., then causal softmax attention of the bf16
- * queries [T][n_q][128] over keys 0 .. p0 + t; o bf16 [T][n_q][128]. Two launches. */
+ * queries [T][n_q][128] over keys 0 .. p0 + t; o bf16 [T][n_q][128]; ws as embla_prefill_int8. */
 int embla_prefill_full(const void* q, const void* k, const void* v, void* kc, void* vc, void* o, int T, int p0,
-                       int max_s, int n_q, int n_kv, hipStream_t stream);
+                       int max_s, int n_q, int n_kv, void* ws, size_t ws_bytes, hipStream_t stream);
 
 /* Reference-signature relu2_prefill_nax (attn_nax.metal:61-364, bound at Prefill.swift:389-406):
  * qn bf16 [16][Tq][128] from q_prep_b, the int8 cache of 2 kv heads (fp32 scales), keys 0 .. Tk-1,

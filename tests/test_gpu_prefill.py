@@ -50,21 +50,24 @@ def upload_prefix(c, max_s):
     return kc, vc
 
 
-@pytest.mark.parametrize("p0,T,window", [(1000, 96, 0), (0, 64, 0), (517, 70, 0), (300, 100, 40), (40, 33, 0)])
-def test_prefill_full_small(torch_gpu, orc, p0, T, window):
+@pytest.mark.parametrize("p0,T,window,split", [(1000, 96, 0, False), (0, 64, 0, False), (517, 70, 0, False),
+                                                (300, 100, 40, False), (40, 33, 0, False), (3000, 70, 0, True),
+                                                (2100, 64, 0, True), (2500, 40, 300, True)])
+def test_prefill_full_small(torch_gpu, orc, p0, T, window, split):
     """Fused quantise-and-append + causal softmax prefill vs the oracle on every row."""
     from embla_attn import ops
     torch = torch_gpu
-    say(f"prefill small p0={p0} T={T} window={window}")
+    say(f"prefill small p0={p0} T={T} window={window} split={split}")
     c = synth.prefill_case(seed=4, p0=p0, T=T)
     max_s = ((p0 + T + 31) // 32) * 32
     kc, vc = upload_prefix(c, max_s)
     q = dev(c["q"], torch.bfloat16)
+    ws = ops.PrefillWorkspace(T, 16) if split else None
     if window == 0:
-        o = ops.prefill_full(q, dev(c["kn"], torch.bfloat16), dev(c["vn"], torch.bfloat16), kc, vc, T, p0, max_s, 4)
+        o = ops.prefill_full(q, dev(c["kn"], torch.bfloat16), dev(c["vn"], torch.bfloat16), kc, vc, T, p0, max_s, 4, ws=ws)
     else:
         ops.kv_quant_append(dev(c["kn"], torch.bfloat16), dev(c["vn"], torch.bfloat16), T, p0, 4, kc, vc, max_s)
-        o = ops.prefill_int8(q, kc, vc, T, p0, max_s, 4, window=window)
+        o = ops.prefill_int8(q, kc, vc, T, p0, max_s, 4, window=window, ws=ws)
     K, ks, V, vs = cache_after_chunk(orc, c)
     ref = orc.prefill_int8(synth.bf16_val(c["q"]), K, ks, V, vs, p0, weights=0, window=window)
     assert_close(bf16_host(o), ref, what=f"p0={p0} T={T} w={window}")
@@ -79,7 +82,7 @@ def test_prefill_c5_full_size_sampled_rows(torch_gpu, orc):
     c = synth.prefill_case(seed=4, p0=p0, T=T)
     kc, vc = upload_prefix(c, max_s)
     o = ops.prefill_full(dev(c["q"], torch.bfloat16), dev(c["kn"], torch.bfloat16), dev(c["vn"], torch.bfloat16),
-                         kc, vc, T, p0, max_s, 4)
+                         kc, vc, T, p0, max_s, 4, ws=ops.PrefillWorkspace(T, 16))
     got = bf16_host(o)
     K, ks, V, vs = cache_after_chunk(orc, c)
     # the chunk's int8 bytes are bit-exact with the oracle's quantisation
