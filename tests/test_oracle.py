@@ -283,3 +283,23 @@ def test_tile_layout_is_a_permutation_matching_the_kernels_formula():
     rows = rng.integers(-127, 128, (2, 64, 128)).astype(np.int8)
     for kind in ("k", "v"):
         np.testing.assert_array_equal(layout.from_tiles(layout.to_tiles(rows, kind), 2, 64, kind), rows)
+
+
+def test_head_norm_vs_fp64(orc):
+    """head_norm (common.metal:13-26): x * (1 + g1) * (1 + g2) / sqrt(mean(x²) + 2^-23)."""
+    g = synth.SplitMix64(23)
+    for ng in (0, 1, 2):
+        x = synth.bf16_val(synth.bf16_bits(g.normal(128) * 4)).astype(np.float32)
+        g1 = synth.bf16_val(synth.bf16_bits(g.normal(128) * 0.3))
+        g2 = synth.bf16_val(synth.bf16_bits(g.normal(128) * 0.3))
+        got = orc.head_norm(x, g1, g2, ng, round_bf=False)
+        ref = x.astype(np.float64) / np.sqrt((x.astype(np.float64) ** 2).mean() + 1.1920929e-07)
+        if ng >= 1:
+            ref = ref * (1 + g1.astype(np.float64))
+        if ng >= 2:
+            ref = ref * (1 + g2.astype(np.float64))
+        np.testing.assert_allclose(got, ref, rtol=3e-6, atol=1e-6)
+        # rounding to bf16 is the RNE of the unrounded value
+        np.testing.assert_array_equal(orc.head_norm(x, g1, g2, ng, round_bf=True), synth.bf16_val(synth.bf16_bits(got)))
+    # a zero row stays zero (eps keeps the factor finite)
+    assert not orc.head_norm(np.zeros(128), None, None, 0).any()
