@@ -176,9 +176,20 @@ def bench_c5(torch, reps=10):
     ws = ops.PrefillWorkspace(T, 16)
     _, ms_fused = time_graph(torch, lambda: ops.prefill_full(q, kn, vn, kc, vc, T, p0, max_s, n_kv, out=out, ws=ws), reps, 2)
     _, ms_attn = time_graph(torch, lambda: ops.prefill_int8(q, kc, vc, T, p0, max_s, n_kv, out=out, ws=ws), reps, 2)
-    return dict(gflop=flops / 1e9, ms_attention=ms_attn, tflops_attention=flops / (ms_attn * 1e-3) / 1e12,
+    full = dict(gflop=flops / 1e9, ms_attention=ms_attn, tflops_attention=flops / (ms_attn * 1e-3) / 1e12,
                 mfma_util_attention=flops / (ms_attn * 1e-3) / 2.5e15, ms_fused=ms_fused,
                 tflops_fused=flops / (ms_fused * 1e-3) / 1e12, tokens_per_s=T / (ms_fused * 1e-3))
+    # sliding layer: the same chunk, window 1024, over a bf16 ring of 8192 (append + attention)
+    R, W = 8192, 1024
+    kring = torch.randn(n_kv * R * 128, generator=g, device="cuda").bfloat16()
+    vring = torch.randn(n_kv * R * 128, generator=g, device="cuda").bfloat16()
+    sflops = 4.0 * 128 * 16 * sum(min(W, p0 + t + 1) for t in range(T))
+    _, ms_sl = time_graph(torch, lambda: ops.prefill_sliding(q, kn, vn, kring, vring, T, p0, R, W, n_kv, out=out), reps, 2)
+    _, ms_sla = time_graph(torch, lambda: ops.prefill_ring(q, kring, vring, T, p0, R, W, n_kv, out=out), reps, 2)
+    sliding = dict(window=W, ring=R, gflop=sflops / 1e9, ms_attention=ms_sla,
+                   tflops_attention=sflops / (ms_sla * 1e-3) / 1e12, ms_fused=ms_sl,
+                   tokens_per_s=T / (ms_sl * 1e-3))
+    return dict(full, sliding=sliding)
 
 
 def cpu_baseline(case, L, budget_s=10.0):
@@ -260,7 +271,9 @@ def main():
         "c3_sweep_gbs": {str(k): round(v["gbs"], 1) for k, v in res.items()},
         "c2_sliding": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in c2.items()},
         "c4_sparse": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in c4.items()},
-        "c5_prefill_full": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c5.items()},
+        "c5_prefill_full": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c5.items()
+                            if k != "sliding"},
+        "c5_prefill_sliding": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c5["sliding"].items()},
     }
     if not args.no_cpu:
         cb, ref = cpu_baseline(case, L)

@@ -300,6 +300,7 @@ int embla_prefill_int8(const void* q, int q_dtype, long q_tok_stride, long q_hea
     a.nsplit = ws && ws_bytes >= embla_prefill_workspace_bytes(T, n_q) && blocks < 512 && p0 + T > 2048
                    ? kPrefillSplits : 1;
     a.part = (float*)ws;
+    a.kring = nullptr; a.vring = nullptr; a.R = 0; a.qg = nullptr;
     a.relu2 = weights == EMBLA_RELU2_SINK; a.scale32 = scale_dtype == EMBLA_F32;
     a.q_bf16 = q_dtype == EMBLA_BF16; a.out_bf16 = o_dtype == EMBLA_BF16;
     return launch_prefill_int8(a, stream);
@@ -319,6 +320,56 @@ int embla_relu2_prefill(const void* qn, const void* kc, const void* vc, void* o,
     // q [16][Tq][128] head-major (q_prep_b), out token-major [Tq][2048] (attn_nax.metal:358)
     return embla_prefill_int8(qn, EMBLA_BF16, 128, (long)Tq * 128, kc, vc, o, EMBLA_BF16, 2048, 128, Tq, Tk - Tq,
                               maxS, 16, 2, EMBLA_RELU2_SINK, EMBLA_F32, 0, nullptr, 0, stream);
+}
+
+int embla_ring_append(const void* k, const void* v, int dtype, int stride, int T, int p0, int n_kv, void* kring,
+                      void* vring, int ring, const void* kg, hipStream_t stream) {
+    if (!k || !v || !kring || !vring || T <= 0 || p0 < 0 || n_kv <= 0 || stride < n_kv * 128) return EMBLA_ERR_INVALID;
+    if (ring <= 0 || ring % 32 || T > ring || !valid_act(dtype)) return EMBLA_ERR_INVALID;
+    if (kg && dtype != EMBLA_BF16) return EMBLA_ERR_UNSUPPORTED;
+    RingAppendArgs a{(const uint16_t*)k, (const uint16_t*)v, stride, T, p0, n_kv, ring, (uint16_t*)kring,
+                     (uint16_t*)vring, (const uint16_t*)kg};
+    return launch_ring_append(a, stream);
+}
+
+int embla_prefill_ring(const void* q, int dtype, long q_tok_stride, long q_head_stride, const void* kring,
+                       const void* vring, int ring, void* o, long o_tok_stride, long o_head_stride, int T, int p0,
+                       int n_q, int n_kv, int window, const void* qg, void* ws, size_t ws_bytes, hipStream_t stream) {
+    if (!q || !kring || !vring || !o || T <= 0 || p0 < 0 || window <= 0 || !valid_act(dtype)) return EMBLA_ERR_INVALID;
+    if (ring <= 0 || ring % 32 || window - 1 + T > ring) return EMBLA_ERR_INVALID;   // the window and chunk fit the ring
+    if (n_kv <= 0 || n_q % n_kv) return EMBLA_ERR_INVALID;
+    if (qg && dtype != EMBLA_BF16) return EMBLA_ERR_UNSUPPORTED;
+    PrefillArgs a;
+    a.q = (const uint16_t*)q; a.q_tok_stride = q_tok_stride; a.q_head_stride = q_head_stride;
+    a.kc = nullptr; a.vc = nullptr;
+    a.o = (uint16_t*)o; a.o_tok_stride = o_tok_stride; a.o_head_stride = o_head_stride;
+    a.T = T; a.p0 = p0; a.max_s = ring; a.n_q = n_q; a.n_kv = n_kv; a.window = window;
+    const int blocks = (T + 31) / 32 * n_kv;
+    a.nsplit = ws && ws_bytes >= embla_prefill_workspace_bytes(T, n_q) && blocks < 512 && window > 2048
+                   ? kPrefillSplits : 1;
+    a.part = (float*)ws;
+    a.relu2 = false; a.scale32 = false; a.q_bf16 = dtype == EMBLA_BF16; a.out_bf16 = dtype == EMBLA_BF16;
+    a.kring = (const uint16_t*)kring; a.vring = (const uint16_t*)vring; a.R = ring; a.qg = (const uint16_t*)qg;
+    return launch_prefill_ring(a, stream);
+}
+
+int embla_prefill_sliding(const void* q, const void* k, const void* v, void* kring, void* vring, void* o, int T,
+                          int p0, int ring, int window, int n_q, int n_kv, void* ws, size_t ws_bytes,
+                          hipStream_t stream) {
+    int rc = embla_ring_append(k, v, EMBLA_BF16, n_kv * 128, T, p0, n_kv, kring, vring, ring, nullptr, stream);
+    if (rc) return rc;
+    return embla_prefill_ring(q, EMBLA_BF16, (long)n_q * 128, 128, kring, vring, ring, o, (long)n_q * 128, 128, T, p0,
+                              n_q, n_kv, window, nullptr, ws, ws_bytes, stream);
+}
+
+int embla_attn_sliding8_b(const void* qkv, const void* qg, const void* kg, void* kc, void* vc, void* o, int p0, int T,
+                          hipStream_t stream) {
+    if (!qkv || !qg || !kg) return EMBLA_ERR_INVALID;
+    const uint16_t* row = (const uint16_t*)qkv;
+    int rc = embla_ring_append(row + 16 * 128, row + 20 * 128, EMBLA_BF16, 4096, T, p0, 4, kc, vc, kRefRing, kg, stream);
+    if (rc) return rc;
+    return embla_prefill_ring(row, EMBLA_BF16, 4096, 128, kc, vc, kRefRing, o, 2048, 128, T, p0, 16, 4, kRefWindow, qg,
+                              nullptr, 0, stream);
 }
 
 }  // extern "C"

@@ -63,8 +63,14 @@ struct PrefillArgs {
     int nsplit;              // key-range splits (> 1: partial rows in part, then a merge)
     float* part;             // [nsplit][T][n_q][132]
     bool relu2, scale32, q_bf16, out_bf16;
+    // 16-bit ring source (kring/vring non-null): keys at slot p % R, no scales, MFMA in the ring's type
+    const uint16_t* kring;
+    const uint16_t* vring;
+    int R;
+    const uint16_t* qg;      // q pre-ops (norm with gains, RoPE, bf16), ring mode only; null: none
 };
 int launch_prefill_int8(const PrefillArgs& a, hipStream_t st);
+int launch_prefill_ring(const PrefillArgs& a, hipStream_t st);
 
 int launch_index_scores(const uint16_t* qi, const float* w, const uint16_t* ki, float* scores, int n, int n_ih,
                         hipStream_t st);
@@ -89,5 +95,15 @@ struct QPrepArgs {
     bool out_bf16;
 };
 int launch_q_prep(const QPrepArgs& a, hipStream_t st);
+
+struct RingAppendArgs {
+    const uint16_t* k;       // rows t at + t * stride, head h at + h * 128 (16-bit)
+    const uint16_t* v;
+    int stride, T, p0, n_kv, R;
+    uint16_t* kring;
+    uint16_t* vring;
+    const uint16_t* kg;      // gains: bf16 pre-ops on K (norm, RoPE); null: copy
+};
+int launch_ring_append(const RingAppendArgs& a, hipStream_t st);
 
 }  // namespace embla

@@ -100,6 +100,42 @@ __global__ __launch_bounds__(64) void q_prep_kernel(QPrepArgs a) {
     out[1] = a.out_bf16 ? f2bf(x1) : f2h(x1);
 }
 
+/// T positions p0 .. of 16-bit K and V rows into a ring (slot p % R, tile layout with ES = 2). With
+/// gains (the reference's sliding layers, kv_sliding_b, prefill.metal:103-125) K is RMS-normed with
+/// them, rotated (RoPE at its position) and rounded to bf16; V is copied. One wave a (token, head).
+__global__ __launch_bounds__(64) void ring_append_kernel(RingAppendArgs a) {
+    const int lane = threadIdx.x, t = blockIdx.x, h = blockIdx.y;
+    const int pos = a.p0 + t, slot = pos % a.R;
+    const uint32_t kraw = *(const uint32_t*)(a.k + (size_t)t * a.stride + h * HD + 2 * lane);
+    const uint32_t vraw = *(const uint32_t*)(a.v + (size_t)t * a.stride + h * HD + 2 * lane);
+    uint32_t kout = kraw;
+    if (a.kg) {   // bf16 rows with pre-ops
+        float x0 = bf2f(kraw & 0xFFFF), x1 = bf2f(kraw >> 16);
+        const float r = rms_factor(x0, x1);
+        x0 = x0 * (r * (1.0f + bf2f(a.kg[2 * lane])));
+        x1 = x1 * (r * (1.0f + bf2f(a.kg[2 * lane + 1])));
+        // RoPE: dims d and d + 32 (d < 32) rotate together; lane l holds 2l, 2l + 1
+        const float o0 = shfl_xor(x0, 16), o1 = shfl_xor(x1, 16);
+        if (lane < 32) {
+            const int d0 = (2 * lane) & 31;
+            float s0, c0, s1, c1;
+            sincosf(-(float)pos * (float)exp2(-(double)d0 / 32.0 * 13.287712379549449), &s0, &c0);
+            sincosf(-(float)pos * (float)exp2(-(double)(d0 + 1) / 32.0 * 13.287712379549449), &s1, &c1);
+            if (lane < 16) { x0 = x0 * c0 - o0 * s0; x1 = x1 * c1 - o1 * s1; }
+            else { x0 = o0 * s0 + x0 * c0; x1 = o1 * s1 + x1 * c1; }
+        }
+        kout = (uint32_t)f2bf(x0) | ((uint32_t)f2bf(x1) << 16);
+    }
+    *(uint32_t*)(a.kring + kt_off(h, a.R, slot, 2 * lane, 2) / 2) = kout;
+    a.vring[vt_off(h, a.R, slot, 2 * lane, 2) / 2] = (uint16_t)(vraw & 0xFFFF);
+    a.vring[vt_off(h, a.R, slot, 2 * lane + 1, 2) / 2] = (uint16_t)(vraw >> 16);
+}
+
+int launch_ring_append(const RingAppendArgs& a, hipStream_t st) {
+    hipLaunchKernelGGL(ring_append_kernel, dim3(a.T, a.n_kv), dim3(64), 0, st, a);
+    return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
+}
+
 int launch_q_prep(const QPrepArgs& a, hipStream_t st) {
     hipLaunchKernelGGL(q_prep_kernel, dim3(a.n_q, a.T), dim3(64), 0, st, a);
     return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;

@@ -36,6 +36,12 @@ constexpr int VTILE = 8 * VUROW;   // fp16 elements a staged 32-key V tile
 __device__ __forceinline__ f16_t mfma32(h8v a, h8v b, f16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
+/// 32x32x16 on 16-byte operands holding fp16 (BF = false) or bf16 (BF = true) values.
+template <bool BF>
+__device__ __forceinline__ f16_t mfma32x(u4_t a, u4_t b, f16_t c) {
+    if constexpr (BF) return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(b8_t, a), __builtin_bit_cast(b8_t, b), c, 0, 0, 0);
+    else return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, a), __builtin_bit_cast(h8v, b), c, 0, 0, 0);
+}
 
 struct __attribute__((aligned(16))) PrefillSmem {
     _Float16 k[2][PBK * KROW];
@@ -44,8 +50,11 @@ struct __attribute__((aligned(16))) PrefillSmem {
 };
 
 constexpr int PPS = HD + 4;        // floats a split partial row: O[128], m, l, pad
+int launch_prefill_tail(const PrefillArgs& a, hipStream_t st);
 
-template <int GQ, bool RELU2, bool SCALE32, bool QBF, bool OBF>
+// RING: K/V from a 16-bit ring (no scales; S = K·Q^T on the MFMA in the ring's type, BF = bf16;
+// V staged as fp16); else from an int8 region (fp16 MFMA). PRE: q normed with gains, rotated, bf16-rounded in-kernel.
+template <int GQ, bool RELU2, bool SCALE32, bool QBF, bool OBF, bool RING = false, bool BF = false, bool PRE = false>
 __global__ __launch_bounds__(64 * GQ, 2) void prefill_int8_kernel(PrefillArgs a) {
     constexpr int NT = 64 * GQ;
     __shared__ PrefillSmem sm;
@@ -73,63 +82,121 @@ __global__ __launch_bounds__(64 * GQ, 2) void prefill_int8_kernel(PrefillArgs a)
     const char* vsb = (const char*)(a.vc + nrow);
 
     // ---- staging: each thread moves 16-byte pieces of the two 32-key global tiles of a 64-key tile
-    constexpr int PIECES = 2 * 256;               // 16-byte pieces a 64-key tile, K (same for V)
+    constexpr int ES = RING ? 2 : 1;
+    constexpr int PIECES = 2 * 256 * ES;          // 16-byte pieces a 64-key tile, K (same for V)
     constexpr int PER = PIECES / NT;              // pieces a thread
     u4_t kr[PER], vr[PER];
     uint32_t sr = 0;                              // a scale (threads 0 .. 2*PBK-1)
+    auto tile_addr = [&](int key) -> size_t {     // byte offset of the 32-key tile holding key
+        if constexpr (RING) return tile_base(kvh, a.R, key % a.R, 2);
+        // a 64-key tile's second half may lie past max_s (max_s % 64 == 32): read the first
+        // half again; those keys are past every row's position and masked
+        else return tile_base(kvh, a.max_s, min(key, a.max_s - 32), 1);
+    };
     auto gload = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < PER; i++) {
-            const int q = tid + NT * i, gt = q >> 8;
-            // a 64-key tile's second half may lie past max_s (max_s % 64 == 32): read the first
-            // half again; those keys are past every row's position and masked
-            const size_t base = tile_base(kvh, a.max_s, min(k0 + 32 * gt, a.max_s - 32), 1) + (size_t)(q & 255) * 16;
-            kr[i] = ld16(a.kc + base);
-            vr[i] = ld16(a.vc + base);
+            const int q = tid + NT * i, gt = q / (256 * ES);
+            const size_t off = tile_addr(k0 + 32 * gt) + (size_t)(q % (256 * ES)) * 16;
+            if constexpr (RING) {
+                kr[i] = ld16((const char*)a.kring + off);
+                vr[i] = ld16((const char*)a.vring + off);
+            } else {
+                kr[i] = ld16(a.kc + off);
+                vr[i] = ld16(a.vc + off);
+            }
         }
-        if (tid < 2 * PBK) {
-            const int key = k0 + (tid & (PBK - 1));
-            const char* sb = tid < PBK ? ksb : vsb;
-            const size_t si = (size_t)kvh * a.max_s + min(key, a.max_s - 1);
-            sr = SCALE32 ? *(const uint32_t*)(sb + si * 4) : (uint32_t)*(const uint16_t*)(sb + si * 2);
+        if constexpr (!RING) {
+            if (tid < 2 * PBK) {
+                const int key = k0 + (tid & (PBK - 1));
+                const char* sb = tid < PBK ? ksb : vsb;
+                const size_t si = (size_t)kvh * a.max_s + min(key, a.max_s - 1);
+                sr = SCALE32 ? *(const uint32_t*)(sb + si * 4) : (uint32_t)*(const uint16_t*)(sb + si * 2);
+            }
         }
     };
     auto sstore = [&](int b) {
 #pragma unroll
         for (int i = 0; i < PER; i++) {
-            const int q = tid + NT * i, gt = q >> 8, j = (q & 255) >> 6, l = q & 63;
-            // K piece (j, l): key 16 (j / 2) + l % 16, dims 32 (l / 16) + 16 (j % 2) .. + 15
-            {
+            const int q = tid + NT * i, gt = q / (256 * ES), j = (q % (256 * ES)) >> 6, l = q & 63;
+            if constexpr (RING) {
+                // K piece (j, l): key 16 (j / 4) + l % 16, dims 32 (l / 16) + 8 (j % 4) .. + 7
+                const int key = 32 * gt + 16 * (j >> 2) + (l & 15), d0 = 32 * (l >> 4) + 8 * (j & 3);
+                *(u4_t*)(sm.k[b] + key * KROW + d0) = kr[i];
+                // V piece (j = u, l): row u of slot l, 8 keys: a copy (bf16 widened to fp16, so P
+                // keeps fp16's 11-bit significand in the P·V product)
+                u4_t vv = vr[i];
+                if constexpr (BF) vv = __builtin_bit_cast(u4_t, bf8_to_h8(vv));
+                *(u4_t*)(sm.vt[b] + gt * VTILE + j * VUROW + l * 8) = vv;
+            } else {
+                // K piece (j, l): key 16 (j / 2) + l % 16, dims 32 (l / 16) + 16 (j % 2) .. + 15
                 const int key = 32 * gt + 16 * (j >> 1) + (l & 15), d0 = 32 * (l >> 4) + 16 * (j & 1);
-                const h8_t lo8 = i8x8_to_h8(kr[i][0], kr[i][1]), hi8 = i8x8_to_h8(kr[i][2], kr[i][3]);
-                *(h8_t*)(sm.k[b] + key * KROW + d0) = lo8;
-                *(h8_t*)(sm.k[b] + key * KROW + d0 + 8) = hi8;
-            }
-            // V piece (j, l): rows u = 2j, 2j + 1 of slot l, 8 keys each: straight copies as fp16
-            {
+                *(h8_t*)(sm.k[b] + key * KROW + d0) = i8x8_to_h8(kr[i][0], kr[i][1]);
+                *(h8_t*)(sm.k[b] + key * KROW + d0 + 8) = i8x8_to_h8(kr[i][2], kr[i][3]);
+                // V piece (j, l): rows u = 2j, 2j + 1 of slot l, 8 keys each: straight copies as fp16
                 _Float16* base = sm.vt[b] + gt * VTILE + l * 8;
                 *(h8_t*)(base + (2 * j) * VUROW) = i8x8_to_h8(vr[i][0], vr[i][1]);
                 *(h8_t*)(base + (2 * j + 1) * VUROW) = i8x8_to_h8(vr[i][2], vr[i][3]);
             }
         }
         if (tid < 2 * PBK) {
-            const float v = SCALE32 ? __uint_as_float(sr) : h2f((uint16_t)sr);
+            const float v = RING ? 1.0f : (SCALE32 ? __uint_as_float(sr) : h2f((uint16_t)sr));
             // scores: scale_k * (1/sqrt(128)) [* log2 e]; weights: scale_v [* 64 into fp16's range]
             if (tid < PBK) sm.ks[b][tid] = v * c;
             else sm.vs[b][tid - PBK] = RELU2 ? v : v * 64.0f;
         }
     };
 
-    // ---- Q^T as the B operand: lane (row r, half h), k-step s: dims 16s + 8h .. + 7 (fp16)
-    h8v qb[8];
+    // ---- Q^T as the B operand: lane (row r, half h), k-step s: dims 16s + 8h .. + 7 (16-bit,
+    // in the MFMA's type)
+    u4_t qb[8];
     {
         const uint16_t* qr = a.q + (size_t)min(tok, a.T - 1) * a.q_tok_stride + (size_t)hq * a.q_head_stride;
 #pragma unroll
-        for (int s = 0; s < 8; s++) {
-            const u4_t raw = ld16(qr + 16 * s + 8 * h);
-            qb[s] = QBF ? __builtin_bit_cast(h8v, bf8_to_h8(raw)) : __builtin_bit_cast(h8v, raw);
+        for (int s = 0; s < 8; s++) qb[s] = ld16(qr + 16 * s + 8 * h);
+        if constexpr (PRE) {
+            // head_norm with the q gains, RoPE at the row's position, bf16 (attn_sliding8_b,
+            // prefill.metal:450-456): the row's dims are split over lanes h = 0, 1 (xor 32); the
+            // rotation pairs d and d + 32 (d < 32) sit in the same lane (k-steps s and s + 2)
+            float x[64];
+#pragma unroll
+            for (int s = 0; s < 8; s++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    x[8 * s + 2 * i] = bf2f(qb[s][i] & 0xFFFF);
+                    x[8 * s + 2 * i + 1] = bf2f(qb[s][i] >> 16);
+                }
+            float ss = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 64; e++) ss += x[e] * x[e];
+            ss += shfl_xor(ss, 32);
+            const float rn = 1.0f / sqrtf(ss / 128.0f + 1.1920929e-07f);
+#pragma unroll
+            for (int s = 0; s < 8; s++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) x[8 * s + e] = x[8 * s + e] * (rn * (1.0f + bf2f(a.qg[16 * s + 8 * h + e])));
+#pragma unroll
+            for (int s = 0; s < 2; s++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int d = 16 * s + 8 * h + e;   // < 32, partner d + 32 at k-step s + 2
+                    float sn, cs;
+                    sincosf(-(float)pos * (float)exp2(-(double)d / 32.0 * 13.287712379549449), &sn, &cs);
+                    const float x1 = x[8 * s + e], x2 = x[8 * (s + 2) + e];
+                    x[8 * s + e] = x1 * cs - x2 * sn;
+                    x[8 * (s + 2) + e] = x1 * sn + x2 * cs;
+                }
+#pragma unroll
+            for (int s = 0; s < 8; s++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    qb[s][i] = (uint32_t)f2bf(x[8 * s + 2 * i]) | ((uint32_t)f2bf(x[8 * s + 2 * i + 1]) << 16);
+        } else if constexpr (!RING && QBF) {
+#pragma unroll
+            for (int s = 0; s < 8; s++) qb[s] = __builtin_bit_cast(u4_t, bf8_to_h8(qb[s]));
         }
     }
+
     float m = NEG_INF, lsum = 0.0f;
     f16_t O[4];
 #pragma unroll
@@ -151,13 +218,13 @@ __global__ __launch_bounds__(64 * GQ, 2) void prefill_int8_kernel(PrefillArgs a)
         const int kmin = (full_tile || a.window == 0) ? -0x7FFFFFFF : pos - a.window;
         auto run_block = [&](int kb) {
             // S^T for keys k0 + 32kb + {8b + 4h + i}: the lane's 16 items e = 4b + i
-            const h8v* krow = (const h8v*)(sm.k[b] + (32 * kb + r) * KROW) + h;
-            f16_t st = mfma32(krow[0], qb[0], (f16_t){});
+            const u4_t* krow = (const u4_t*)(sm.k[b] + (32 * kb + r) * KROW) + h;
+            f16_t st = mfma32x<BF>(krow[0], qb[0], (f16_t){});
 #pragma unroll
-            for (int s = 1; s < 8; s++) st = mfma32(krow[2 * s], qb[s], st);
+            for (int s = 1; s < 8; s++) st = mfma32x<BF>(krow[2 * s], qb[s], st);
             const f4_t* ks4 = (const f4_t*)(sm.ks[b] + 32 * kb + 4 * h);   // [2b]: keys 8b + 4h ..
             const f4_t* vs4 = (const f4_t*)(sm.vs[b] + 32 * kb + 4 * h);
-            h8v pb[2];   // P^T B operands of the two 16-key k-steps: step s = items b = s, b = 2 + s
+            float pw[16];   // P^T values (with the V scales), item e
             if constexpr (RELU2) {
 #pragma unroll
                 for (int bb = 0; bb < 4; bb++) {
@@ -170,7 +237,7 @@ __global__ __launch_bounds__(64 * GQ, 2) void prefill_int8_kernel(PrefillArgs a)
                         const float t = fmaxf(st[e] * kq[i], 0.0f);
                         const float p = ok ? t * t : 0.0f;
                         lsum += p;
-                        pb[bb & 1][((bb >> 1) << 2) | i] = (_Float16)(p * vq[i]);
+                        pw[4 * bb + i] = p * vq[i];
                     }
                 }
             } else {
@@ -216,20 +283,30 @@ __global__ __launch_bounds__(64 * GQ, 2) void prefill_int8_kernel(PrefillArgs a)
                     for (int i = 0; i < 4; i++) {
                         const float p = __builtin_amdgcn_exp2f(x[4 * bb + i] - msub);
                         lsum += p;
-                        pb[bb & 1][((bb >> 1) << 2) | i] = (_Float16)(p * vq[i]);
+                        pw[4 * bb + i] = p * vq[i];
                     }
                 }
             }
+            // P^T B operands (fp16) of the two 16-key k-steps: step s = items b = s (slots 0..3)
+            // and b = 2 + s (slots 4..7)
+            u4_t pb[2];
+#pragma unroll
+            for (int s = 0; s < 2; s++)
+#pragma unroll
+                for (int q2 = 0; q2 < 4; q2++) {
+                    const int e0 = (q2 < 2 ? 4 * s : 4 * (2 + s)) + 2 * (q2 & 1);
+                    pb[s][q2] = __builtin_bit_cast(uint32_t, (h2_t){(_Float16)pw[e0], (_Float16)pw[e0 + 1]});
+                }
             // O^T (dims 32i + {8b + 4h + i}) += V^T P^T over two 16-key k-steps: in step s lane
             // (dim 32i + r, h) takes slot (n = dim / 8, g = 2s + h) of row u = dim % 8, whose 8 keys
             // {8s + 4h + i, 16 + 8s + 4h + i} are the P^T items b = s and b = 2 + s
-            const h8v* vt = (const h8v*)(sm.vt[b] + kb * VTILE);
+            const u4_t* vt = (const u4_t*)(sm.vt[b] + kb * VTILE);
 #pragma unroll
             for (int s = 0; s < 2; s++) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int dim = 32 * i + r;
-                    O[i] = mfma32(vt[(dim & 7) * (VUROW / 8) + (dim >> 3) + 16 * (2 * s + h)], pb[s], O[i]);
+                    O[i] = mfma32x<false>(vt[(dim & 7) * (VUROW / 8) + (dim >> 3) + 16 * (2 * s + h)], pb[s], O[i]);
                 }
             }
         };
@@ -303,6 +380,24 @@ int launch_prefill_int8(const PrefillArgs& a, hipStream_t st) {
     else if (gq == 8 && !a.relu2 && a.scale32 && a.q_bf16 && a.out_bf16) EMBLA_PF(8, false, true, true, true);
     else return EMBLA_ERR_UNSUPPORTED;
 #undef EMBLA_PF
+    return launch_prefill_tail(a, st);
+}
+
+int launch_prefill_ring(const PrefillArgs& a, hipStream_t st) {
+    const int gq = a.n_q / a.n_kv;
+    const dim3 grid((a.T + 31) / 32, a.n_kv, a.nsplit);
+#define EMBLA_PR(BF, PRE) \
+    hipLaunchKernelGGL((prefill_int8_kernel<4, false, false, BF, BF, true, BF, PRE>), grid, dim3(256), 0, st, a)
+    if (gq != 4 || a.relu2) return EMBLA_ERR_UNSUPPORTED;
+    if (a.q_bf16 && a.out_bf16 && a.qg) EMBLA_PR(true, true);
+    else if (a.q_bf16 && a.out_bf16) EMBLA_PR(true, false);
+    else if (!a.q_bf16 && !a.out_bf16 && !a.qg) EMBLA_PR(false, false);
+    else return EMBLA_ERR_UNSUPPORTED;
+#undef EMBLA_PR
+    return launch_prefill_tail(a, st);
+}
+
+int launch_prefill_tail(const PrefillArgs& a, hipStream_t st) {
     if (a.nsplit > 1) {
         const dim3 mg((a.T + 3) / 4, a.n_q);
         if (a.relu2) hipLaunchKernelGGL((prefill_merge_kernel<true, true>), mg, dim3(256), 0, st, a);

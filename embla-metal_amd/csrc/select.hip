@@ -70,7 +70,28 @@ __global__ __launch_bounds__(SEL_T) void select_topk_kernel(const float* __restr
     uint32_t* out = idx + (size_t)set * idx_stride;
     const int n = S - recent;
 
-    for (int j = tid; j < n; j += SEL_T) keys[lds_pad(j)] = order_bits(sc[j]);
+    // one round of independent loads: 16 bytes a thread a step, every step issued before the stores
+    constexpr int NV = (SEL_MAXN + 4 * SEL_T - 1) / (4 * SEL_T);
+    if (((uintptr_t)sc & 15) == 0) {
+        u4_t v[NV];
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int j = 4 * (tid + SEL_T * i);
+            v[i] = j + 3 < n ? ld16(sc + j) : (u4_t){0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int j = 4 * (tid + SEL_T * i);
+            if (j + 3 < n) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) keys[lds_pad(j + e)] = order_bits(__uint_as_float(v[i][e]));
+            } else {
+                for (int e = 0; e < 4 && j + e < n; e++) keys[lds_pad(j + e)] = order_bits(sc[j + e]);
+            }
+        }
+    } else {
+        for (int j = tid; j < n; j += SEL_T) keys[lds_pad(j)] = order_bits(sc[j]);
+    }
     const int per = (n + SEL_T - 1) / SEL_T, s0 = tid * per, s1 = min(n, s0 + per);
     __syncthreads();
 

@@ -59,6 +59,11 @@ SIGNATURES = {
     "embla_prefill_workspace_bytes": (sz, [i32, i32]),
     "embla_prefill_full": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp, sz, vp]),
     "embla_relu2_prefill": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
+    "embla_ring_append": (i32, [vp, vp, i32, i32, i32, i32, i32, vp, vp, i32, vp, vp]),
+    "embla_prefill_ring": (i32, [vp, i32, C.c_long, C.c_long, vp, vp, i32, vp, C.c_long, C.c_long, i32, i32, i32, i32,
+                                 i32, vp, vp, sz, vp]),
+    "embla_prefill_sliding": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, sz, vp]),
+    "embla_attn_sliding8_b": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, vp]),
     "embla_sparse_layer_decode": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, sz, vp]),
 }
 

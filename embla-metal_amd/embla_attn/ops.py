@@ -177,3 +177,36 @@ def relu2_prefill(qn, kc, vc, Tq, Tk, maxS, out=None, stream=None):
         out = torch.empty((Tq, 2048), dtype=torch.bfloat16, device=qn.device)
     call("embla_relu2_prefill", _p(qn), _p(kc), _p(vc), _p(out), Tq, Tk, maxS, stream_handle(stream))
     return out
+
+
+def ring_append(k, v, T, p0, n_kv, kring, vring, ring, dtype=BF16, kg=None, stride=None, stream=None):
+    stride = stride if stride is not None else n_kv * 128
+    call("embla_ring_append", _p(k), _p(v), dtype, stride, T, p0, n_kv, _p(kring), _p(vring), ring, _p(kg),
+         stream_handle(stream))
+
+
+def prefill_sliding(q, k, v, kring, vring, T, p0, ring, window, n_kv, out=None, ws=None, stream=None):
+    n_q = q.shape[1]
+    if out is None:
+        out = torch.empty((T, n_q, 128), dtype=torch.bfloat16, device=q.device)
+    call("embla_prefill_sliding", _p(q), _p(k), _p(v), _p(kring), _p(vring), _p(out), T, p0, ring, window, n_q, n_kv,
+         ws.ptr if ws else None, ws.nbytes if ws else 0, stream_handle(stream))
+    return out
+
+
+def attn_sliding8_b(qkv, qg, kg, kc, vc, p0, T, out=None, stream=None):
+    """Reference-signature kv_sliding_b + attn_sliding8_b: qkv [T][4096] bf16 -> o [T][2048] bf16."""
+    if out is None:
+        out = torch.empty((T, 2048), dtype=torch.bfloat16, device=qkv.device)
+    call("embla_attn_sliding8_b", _p(qkv), _p(qg), _p(kg), _p(kc), _p(vc), _p(out), p0, T, stream_handle(stream))
+    return out
+
+
+def prefill_ring(q, kring, vring, T, p0, ring, window, n_kv, dtype=BF16, qg=None, out=None, ws=None, stream=None):
+    """Windowed prefill over a 16-bit ring already holding the chunk; q [T][n_q][128]."""
+    n_q = q.shape[1]
+    if out is None:
+        out = torch.empty((T, n_q, 128), dtype=q.dtype, device=q.device)
+    call("embla_prefill_ring", _p(q), dtype, n_q * 128, 128, _p(kring), _p(vring), ring, _p(out), n_q * 128, 128, T,
+         p0, n_q, n_kv, window, _p(qg), ws.ptr if ws else None, ws.nbytes if ws else 0, stream_handle(stream))
+    return out

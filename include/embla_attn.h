@@ -174,6 +174,34 @@ int embla_prefill_full(const void* q, const void* k, const void* v, void* kc, vo
 int embla_relu2_prefill(const void* qn, const void* kc, const void* vc, void* o, int Tq, int Tk, int maxS,
                         hipStream_t stream);
 
+/* ---------------------------------------------------------------- batched prefill, 16-bit ring
+ * 16-bit K, V rows of T positions p0 .. into a ring (slot p % ring, tile layout with ES = 2).
+ * kg != NULL (bf16 only): K rows are RMS-normed with gains kg, rotated (RoPE at their position)
+ * and rounded to bf16 first, as kv_sliding_b (prefill.metal:103-125). Rows at (t * stride + h * 128). */
+int embla_ring_append(const void* k, const void* v, int dtype, int stride, int T, int p0, int n_kv, void* kring,
+                      void* vring, int ring, const void* kg, hipStream_t stream);
+
+/* Sliding-window prefill over a 16-bit ring that already holds the chunk: T tokens at p0 .. attend
+ * their last `window` positions (the own one included), softmax. dtype EMBLA_BF16 or EMBLA_F16 for
+ * q, ring and o; strides as embla_prefill_int8. qg != NULL (bf16): q is normed with gains qg,
+ * rotated and rounded to bf16 in the kernel (attn_sliding8_b, prefill.metal:428-548). Requires
+ * window - 1 + T <= ring. ws optional (embla_prefill_workspace_bytes). */
+int embla_prefill_ring(const void* q, int dtype, long q_tok_stride, long q_head_stride, const void* kring,
+                       const void* vring, int ring, void* o, long o_tok_stride, long o_head_stride, int T, int p0,
+                       int n_q, int n_kv, int window, const void* qg, void* ws, size_t ws_bytes, hipStream_t stream);
+
+/* Sliding-layer prefill chunk (config C5 sliding): bf16 K, V [T][n_kv][128] appended to the bf16 ring,
+ * then windowed softmax attention of q [T][n_q][128]; o bf16 [T][n_q][128]. */
+int embla_prefill_sliding(const void* q, const void* k, const void* v, void* kring, void* vring, void* o, int T,
+                          int p0, int ring, int window, int n_q, int n_kv, void* ws, size_t ws_bytes,
+                          hipStream_t stream);
+
+/* Reference-signature sliding prefill: kv_sliding_b then attn_sliding8_b (prefill.metal:103-125,
+ * 428-548; Prefill.swift:291-313): qkv bf16 [T][4096], gains qg, kg, bf16 rings kc, vc of 4096 slots
+ * (tile layout), window 128; o bf16 token-major [T][2048]. */
+int embla_attn_sliding8_b(const void* qkv, const void* qg, const void* kg, void* kc, void* vc, void* o, int p0, int T,
+                          hipStream_t stream);
+
 /* ---------------------------------------------------------------- quantise-and-append
  * T new positions p0 .. p0+T-1 of K and V rows into an int8 layer cache (write_row8,
  * common.metal:72-84; kv_append / kv_append_b, attention.metal:113-140, prefill.metal:182-212):
