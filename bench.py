@@ -184,8 +184,8 @@ def bench_c5(torch, reps=10):
     kring = torch.randn(n_kv * R * 128, generator=g, device="cuda").bfloat16()
     vring = torch.randn(n_kv * R * 128, generator=g, device="cuda").bfloat16()
     sflops = 4.0 * 128 * 16 * sum(min(W, p0 + t + 1) for t in range(T))
-    _, ms_sl = time_graph(torch, lambda: ops.prefill_sliding(q, kn, vn, kring, vring, T, p0, R, W, n_kv, out=out), reps, 2)
-    _, ms_sla = time_graph(torch, lambda: ops.prefill_ring(q, kring, vring, T, p0, R, W, n_kv, out=out), reps, 2)
+    _, ms_sl = time_graph(torch, lambda: ops.prefill_sliding(q, kn, vn, kring, vring, T, p0, R, W, n_kv, out=out, ws=ws), reps, 2)
+    _, ms_sla = time_graph(torch, lambda: ops.prefill_ring(q, kring, vring, T, p0, R, W, n_kv, out=out, ws=ws), reps, 2)
     sliding = dict(window=W, ring=R, gflop=sflops / 1e9, ms_attention=ms_sla,
                    tflops_attention=sflops / (ms_sla * 1e-3) / 1e12, ms_fused=ms_sl,
                    tokens_per_s=T / (ms_sl * 1e-3))

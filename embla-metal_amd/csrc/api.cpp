@@ -16,9 +16,23 @@ constexpr int kPartStride = 132;
 constexpr int kRefWindow = 128;         // the reference's sliding window (Engine.swift:9)
 constexpr int kRefRing = 4096;          // the reference's ring (attention.metal:6)
 constexpr int kTopK = 1024, kRecent = 128;   // Engine.swift:9 (topk, recent)
-constexpr int kPrefillSplits = 2;       // key-range splits of a prefill chunk (two waves a SIMD)        // floats a (chunk, query head) partial: acc[128], m, l, pad
+constexpr int kPrefillSplits = 4;       // most key-range splits of a prefill chunk (workspace sizing)
 
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+/// Key-range splits of a prefill launch: as many as keep every split >= 4 key tiles while the grid
+/// is under 512 workgroups (2 a CU: the kernel runs 2 waves a SIMD), at most kPrefillSplits, and
+/// only with a workspace for the partial rows. EMBLA_PREFILL_SPLITS caps it (tuning).
+int prefill_splits(const void* ws, size_t ws_bytes, int T, int n_q, int blocks, int tiles) {
+    if (!ws || ws_bytes < (size_t)kPrefillSplits * T * n_q * kPartStride * 4) return 1;
+    static const int cap = [] {
+        const char* e = getenv("EMBLA_PREFILL_SPLITS");
+        return e ? atoi(e) : 2;
+    }();
+    int ns = 1;
+    while (ns * 2 <= cap && ns * 2 <= kPrefillSplits && blocks * ns < 512 && tiles / (ns * 2) >= 4) ns *= 2;
+    return ns;
+}
 
 struct Workspace {
     uint32_t* counter;
@@ -297,8 +311,8 @@ int embla_prefill_int8(const void* q, int q_dtype, long q_tok_stride, long q_hea
     // two key-range splits when a workspace is given and the blocks are too few to fill the GPU
     // with two waves a SIMD (the split partials cost one merge pass)
     const int blocks = (T + 31) / 32 * n_kv;
-    a.nsplit = ws && ws_bytes >= embla_prefill_workspace_bytes(T, n_q) && blocks < 512 && p0 + T > 2048
-                   ? kPrefillSplits : 1;
+    a.nsplit = prefill_splits(ws, ws_bytes, T, n_q, blocks,
+                              window > 0 ? min((p0 + T) / 64, (window + 63) / 64 + 1) : (p0 + T) / 64);
     a.part = (float*)ws;
     a.kring = nullptr; a.vring = nullptr; a.R = 0; a.qg = nullptr;
     a.relu2 = weights == EMBLA_RELU2_SINK; a.scale32 = scale_dtype == EMBLA_F32;
@@ -345,8 +359,7 @@ int embla_prefill_ring(const void* q, int dtype, long q_tok_stride, long q_head_
     a.o = (uint16_t*)o; a.o_tok_stride = o_tok_stride; a.o_head_stride = o_head_stride;
     a.T = T; a.p0 = p0; a.max_s = ring; a.n_q = n_q; a.n_kv = n_kv; a.window = window;
     const int blocks = (T + 31) / 32 * n_kv;
-    a.nsplit = ws && ws_bytes >= embla_prefill_workspace_bytes(T, n_q) && blocks < 512 && window > 2048
-                   ? kPrefillSplits : 1;
+    a.nsplit = prefill_splits(ws, ws_bytes, T, n_q, blocks, (window + 63) / 64 + 1);
     a.part = (float*)ws;
     a.relu2 = false; a.scale32 = false; a.q_bf16 = dtype == EMBLA_BF16; a.out_bf16 = dtype == EMBLA_BF16;
     a.kring = (const uint16_t*)kring; a.vring = (const uint16_t*)vring; a.R = ring; a.qg = (const uint16_t*)qg;

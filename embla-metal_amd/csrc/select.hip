@@ -2,11 +2,11 @@
 //
 // select_topk_kernel restates select_keys (Sources/EmblaMetal/Kernels/attention.metal:647-744):
 // among keys [0, n = S - recent) the topk with the largest order_bits(score) (order_bits,
-// attention.metal:657-660), found by four 8-bit MSB-first radix passes, then an ordered
+// attention.metal:657-660), found by three MSB-first radix passes (11, 11, 10 bits), then an ordered
 // compaction: keys above the topk-th value in index order, then the first keys equal to it in
 // index order, then the recent keys n .. S-1. The output is bit-exact with the reference's
-// definition (order included). MI355X design: one 1024-thread workgroup a set stages all n scores'
-// order bits in LDS once (gfx950 has 160 KB a CU; 32K scores take 132 KB), so the four passes and
+// definition (order included). MI355X design: one 1024-thread workgroup a set keeps all n scores
+// order bits in LDS (gfx950 has 160 KB a CU; 32K scores take 128 KB), so the passes and
 // the compaction read LDS, not HBM.
 //
 // index_scores_kernel computes score_j = Σ_h w_h relu(q_h·k_j)² (the BASELINE configs' indexer,
@@ -21,14 +21,18 @@
 
 namespace embla {
 
-constexpr int SEL_T = 1024;            // threads of the select workgroup
-constexpr int SEL_MAXN = 32768 + 256;  // candidates it stages in LDS
+constexpr int SEL_T = 1024;                 // threads of the select workgroup (16 waves)
+constexpr int SEL_MAXN = 32768;             // candidates: their order bits stay in LDS
+constexpr int HBINS = 2048;                 // 11-bit radix digits: bits 31..21, 20..10, 9..0
+constexpr int HCOPIES = 2;                  // copies of the first pass's histogram
+constexpr int HSTRIDE = HBINS + 1;          // words a copy (offset by one word: other banks)
+constexpr int LCAP = 2048;                  // bucket list capacity (else passes 2-3 read every key)
+constexpr int SEL_OUTCAP = HCOPIES * HSTRIDE + LCAP;   // topk indices staged in hist + list
 
 __device__ __forceinline__ uint32_t order_bits(float f) {
     const uint32_t u = __float_as_uint(f);
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
-__device__ __forceinline__ int lds_pad(int j) { return j + (j >> 5); }   // conflict-free segments
 
 /// Exclusive prefix sum over the 1024 threads, and the total.
 __device__ __forceinline__ uint32_t block_scan_excl(uint32_t v, uint32_t* buf, uint32_t& total) {
@@ -58,95 +62,217 @@ __device__ __forceinline__ uint32_t block_scan_excl(uint32_t v, uint32_t* buf, u
     return r;
 }
 
+struct SelSmem {
+    uint32_t keys[SEL_MAXN];            // order bits, in index order
+    uint32_t hist[HCOPIES * HSTRIDE];   // histograms; with list: the staged output at the end
+    uint32_t list[LCAP];                // low 21 bits of the keys in the first pass's bucket
+    uint32_t tab[2][SEL_MAXN / 256];    // compaction: counts, then offsets, a (round, wave)
+    uint32_t buf[17];
+    uint32_t sel[3];
+    uint32_t cnt;
+};
+
+/// The digit holding the k-th largest of a histogram (ncopies copies of HBINS bins, HSTRIDE
+/// apart): sel = {digit, keys in digits above it, keys in it}. Thread t owns digits 2047 - 2t and
+/// 2046 - 2t.
+__device__ void pick_digit(SelSmem& sm, int ncopies, uint32_t k) {
+    const int tid = threadIdx.x;
+    uint32_t c0 = 0, c1 = 0;
+    for (int i = 0; i < ncopies; i++) {
+        c0 += sm.hist[i * HSTRIDE + HBINS - 1 - 2 * tid];
+        c1 += sm.hist[i * HSTRIDE + HBINS - 2 - 2 * tid];
+    }
+    uint32_t tot;
+    const uint32_t above = block_scan_excl(c0 + c1, sm.buf, tot);
+    if (above < k && above + c0 >= k) { sm.sel[0] = HBINS - 1 - 2 * tid; sm.sel[1] = above; sm.sel[2] = c0; }
+    if (above + c0 < k && above + c0 + c1 >= k) { sm.sel[0] = HBINS - 2 - 2 * tid; sm.sel[1] = above + c0; sm.sel[2] = c1; }
+    __syncthreads();
+}
+
+/// One set a 1024-thread workgroup. The kernel runs once a launch and is bound by instruction
+/// issue on its one CU, so every pass is a short rolled loop over the LDS-resident keys that takes
+/// 4 keys a lane (round r: lane t of wave w holds keys 4096 r + 4 (64 w + t) + e), with compares
+/// written as wave masks and counted by scalar popcounts. Phase 1 loads the scores (16-byte,
+/// every load in flight at once), stores their order bits and histograms their top 11 bits into 2
+/// copies (lane parity). The bucket holding the topk-th largest goes to an LDS list (when it
+/// fits) and passes 2 and 3 histogram only the list. The compaction writes, in index order, every
+/// key above the topk-th value and the first keys equal to it, at offsets from a scan of
+/// per-(round, wave) counts, staged in LDS and stored as one coalesced run.
 __global__ __launch_bounds__(SEL_T) void select_topk_kernel(const float* __restrict__ scores, int score_stride,
                                                             uint32_t* __restrict__ idx, int idx_stride, int S,
                                                             int topk, int recent) {
-    __shared__ uint32_t keys[SEL_MAXN + SEL_MAXN / 32];
-    __shared__ uint32_t hist[256];
-    __shared__ uint32_t buf[17];
-    __shared__ uint32_t sel[2];
+    __shared__ SelSmem sm;
     const int set = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const float* sc = scores + (size_t)set * score_stride;
     uint32_t* out = idx + (size_t)set * idx_stride;
     const int n = S - recent;
+    const int rounds = (n + 4 * SEL_T - 1) / (4 * SEL_T);
+    constexpr int NL = SEL_MAXN / (4 * SEL_T);   // rounds at most (8)
 
-    // one round of independent loads: 16 bytes a thread a step, every step issued before the stores
-    constexpr int NV = (SEL_MAXN + 4 * SEL_T - 1) / (4 * SEL_T);
-    if (((uintptr_t)sc & 15) == 0) {
-        u4_t v[NV];
-#pragma unroll
-        for (int i = 0; i < NV; i++) {
-            const int j = 4 * (tid + SEL_T * i);
-            v[i] = j + 3 < n ? ld16(sc + j) : (u4_t){0, 0, 0, 0};
-        }
-#pragma unroll
-        for (int i = 0; i < NV; i++) {
-            const int j = 4 * (tid + SEL_T * i);
-            if (j + 3 < n) {
-#pragma unroll
-                for (int e = 0; e < 4; e++) keys[lds_pad(j + e)] = order_bits(__uint_as_float(v[i][e]));
-            } else {
-                for (int e = 0; e < 4 && j + e < n; e++) keys[lds_pad(j + e)] = order_bits(sc[j + e]);
-            }
-        }
-    } else {
-        for (int j = tid; j < n; j += SEL_T) keys[lds_pad(j)] = order_bits(sc[j]);
-    }
-    const int per = (n + SEL_T - 1) / SEL_T, s0 = tid * per, s1 = min(n, s0 + per);
+    for (int q = tid; q < HCOPIES * HSTRIDE; q += SEL_T) sm.hist[q] = 0;
+    if (tid == 0) sm.cnt = 0;
     __syncthreads();
+    // ---- phase 1: load, order bits (0 past n: below every real key and never counted), histogram
+    {
+        const bool al = ((uintptr_t)sc & 15) == 0;
+        u4_t v[NL];
+#pragma unroll
+        for (int i = 0; i < NL; i++) {
+            const int j = 4 * tid + 4 * SEL_T * i;
+            v[i] = (u4_t){0, 0, 0, 0};
+            if (al && j + 3 < n) v[i] = ld16(sc + j);
+            else if (j < n)
+                for (int e = 0; e < 4; e++) v[i][e] = j + e < n ? __float_as_uint(sc[j + e]) : 0u;
+        }
+        uint32_t* hc = sm.hist + (lane & 1) * HSTRIDE;
+#pragma unroll
+        for (int i = 0; i < NL; i++) {
+            const int j = 4 * tid + 4 * SEL_T * i;
+            if (i < rounds) {
+                u4_t o;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    o[e] = j + e < n ? order_bits(__uint_as_float(v[i][e])) : 0u;
+                    if (j + e < n) atomicAdd(&hc[o[e] >> 21], 1u);
+                }
+                *(u4_t*)(sm.keys + j) = o;
+            }
+        }
+    }
+    __syncthreads();
+    uint32_t k = (uint32_t)topk;
+    pick_digit(sm, HCOPIES, k);
+    const uint32_t d1 = sm.sel[0], nb = sm.sel[2];
+    k -= sm.sel[1];
+    uint32_t kth;
+    if (nb <= LCAP) {
+        // ---- the bucket's keys (low 21 bits) to the list, then passes 2 and 3 over it
+        const uint64_t below = (1ull << lane) - 1ull;
+        for (int r = 0; r < rounds; r++) {
+            const int j = 4 * tid + 4 * SEL_T * r;
+            const u4_t v = *(const u4_t*)(sm.keys + j);
+            // list slots: one atomic a wave, lanes below first (the list's order is free)
+            bool h[4];
+            uint32_t tot = 0, pos = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                h[e] = (v[e] >> 21) == d1;   // padding (0) is never in the bucket holding the k-th
+                const uint64_t m = __ballot(h[e]);
+                tot += __popcll(m);
+                pos += __popcll(m & below);
+            }
+            if (tot) {
+                uint32_t base = 0;
+                if (lane == 0) base = atomicAdd(&sm.cnt, tot);
+                pos += __shfl(base, 0, 64);
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (h[e]) sm.list[pos++] = v[e] & 0x1FFFFFu;
+            }
+        }
+        uint32_t pre = 0;
+        for (int pass = 0; pass < 2; pass++) {
+            const int shift = pass == 0 ? 10 : 0;
+            sm.hist[tid] = 0;
+            sm.hist[tid + SEL_T] = 0;
+            __syncthreads();
+            for (uint32_t q = tid; q < nb; q += SEL_T) {
+                const uint32_t v = sm.list[q];
+                if (pass == 0 || (v >> 10) == pre) atomicAdd(&sm.hist[(v >> shift) & 2047u], 1u);
+            }
+            __syncthreads();
+            pick_digit(sm, 1, k);
+            pre = pass == 0 ? sm.sel[0] : (pre << 10) | sm.sel[0];
+            k -= sm.sel[1];
+            __syncthreads();
+        }
+        kth = (d1 << 21) | pre;
+    } else {
+        // ---- a bucket too large for the list: passes 2 and 3 over every key
+        uint32_t prefix = d1 << 21, mask = 0xFFE00000u;
+        for (int pass = 0; pass < 2; pass++) {
+            const int shift = pass == 0 ? 10 : 0;
+            const uint32_t dm = pass == 0 ? 2047u : 1023u;
+            for (int q = tid; q < HCOPIES * HSTRIDE; q += SEL_T) sm.hist[q] = 0;
+            __syncthreads();
+            uint32_t* hc = sm.hist + (lane & 1) * HSTRIDE;
+            for (int r = 0; r < rounds; r++) {
+                const int j = 4 * tid + 4 * SEL_T * r;
+                const u4_t v = *(const u4_t*)(sm.keys + j);
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if ((v[e] & mask) == prefix && j + e < n) atomicAdd(&hc[(v[e] >> shift) & dm], 1u);
+            }
+            __syncthreads();
+            pick_digit(sm, HCOPIES, k);
+            prefix |= sm.sel[0] << shift;
+            mask |= dm << shift;
+            k -= sm.sel[1];
+            __syncthreads();
+        }
+        kth = prefix;
+    }
 
-    uint32_t prefix = 0, mask = 0, k = (uint32_t)topk;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        if (tid < 256) hist[tid] = 0;
-        __syncthreads();
-        for (int j = s0; j < s1; j++) {
-            const uint32_t b = keys[lds_pad(j)];
-            if ((b & mask) == prefix) atomicAdd(&hist[(b >> shift) & 255u], 1u);
+    // ---- ordered compaction: keys above kth, then the first k equal to it, by index. Round r,
+    // wave w holds keys 4096 r + 256 w .. + 255: table entry 16 r + w. Padding keys are 0, never
+    // above kth, and equal to it only if kth is 0, which needs k > every real key's count: no.
+    for (int r = 0; r < rounds; r++) {
+        const int j = 4 * tid + 4 * SEL_T * r;
+        const u4_t v = *(const u4_t*)(sm.keys + j);
+        uint32_t cg = 0, ce = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            cg += __popcll(__ballot(v[e] > kth));
+            ce += __popcll(__ballot(v[e] == kth && j + e < n));
         }
-        __syncthreads();
-        // counts at or above each digit, from the top: the digit whose bucket holds the k-th largest
-        if (w == 0) {
-            uint32_t c[4], s = 0;
+        if (lane == 0) { sm.tab[0][16 * r + w] = cg; sm.tab[1][16 * r + w] = ce; }
+    }
+    __syncthreads();
+    if (w < 2) {   // wave 0 scans the "above" table, wave 1 the "equal" one (2 entries a lane)
+        uint32_t* t = sm.tab[w];
+        const int m = 16 * rounds;
+        const uint32_t v0 = 2 * lane < m ? t[2 * lane] : 0u, v1 = 2 * lane + 1 < m ? t[2 * lane + 1] : 0u;
+        const uint32_t s = v0 + v1;
+        uint32_t incl = s;
 #pragma unroll
-            for (int i = 0; i < 4; i++) { c[i] = hist[255 - (lane * 4 + i)]; s += c[i]; }
-            uint32_t above = s;
+        for (int d = 1; d < 64; d <<= 1) {
+            const uint32_t o = __shfl_up(incl, d, 64);
+            if (lane >= d) incl += o;
+        }
+        if (2 * lane < m) t[2 * lane] = incl - s;
+        if (2 * lane + 1 < m) t[2 * lane + 1] = incl - s + v0;
+        if (lane == 63) sm.sel[w] = incl;   // totals: keys above kth, keys equal to it
+    }
+    __syncthreads();
+    const uint32_t ngt = sm.sel[0];
+    const uint64_t below = (1ull << lane) - 1ull;
+    uint32_t* sout = topk <= SEL_OUTCAP ? sm.hist : out;   // hist and list are contiguous
+    for (int r = 0; r < rounds; r++) {
+        const int j = 4 * tid + 4 * SEL_T * r;
+        const u4_t v = *(const u4_t*)(sm.keys + j);
+        bool g[4], e[4];
+        uint32_t pg = sm.tab[0][16 * r + w], pe = sm.tab[1][16 * r + w];
 #pragma unroll
-            for (int d = 1; d < 64; d <<= 1) {
-                const uint32_t o = __shfl_up(above, d, 64);
-                if (lane >= d) above += o;
+        for (int u = 0; u < 4; u++) {
+            g[u] = v[u] > kth;
+            e[u] = v[u] == kth && j + u < n;
+            pg += __popcll(__ballot(g[u]) & below);   // the keys of lanes below this one
+            pe += __popcll(__ballot(e[u]) & below);
+        }
+        if (g[0] | g[1] | g[2] | g[3] | e[0] | e[1] | e[2] | e[3]) {
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                if (g[u]) sout[pg++] = (uint32_t)(j + u);
+                if (e[u]) {
+                    if (pe < k) sout[ngt + pe] = (uint32_t)(j + u);
+                    pe++;
+                }
             }
-            above -= s;   // exclusive
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                if (above < k && above + c[i] >= k) { sel[0] = 255u - (uint32_t)(lane * 4 + i); sel[1] = above; }
-                above += c[i];
-            }
-        }
-        __syncthreads();
-        prefix |= sel[0] << shift;
-        mask |= 255u << shift;
-        k -= sel[1];
-        __syncthreads();
-    }
-    // prefix is the topk-th largest; every key above it, then the first k equal to it
-    uint32_t gt = 0, eq = 0;
-    for (int j = s0; j < s1; j++) {
-        const uint32_t b = keys[lds_pad(j)];
-        gt += b > prefix;
-        eq += b == prefix;
-    }
-    uint32_t ngt, neq;
-    const uint32_t gpos = block_scan_excl(gt, buf, ngt);
-    uint32_t epos = block_scan_excl(eq, buf, neq);
-    uint32_t gp = gpos;
-    for (int j = s0; j < s1; j++) {
-        const uint32_t b = keys[lds_pad(j)];
-        if (b > prefix) out[gp++] = (uint32_t)j;
-        else if (b == prefix) {
-            if (epos < k) out[ngt + epos] = (uint32_t)j;
-            epos++;
         }
     }
+    __syncthreads();
+    if (sout != out)
+        for (int j = tid; j < topk; j += SEL_T) out[j] = sout[j];
     for (int j = tid; j < recent; j += SEL_T) out[topk + j] = (uint32_t)(n + j);
 }
 

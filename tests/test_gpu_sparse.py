@@ -100,3 +100,19 @@ def test_sparse_layer_end_to_end(torch_gpu, orc, c4, S):
         sel = np.arange(S, dtype=np.int32)
     ref = orc.decode_rows(synth.f16_val(c4["q"]), synth.f16_val(c4["K"]), synth.f16_val(c4["V"]), sel)
     assert_close(f16_host(o), ref, what=f"S={S}")
+
+
+def test_select_topk_many_sets_unaligned(torch_gpu, orc):
+    """Several sets at an odd stride (rows not 16-byte aligned), ragged n, a small topk."""
+    from embla_attn import ops
+    torch = torch_gpu
+    S, stride, n_sets, topk, recent = 5003, 5007, 5, 300, 17
+    g = synth.SplitMix64(123)
+    sc = (g.normal(n_sets * stride).astype(np.float32) * 10).round().reshape(n_sets, stride)
+    say("select topk many sets unaligned")
+    idx = ops.select_topk(dev(sc.reshape(-1)), S, n_sets=n_sets, topk=topk, recent=recent, score_stride=stride)
+    got = idx.cpu().numpy().astype(np.uint32)
+    for s in range(n_sets):
+        row = np.concatenate([sc[s, :S - recent], np.zeros(recent, np.float32)])
+        ref = orc.select_keys(row, S, topk=topk, recent=recent)
+        np.testing.assert_array_equal(got[s], ref, err_msg=f"set {s}")
