@@ -189,7 +189,24 @@ def bench_c5(torch, reps=10):
     sliding = dict(window=W, ring=R, gflop=sflops / 1e9, ms_attention=ms_sla,
                    tflops_attention=sflops / (ms_sla * 1e-3) / 1e12, ms_fused=ms_sl,
                    tokens_per_s=T / (ms_sl * 1e-3))
-    return dict(full, sliding=sliding)
+    # sparse layer: the same chunk, per-row top-1024 + latest 128 by the index score, over a
+    # row-major int8 cache (quantise-and-append, MFMA indexer, exact band select, gathered attention)
+    kr = torch.empty(nrow + n_kv * max_s * 2, dtype=torch.uint8, device="cuda")
+    vr = torch.empty_like(kr)
+    for t in (kr, vr):
+        t[:nrow].random_(0, 256, generator=g)
+        t[nrow:].view(torch.float16).uniform_(0.005, 0.02, generator=g)
+    qi = torch.randn(T, 4, 64, generator=g, device="cuda").half()
+    wi = torch.rand(T, 4, generator=g, device="cuda")
+    ki = torch.randn(p0 + T, 64, generator=g, device="cuda").half()
+    sws = ops.SparsePrefillWorkspace(T, p0)
+    _, ms_sp = time_graph(torch, lambda: ops.prefill_sparse(q, kn, vn, qi, wi, ki, kr, vr, T, p0, max_s, n_kv, sws,
+                                                            out=out), reps, 2)
+    att = 4.0 * 128 * 16 * T * 1152
+    idxf = 4.0 * 128 * sum(p0 + t + 1 - 128 for t in range(T))
+    sparse = dict(gflop_attention=att / 1e9, gflop_indexer=idxf / 1e9, ms_layer=ms_sp,
+                  tflops_layer=(att + idxf) / (ms_sp * 1e-3) / 1e12, tokens_per_s=T / (ms_sp * 1e-3))
+    return dict(full, sliding=sliding, sparse=sparse)
 
 
 def cpu_baseline(case, L, budget_s=10.0):
@@ -272,7 +289,8 @@ def main():
         "c2_sliding": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in c2.items()},
         "c4_sparse": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in c4.items()},
         "c5_prefill_full": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c5.items()
-                            if k != "sliding"},
+                            if k not in ("sliding", "sparse")},
+        "c5_prefill_sparse": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c5["sparse"].items()},
         "c5_prefill_sliding": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c5["sliding"].items()},
     }
     if not args.no_cpu:

@@ -16,6 +16,7 @@ constexpr int kPartStride = 132;
 constexpr int kRefWindow = 128;         // the reference's sliding window (Engine.swift:9)
 constexpr int kRefRing = 4096;          // the reference's ring (attention.metal:6)
 constexpr int kTopK = 1024, kRecent = 128;   // Engine.swift:9 (topk, recent)
+constexpr int kIndexChunk = 2048;         // keys a workgroup of the MFMA indexer
 constexpr int kPrefillSplits = 4;       // most key-range splits of a prefill chunk (workspace sizing)
 
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
@@ -383,6 +384,44 @@ int embla_attn_sliding8_b(const void* qkv, const void* qg, const void* kg, void*
     if (rc) return rc;
     return embla_prefill_ring(row, EMBLA_BF16, 4096, 128, kc, vc, kRefRing, o, 2048, 128, T, p0, 16, 4, kRefWindow, qg,
                               nullptr, 0, stream);
+}
+
+size_t embla_sparse_prefill_workspace_bytes(int T, int p0) {
+    if (T <= 0 || p0 < 0) return 0;
+    const size_t ld = round_up((size_t)(p0 + T > kRecent ? p0 + T - kRecent : 1), kIndexChunk);
+    const size_t nch = ld / kIndexChunk;
+    return round_up((size_t)T * ld * 2, 256) + round_up(nch * 4, 256) + (size_t)T * (kTopK + kRecent) * 4;
+}
+
+int embla_prefill_sparse(const void* q, const void* k, const void* v, const void* qi, const float* w, const void* ki,
+                         void* kc, void* vc, void* o, uint32_t* idx, int T, int p0, int max_s, int n_q, int n_kv,
+                         void* ws, size_t ws_bytes, hipStream_t stream) {
+    if (!q || !k || !v || !qi || !w || !ki || !kc || !vc || !o || T <= 0 || p0 < 0) return EMBLA_ERR_INVALID;
+    if (n_kv <= 0 || n_q % n_kv || n_kv > kMaxKV || max_s <= 0 || p0 + T > max_s) return EMBLA_ERR_INVALID;
+    if (!ws || ws_bytes < embla_sparse_prefill_workspace_bytes(T, p0)) return EMBLA_ERR_WORKSPACE;
+    if (p0 + T - kRecent > 32768) return EMBLA_ERR_UNSUPPORTED;
+    const int ld = (int)round_up((size_t)(p0 + T > kRecent ? p0 + T - kRecent : 1), kIndexChunk);
+    const int nch = ld / kIndexChunk;
+    char* wp = (char*)ws;
+    uint16_t* keys = (uint16_t*)wp;
+    wp += round_up((size_t)T * ld * 2, 256);
+    float* kmax = (float*)wp;
+    wp += round_up((size_t)nch * 4, 256);
+    uint32_t* sel = idx ? idx : (uint32_t*)wp;
+    // the chunk's K, V quantised into the row-major int8 cache
+    KVQuantArgs qa{(const uint16_t*)k, (const uint16_t*)v, n_kv * 128, T, p0, n_kv, max_s,
+                   (int8_t*)kc, (int8_t*)vc, true, false, false, true};
+    int rc = launch_kv_quant(qa, stream);
+    if (rc) return rc;
+    IndexMfmaArgs ia{(const uint16_t*)qi, w, (const uint16_t*)ki, keys, kmax, T, p0 + T, ld, kIndexChunk};
+    if ((rc = launch_index_mfma(ia, stream))) return rc;
+    BandSelectArgs ba{keys, ld, (const uint16_t*)qi, w, (const uint16_t*)ki, kmax, nch, sel, kTopK + kRecent,
+                      T, p0, kTopK, kRecent};
+    if ((rc = launch_select_band(ba, stream))) return rc;
+    SparseRows8Args sa{(const uint16_t*)q, (long)n_q * 128, (const int8_t*)kc, (const int8_t*)vc, sel,
+                       kTopK + kRecent, kTopK + kRecent, p0, T, (uint16_t*)o, (long)n_q * 128, max_s, n_q, n_kv,
+                       true, true};
+    return launch_sparse_rows8(sa, stream);
 }
 
 }  // extern "C"

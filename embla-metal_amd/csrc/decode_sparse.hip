@@ -187,4 +187,179 @@ int launch_sparse_decode(const SparseArgs& a, hipStream_t st) {
     return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
 }
 
+/// Batched gathered attention over a row-major int8 cache: one workgroup a (query row, kv head),
+/// its 4 waves taking interleaved 32-key steps of the row's key list. A wave gathers 32 rows of K
+/// and V (each 16-byte load covers eight 128-byte rows), widens them to fp16 (exact) into its LDS
+/// stage, and runs the same MFMA scheme as sparse_decode_kernel; each key's scale multiplies its
+/// score, each value row's scale (x 64, into fp16's normal range) its weight. Follows the sparse
+/// layer's softmax over the selected rows of an int8 cache (attention.metal:448-584), one query
+/// row at a time, for the batched prefill chunk.
+template <int GQ>
+__global__ __launch_bounds__(256) void sparse_rows8_kernel(SparseRows8Args a) {
+    const int kvh = blockIdx.y, r = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int n = lane & 15, g = lane >> 4;
+    const int pos = a.p0 + r;
+    const bool sel = a.idx && pos + 1 > a.nsel;
+    const int nk = sel ? a.nsel : pos + 1;
+    const uint32_t* rows = sel ? a.idx + (size_t)r * a.idx_row_stride : nullptr;
+    const int8_t* kb = a.kc + (size_t)kvh * a.max_s * HD;
+    const int8_t* vb = a.vc + (size_t)kvh * a.max_s * HD;
+    const size_t nrow = (size_t)a.n_kv * a.max_s * HD;
+    const uint16_t* ksc = (const uint16_t*)(a.kc + nrow) + (size_t)kvh * a.max_s;
+    const uint16_t* vsc = (const uint16_t*)(a.vc + nrow) + (size_t)kvh * a.max_s;
+
+    __shared__ uint16_t stage[4][2][32 * SROW];
+    __shared__ float sks[4][32], svs[4][32];
+    uint16_t* Ks = stage[w][0];
+    uint16_t* Vs = stage[w][1];
+
+    // q^T, B operand (fp16): lane (head n, group g), MFMA u: dims 32g + 8u .. + 7
+    u4_t qb[4];
+    {
+        const uint16_t* qr = a.q + (size_t)r * a.q_row_stride + (size_t)(kvh * GQ + (n < GQ ? n : 0)) * HD;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            u4_t v = ld16(qr + 32 * g + 8 * u);
+            if (a.q_bf16) v = __builtin_bit_cast(u4_t, bf8_to_h8(v));
+            qb[u] = n < GQ ? v : (u4_t){0, 0, 0, 0};
+        }
+    }
+    const float sc = 0.08838834764831845f * 1.4426950408889634f;
+    float m = NEG_INF, l = 0.0f;
+    f4_t O[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) O[u] = (f4_t){0, 0, 0, 0};
+
+    for (int t0 = 32 * w; t0 < nk; t0 += 128) {
+        // gather: load j covers keys t0 + 8j .. + 7, lane l: key t0 + 8j + l / 8, dims 16 (l % 8) ..
+        u4_t kr[4], vr[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int p = t0 + 8 * j + (lane >> 3);
+            const size_t row = p < nk ? (size_t)min(rows ? (int)rows[p] : p, a.max_s - 1) : 0;
+            kr[j] = ld16(kb + row * HD + 16 * (lane & 7));
+            vr[j] = ld16(vb + row * HD + 16 * (lane & 7));
+        }
+        if (lane < 32) {
+            const int p = t0 + lane;
+            const size_t row = p < nk ? (size_t)min(rows ? (int)rows[p] : p, a.max_s - 1) : 0;
+            sks[w][lane] = h2f(ksc[row]) * sc;
+            svs[w][lane] = h2f(vsc[row]) * 64.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int rr = 8 * j + (lane >> 3);
+            uint16_t* kd = Ks + rr * SROW + 16 * (lane & 7);
+            uint16_t* vd = Vs + rr * SROW + 16 * (lane & 7);
+            *(h8_t*)kd = i8x8_to_h8(kr[j][0], kr[j][1]);
+            *(h8_t*)(kd + 8) = i8x8_to_h8(kr[j][2], kr[j][3]);
+            *(h8_t*)vd = i8x8_to_h8(vr[j][0], vr[j][1]);
+            *(h8_t*)(vd + 8) = i8x8_to_h8(vr[j][2], vr[j][3]);
+        }
+        wave_lds_sync();
+        // S^T: lane (head n, group g) item i of half t = key 16t + 4g + i
+        float x[8];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            f4_t st = {0, 0, 0, 0};
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                st = mfma16s<false>(*(const u4_t*)(Ks + (16 * t + n) * SROW + 32 * g + 8 * u), qb[u], st);
+            const f4_t kq = *(const f4_t*)(&sks[w][16 * t + 4 * g]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) x[4 * t + i] = t0 + 16 * t + 4 * g + i < nk ? st[i] * kq[i] : NEG_INF;
+        }
+        float mt = NEG_INF;
+#pragma unroll
+        for (int e = 0; e < 8; e++) mt = fmaxf(mt, x[e]);
+        mt = fmaxf(mt, shfl_xor(mt, 16));
+        mt = fmaxf(mt, shfl_xor(mt, 32));
+        const float mn = fmaxf(m, mt);
+        if (__any(n < GQ && mn > m)) {
+            if (__any(n < GQ && m != NEG_INF)) {
+                const float corr = m == NEG_INF ? 0.0f : exp2f(m - mn);
+                l *= corr;
+                float cf[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float c0 = readlane(corr, i);
+                    if constexpr (GQ == 8) cf[i] = g == 1 ? readlane(corr, 4 + i) : c0;
+                    else cf[i] = c0;
+                }
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) O[u][i] *= cf[i];
+            }
+            m = mn;
+        }
+        u4_t wb;
+        const f4_t vq0 = *(const f4_t*)(&svs[w][4 * g]), vq1 = *(const f4_t*)(&svs[w][16 + 4 * g]);
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            const float p0 = exp2f(x[e] - m), p1 = exp2f(x[e + 1] - m);
+            l += p0 + p1;
+            const float s0 = e < 4 ? vq0[e & 3] : vq1[e & 3], s1 = e < 4 ? vq0[(e + 1) & 3] : vq1[(e + 1) & 3];
+            wb[e / 2] = __builtin_bit_cast(uint32_t, (h2_t){(_Float16)(p0 * s0), (_Float16)(p1 * s1)});
+        }
+        // V operand: lane (dim column n, group g), MFMA u = dim 8n + u, item e = key 16t + 4g + i
+        u4_t vrow[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) vrow[e] = *(const u4_t*)(Vs + (16 * (e >> 2) + 4 * g + (e & 3)) * SROW + 8 * n);
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            u4_t b;
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                const uint32_t lo = (vrow[e][u >> 1] >> (16 * (u & 1))) & 0xFFFF;
+                const uint32_t hi = (vrow[e + 1][u >> 1] >> (16 * (u & 1))) & 0xFFFF;
+                b[e / 2] = lo | (hi << 16);
+            }
+            O[u] = mfma16s<false>(wb, b, O[u]);
+        }
+        wave_lds_sync();   // the next step's stores come after every lane's reads
+    }
+
+    // ---- merge the 4 waves (LDS) and write the row's output
+    __shared__ float om[4][GQ][HD];
+    __shared__ float mm[4][GQ], ll[4][GQ];
+    l += shfl_xor(l, 16);
+    l += shfl_xor(l, 32);
+    if (g == 0 && n < GQ) { mm[w][n] = m; ll[w][n] = l; }
+#pragma unroll
+    for (int u = 0; u < 8; u++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (4 * g + i < GQ) om[w][4 * g + i][8 * n + u] = O[u][i];
+    __syncthreads();
+    constexpr int PER = GQ * HD / 256;
+    const int oh = tid * PER / HD, od = tid * PER % HD;
+    const float M = fmaxf(fmaxf(mm[0][oh], mm[1][oh]), fmaxf(mm[2][oh], mm[3][oh]));
+    float f[4], L = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ww++) {
+        f[ww] = mm[ww][oh] == NEG_INF ? 0.0f : exp2f(mm[ww][oh] - M);
+        L += ll[ww][oh] * f[ww];
+    }
+    const float inv = 1.0f / (64.0f * L);
+    uint16_t* orow = a.o + (size_t)r * a.o_row_stride + (size_t)(kvh * GQ + oh) * HD + od;
+#pragma unroll
+    for (int e = 0; e < PER; e++) {
+        float s = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < 4; ww++) s += om[ww][oh][od + e] * f[ww];
+        orow[e] = a.o_bf16 ? f2bf(s * inv) : f2h(s * inv);
+    }
+}
+
+int launch_sparse_rows8(const SparseRows8Args& a, hipStream_t st) {
+    const dim3 grid(1, a.n_kv, a.R), block(256);
+    const int gq = a.n_q / a.n_kv;
+    if (gq == 4) hipLaunchKernelGGL((sparse_rows8_kernel<4>), grid, block, 0, st, a);
+    else if (gq == 8) hipLaunchKernelGGL((sparse_rows8_kernel<8>), grid, block, 0, st, a);
+    else return EMBLA_ERR_UNSUPPORTED;
+    return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
+}
+
 }  // namespace embla

@@ -50,6 +50,52 @@ struct SparseArgs {
     bool bf16;
 };
 int launch_sparse_decode(const SparseArgs& a, hipStream_t st);
+
+/// Batched gathered attention over a row-major int8 cache (fp16 scales after the rows): query row r
+/// (position p0 + r) attends the keys idx[r][0 .. nsel) when p0 + r + 1 > nsel, else keys 0 .. p0 + r.
+struct SparseRows8Args {
+    const uint16_t* q;       // row r, head h at q + r * q_row_stride + h * 128 (fp16 or bf16)
+    long q_row_stride;
+    const int8_t* kc;        // [n_kv][max_s][128] int8, then fp16 scales [n_kv][max_s]
+    const int8_t* vc;
+    const uint32_t* idx;     // [R][idx_row_stride], one set a row shared by the kv heads
+    long idx_row_stride;
+    int nsel, p0, R;
+    uint16_t* o;             // row r, head h at o + r * o_row_stride + h * 128
+    long o_row_stride;
+    int max_s, n_q, n_kv;
+    bool q_bf16, o_bf16;
+};
+int launch_sparse_rows8(const SparseRows8Args& a, hipStream_t st);
+
+/// Approximate index scores of T rows (4 fp16 index heads of 64 dims, fp32 weights) against keys
+/// 0 .. ld-1 (zero past nk), as the top 16 bits of their order bits, and each key chunk's largest
+/// key norm (kmax[c], chunk c = keys c * kchunk ..).
+struct IndexMfmaArgs {
+    const uint16_t* qi;   // [T][4][64]
+    const float* w;       // [T][4]
+    const uint16_t* ki;   // [nk][64]
+    uint16_t* keys;       // [T][ld]
+    float* kmax;          // [ld / kchunk]
+    int T, nk, ld, kchunk;
+};
+int launch_index_mfma(const IndexMfmaArgs& a, hipStream_t st);
+
+/// Row t (position p0 + t, S = p0 + t + 1 keys) selects, when S > topk + recent, the topk keys of
+/// [0, S - recent) by the spec score, in select_keys' order, then the recent ones: idx[t][..].
+struct BandSelectArgs {
+    const uint16_t* keys;  // [T][ld] from index_mfma
+    int ld;
+    const uint16_t* qi;
+    const float* w;
+    const uint16_t* ki;
+    const float* kmax;
+    int nchunks;
+    uint32_t* idx;
+    int idx_stride;
+    int T, p0, topk, recent;
+};
+int launch_select_band(const BandSelectArgs& a, hipStream_t st);
 int launch_select_topk(const float* scores, int score_stride, uint32_t* idx, int idx_stride, int S, int n_sets,
                        int topk, int recent, hipStream_t st);
 struct PrefillArgs {
@@ -83,6 +129,7 @@ struct KVQuantArgs {
     int8_t* kc;
     int8_t* vc;
     bool in_bf16, scale32, norm_k;
+    bool row_major;      // rows [n_kv][max_s][128] (the sparse layer's gathered cache), else MFMA tiles
 };
 int launch_kv_quant(const KVQuantArgs& a, hipStream_t st);
 

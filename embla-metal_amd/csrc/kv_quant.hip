@@ -37,7 +37,8 @@ __device__ __forceinline__ float rms_factor(float x0, float x1) {
 }
 
 /// One wave a (token, kv head, K or V): two dims a lane, quantised, then stored at their places
-/// in the MFMA lane-order tiles (common.hpp); K's two bytes are adjacent, V's are not.
+/// in the MFMA lane-order tiles (common.hpp; K's two bytes are adjacent, V's are not), or in plain
+/// 128-byte rows for a cache that is read by gathering (row_major).
 __global__ __launch_bounds__(64) void kv_quant_kernel(KVQuantArgs a) {
     const int lane = threadIdx.x;
     const int t = blockIdx.x, h = blockIdx.y;
@@ -64,7 +65,9 @@ __global__ __launch_bounds__(64) void kv_quant_kernel(KVQuantArgs a) {
         if (a.scale32) ((float*)(rows + nrow))[si] = am / 127.0f;
         else ((uint16_t*)(rows + nrow))[si] = f2h(am / 127.0f);
     }
-    if (!is_v) {
+    if (a.row_major) {
+        *(uint16_t*)(rows + ((size_t)h * a.max_s + pos) * HD + 2 * lane) = (uint16_t)((q0 & 0xFF) | ((q1 & 0xFF) << 8));
+    } else if (!is_v) {
         *(uint16_t*)(rows + kt_off(h, a.max_s, pos, 2 * lane, 1)) = (uint16_t)((q0 & 0xFF) | ((q1 & 0xFF) << 8));
     } else {
         rows[vt_off(h, a.max_s, pos, 2 * lane, 1)] = (int8_t)q0;

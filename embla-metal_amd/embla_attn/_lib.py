@@ -59,6 +59,8 @@ SIGNATURES = {
     "embla_prefill_workspace_bytes": (sz, [i32, i32]),
     "embla_prefill_full": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp, sz, vp]),
     "embla_relu2_prefill": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
+    "embla_sparse_prefill_workspace_bytes": (sz, [i32, i32]),
+    "embla_prefill_sparse": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp, sz, vp]),
     "embla_ring_append": (i32, [vp, vp, i32, i32, i32, i32, i32, vp, vp, i32, vp, vp]),
     "embla_prefill_ring": (i32, [vp, i32, C.c_long, C.c_long, vp, vp, i32, vp, C.c_long, C.c_long, i32, i32, i32, i32,
                                  i32, vp, vp, sz, vp]),

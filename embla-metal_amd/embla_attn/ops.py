@@ -210,3 +210,24 @@ def prefill_ring(q, kring, vring, T, p0, ring, window, n_kv, dtype=BF16, qg=None
     call("embla_prefill_ring", _p(q), dtype, n_q * 128, 128, _p(kring), _p(vring), ring, _p(out), n_q * 128, 128, T,
          p0, n_q, n_kv, window, _p(qg), ws.ptr if ws else None, ws.nbytes if ws else 0, stream_handle(stream))
     return out
+
+
+class SparsePrefillWorkspace:
+    def __init__(self, T: int, p0: int, device="cuda"):
+        self.nbytes = int(lib().embla_sparse_prefill_workspace_bytes(T, p0))
+        self.buf = torch.empty(self.nbytes, dtype=torch.uint8, device=device)
+
+    @property
+    def ptr(self):
+        return _p(self.buf)
+
+
+def prefill_sparse(q, k, v, qi, w, ki, kc, vc, T, p0, max_s, n_kv, ws, out=None, idx=None, stream=None):
+    """Sparse-layer prefill chunk: append k, v (row-major int8 cache), per-row top-1024 + latest 128
+    by the index score, attention. Returns (o [T][n_q][128] bf16, idx [T][1152] int32 or None)."""
+    n_q = q.shape[1]
+    if out is None:
+        out = torch.empty((T, n_q, 128), dtype=torch.bfloat16, device=q.device)
+    call("embla_prefill_sparse", _p(q), _p(k), _p(v), _p(qi), _p(w), _p(ki), _p(kc), _p(vc), _p(out), _p(idx), T, p0,
+         max_s, n_q, n_kv, ws.ptr, ws.nbytes, stream_handle(stream))
+    return out, idx

@@ -101,3 +101,15 @@ def prefill_case(seed: int, p0: int, T: int, n_q: int = 16, n_kv: int = 4, lo: f
     kn = bf16_bits(g.normal(T * n_kv * 128).astype(np.float32)).reshape(T, n_kv, 128)
     vn = bf16_bits(g.normal(T * n_kv * 128).astype(np.float32)).reshape(T, n_kv, 128)
     return dict(K=K, ks=ks, V=V, vs=vs, q=q, kn=kn, vn=vn, p0=p0, T=T, n_q=n_q, n_kv=n_kv)
+
+
+def sparse_prefill_case(seed: int, p0: int, T: int, n_q: int = 16, n_kv: int = 4, n_ih: int = 4) -> dict:
+    """Config C5's sparse layer: prefill_case's cache prefix and chunk, then the indexer: fp16
+    index queries [T][n_ih][64] and keys [p0 + T][64] drawn from N(0,1), weights [T][n_ih] from
+    U(0,1). Draw order: prefill_case's, then qi, w, ki."""
+    c = prefill_case(seed, p0, T, n_q, n_kv)
+    g = SplitMix64(seed + 1000)
+    c["qi"] = f16_bits(g.normal(T * n_ih * 64)).reshape(T, n_ih, 64)
+    c["w"] = g.uniform(T * n_ih).astype(np.float32).reshape(T, n_ih)
+    c["ki"] = f16_bits(g.normal((p0 + T) * 64)).reshape(p0 + T, 64)
+    return c

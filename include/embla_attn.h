@@ -202,6 +202,21 @@ int embla_prefill_sliding(const void* q, const void* k, const void* v, void* kri
 int embla_attn_sliding8_b(const void* qkv, const void* qg, const void* kg, void* kc, void* vc, void* o, int p0, int T,
                           hipStream_t stream);
 
+/* ---------------------------------------------------------------- sparse-layer batched prefill
+ * Config C5's sparse layer: T rows at p0 .. (q bf16 [T][n_q][128]); the chunk's K, V (bf16
+ * [T][n_kv][128]) are quantised into a ROW-MAJOR int8 cache (kc, vc: [n_kv][max_s][128] int8, then
+ * fp16 scales [n_kv][max_s]: the layout a gathering reader wants). Row t (S = p0 + t + 1 keys)
+ * selects, when S > 1152, the top 1024 of keys [0, S - 128) by the ReLU² index score (index queries
+ * qi fp16 [T][4][64], weights w f32 [T][4], index keys ki fp16 [p0 + T][64]; the score is
+ * embla_index_scores' spec, bit for bit) plus the latest 128, in select_keys' order, else all S
+ * keys; softmax attention over those rows gives o bf16 [T][n_q][128]. idx (optional, [T][1152]
+ * u32) receives the selection. ws: embla_sparse_prefill_workspace_bytes(T, p0). Requires
+ * p0 + T - 128 <= 32768. */
+size_t embla_sparse_prefill_workspace_bytes(int T, int p0);
+int embla_prefill_sparse(const void* q, const void* k, const void* v, const void* qi, const float* w, const void* ki,
+                         void* kc, void* vc, void* o, uint32_t* idx, int T, int p0, int max_s, int n_q, int n_kv,
+                         void* ws, size_t ws_bytes, hipStream_t stream);
+
 /* ---------------------------------------------------------------- quantise-and-append
  * T new positions p0 .. p0+T-1 of K and V rows into an int8 layer cache (write_row8,
  * common.metal:72-84; kv_append / kv_append_b, attention.metal:113-140, prefill.metal:182-212):
