@@ -232,12 +232,47 @@ def cpu_baseline(case, L, budget_s=10.0):
                        f"{dt * 1e6:.0f} us a layer, scalar fp32 oracle, 1 thread"), out
 
 
+def traffic_probe(torch, reps=6):
+    """Dispatches for the HBM traffic counters: a C3 decode call at 32k (split-K kernel + merge)
+    and a 64 MB device copy (the counters' calibration), each after a 512 MB fill that evicts the
+    caches, so both read from HBM."""
+    from embla_attn import ops
+    regions, case = make_caches(torch, 2, 32768)
+    q = torch.from_numpy(case["q"]).cuda().view(torch.float16)
+    ws = ops.Workspace(32768, 16)
+    out = torch.empty((16, 128), dtype=torch.float16, device="cuda")
+    src = torch.empty(64 << 20, dtype=torch.uint8, device="cuda").random_(0, 255)
+    dst = torch.empty_like(src)
+    big = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+    for i in range(reps):
+        big.zero_()
+        ops.decode_int8(q, regions[i % 2][0], regions[i % 2][1], 32768, 32768, 4, ws=ws, out=out)
+        big.zero_()
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
+def measured_traffic():
+    """HBM bytes a C3 decode launch moves, from the committed counter summary (FETCH_SIZE scaled by
+    the copy calibration, plus WRITE_SIZE), or None."""
+    f = ROOT / "profiles" / "decode_c3_hbm_traffic.md"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1])
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only dispatch C3 decode layers and a 64 MB copy (each after a cache-evicting "
+                         "fill) for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs; prints nothing else")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the attention hot path runs on a "
@@ -250,6 +285,9 @@ def main():
         sys.exit(1)
     from embla_attn import _lib
     _lib.lib()   # the HIP library must load; there is no fallback path
+    if args.traffic_probe:
+        traffic_probe(torch)
+        return
 
     L = 32768
     res, case, out0, _ = bench_c3(torch, args.steps, args.warmup)
@@ -280,7 +318,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(layer_bytes(L) / (head["us_per_layer"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "kernel": "full_decode_kernel + decode_merge_kernel (one layer's decode call)",
             "per_launch_bytes": layer_bytes(L),
         },

@@ -17,6 +17,7 @@ namespace embla {
 
 constexpr int SROW = HD + 8;   // LDS row stride in 16-bit elements (272 bytes: conflict-free rows)
 constexpr int SPS = HD + 4;    // partial record stride, as decode_full.hip
+constexpr int SPR_MAXSEL = 1152;   // keys a row of the batched gathered attention (top-k + recent)
 
 template <bool BF>
 __device__ __forceinline__ f4_t mfma16s(u4_t a, u4_t b, f4_t c) {
@@ -202,17 +203,24 @@ __global__ __launch_bounds__(256) void sparse_rows8_kernel(SparseRows8Args a) {
     const int pos = a.p0 + r;
     const bool sel = a.idx && pos + 1 > a.nsel;
     const int nk = sel ? a.nsel : pos + 1;
-    const uint32_t* rows = sel ? a.idx + (size_t)r * a.idx_row_stride : nullptr;
     const int8_t* kb = a.kc + (size_t)kvh * a.max_s * HD;
     const int8_t* vb = a.vc + (size_t)kvh * a.max_s * HD;
     const size_t nrow = (size_t)a.n_kv * a.max_s * HD;
     const uint16_t* ksc = (const uint16_t*)(a.kc + nrow) + (size_t)kvh * a.max_s;
     const uint16_t* vsc = (const uint16_t*)(a.vc + nrow) + (size_t)kvh * a.max_s;
 
-    __shared__ uint16_t stage[4][2][32 * SROW];
+    // the stage (per wave: 32 K and 32 V rows as fp16) and, after the loop, the merge buffers
+    constexpr int STAGE = 4 * 2 * 32 * SROW * 2;
+    constexpr int MERGE = (4 * GQ * HD + 8 * GQ) * 4;
+    __shared__ __attribute__((aligned(16))) char smem[STAGE > MERGE ? STAGE : MERGE];
+    __shared__ uint32_t sidx[SPR_MAXSEL];
     __shared__ float sks[4][32], svs[4][32];
-    uint16_t* Ks = stage[w][0];
-    uint16_t* Vs = stage[w][1];
+    uint16_t* Ks = (uint16_t*)smem + (2 * w) * 32 * SROW;
+    uint16_t* Vs = Ks + 32 * SROW;
+
+    // the row's key list into LDS (rows clamped in range), so gathers need no dependent load
+    for (int p = tid; p < nk; p += 256) sidx[p] = (uint32_t)min(sel ? (int)a.idx[(size_t)r * a.idx_row_stride + p] : p, a.max_s - 1);
+    __syncthreads();
 
     // q^T, B operand (fp16): lane (head n, group g), MFMA u: dims 32g + 8u .. + 7
     u4_t qb[4];
@@ -231,22 +239,27 @@ __global__ __launch_bounds__(256) void sparse_rows8_kernel(SparseRows8Args a) {
 #pragma unroll
     for (int u = 0; u < 8; u++) O[u] = (f4_t){0, 0, 0, 0};
 
-    for (int t0 = 32 * w; t0 < nk; t0 += 128) {
-        // gather: load j covers keys t0 + 8j .. + 7, lane l: key t0 + 8j + l / 8, dims 16 (l % 8) ..
-        u4_t kr[4], vr[4];
+    // gather of one 32-key step: load j covers keys t0 + 8j .. + 7, lane l: key t0 + 8j + l / 8,
+    // dims 16 (l % 8) ..; lanes < 32 also fetch key t0 + l's two scales
+    u4_t kr[4], vr[4];
+    uint16_t s_k = 0, s_v = 0;
+    auto gather = [&](int t0) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int p = t0 + 8 * j + (lane >> 3);
-            const size_t row = p < nk ? (size_t)min(rows ? (int)rows[p] : p, a.max_s - 1) : 0;
+            const size_t row = p < nk ? sidx[p] : 0;
             kr[j] = ld16(kb + row * HD + 16 * (lane & 7));
             vr[j] = ld16(vb + row * HD + 16 * (lane & 7));
         }
         if (lane < 32) {
             const int p = t0 + lane;
-            const size_t row = p < nk ? (size_t)min(rows ? (int)rows[p] : p, a.max_s - 1) : 0;
-            sks[w][lane] = h2f(ksc[row]) * sc;
-            svs[w][lane] = h2f(vsc[row]) * 64.0f;
+            const size_t row = p < nk ? sidx[p] : 0;
+            s_k = ksc[row];
+            s_v = vsc[row];
         }
+    };
+    if (32 * w < nk) gather(32 * w);
+    for (int t0 = 32 * w; t0 < nk; t0 += 128) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int rr = 8 * j + (lane >> 3);
@@ -257,6 +270,8 @@ __global__ __launch_bounds__(256) void sparse_rows8_kernel(SparseRows8Args a) {
             *(h8_t*)vd = i8x8_to_h8(vr[j][0], vr[j][1]);
             *(h8_t*)(vd + 8) = i8x8_to_h8(vr[j][2], vr[j][3]);
         }
+        if (lane < 32) { sks[w][lane] = h2f(s_k) * sc; svs[w][lane] = h2f(s_v) * 64.0f; }
+        if (t0 + 128 < nk) gather(t0 + 128);   // in flight during this step's products
         wave_lds_sync();
         // S^T: lane (head n, group g) item i of half t = key 16t + 4g + i
         float x[8];
@@ -321,9 +336,11 @@ __global__ __launch_bounds__(256) void sparse_rows8_kernel(SparseRows8Args a) {
         wave_lds_sync();   // the next step's stores come after every lane's reads
     }
 
-    // ---- merge the 4 waves (LDS) and write the row's output
-    __shared__ float om[4][GQ][HD];
-    __shared__ float mm[4][GQ], ll[4][GQ];
+    // ---- merge the 4 waves (LDS, over the stage) and write the row's output
+    __syncthreads();
+    float (*om)[GQ][HD] = (float (*)[GQ][HD])smem;
+    float (*mm)[GQ] = (float (*)[GQ])(smem + 4 * GQ * HD * 4);
+    float (*ll)[GQ] = (float (*)[GQ])(smem + (4 * GQ * HD + 4 * GQ) * 4);
     l += shfl_xor(l, 16);
     l += shfl_xor(l, 32);
     if (g == 0 && n < GQ) { mm[w][n] = m; ll[w][n] = l; }
@@ -354,6 +371,8 @@ __global__ __launch_bounds__(256) void sparse_rows8_kernel(SparseRows8Args a) {
 }
 
 int launch_sparse_rows8(const SparseRows8Args& a, hipStream_t st) {
+    if (a.idx && a.nsel > SPR_MAXSEL) return EMBLA_ERR_UNSUPPORTED;
+    if (a.p0 + a.R > SPR_MAXSEL && !a.idx) return EMBLA_ERR_UNSUPPORTED;   // a row's keys must fit the list
     const dim3 grid(1, a.n_kv, a.R), block(256);
     const int gq = a.n_q / a.n_kv;
     if (gq == 4) hipLaunchKernelGGL((sparse_rows8_kernel<4>), grid, block, 0, st, a);

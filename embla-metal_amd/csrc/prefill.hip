@@ -216,12 +216,17 @@ __global__ __launch_bounds__(64 * GQ, 2) void prefill_int8_kernel(PrefillArgs a)
         // keys above kmax or at/below kmin are masked; a tile every row sees whole masks nothing
         const int kmax = full_tile ? 0x7FFFFFFF : pos;
         const int kmin = (full_tile || a.window == 0) ? -0x7FFFFFFF : pos - a.window;
-        auto run_block = [&](int kb) {
-            // S^T for keys k0 + 32kb + {8b + 4h + i}: the lane's 16 items e = 4b + i
+        // S^T for keys k0 + 32kb + {8b + 4h + i}: the lane's 16 items e = 4b + i. Both blocks'
+        // products are issued before either block's softmax, so one chain runs under the other's
+        // VALU work.
+        auto s_block = [&](int kb) -> f16_t {
             const u4_t* krow = (const u4_t*)(sm.k[b] + (32 * kb + r) * KROW) + h;
             f16_t st = mfma32x<BF>(krow[0], qb[0], (f16_t){});
 #pragma unroll
             for (int s = 1; s < 8; s++) st = mfma32x<BF>(krow[2 * s], qb[s], st);
+            return st;
+        };
+        auto run_block = [&](int kb, const f16_t& st) {
             const f4_t* ks4 = (const f4_t*)(sm.ks[b] + 32 * kb + 4 * h);   // [2b]: keys 8b + 4h ..
             const f4_t* vs4 = (const f4_t*)(sm.vs[b] + 32 * kb + 4 * h);
             float pw[16];   // P^T values (with the V scales), item e
@@ -310,10 +315,12 @@ __global__ __launch_bounds__(64 * GQ, 2) void prefill_int8_kernel(PrefillArgs a)
                 }
             }
         };
-        run_block(0);
-        run_block(1);
+        const f16_t s0 = s_block(0), s1 = s_block(1);
+        run_block(0, s0);
+        run_block(1, s1);
         if (it + 1 < ntiles) {
-            __syncthreads();          // every wave is done with buffer b ^ 1 (its previous tile)
+            // buffer b ^ 1 was last read in the previous iteration, which every wave finished
+            // before that iteration's barrier: one barrier a tile
             sstore(b ^ 1);
             __syncthreads();
         }
