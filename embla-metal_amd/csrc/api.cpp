@@ -16,6 +16,7 @@ constexpr int kPartStride = 132;
 constexpr int kRefWindow = 128;         // the reference's sliding window (Engine.swift:9)
 constexpr int kRefRing = 4096;          // the reference's ring (attention.metal:6)
 constexpr int kTopK = 1024, kRecent = 128;   // Engine.swift:9 (topk, recent)
+constexpr int kSparseRefCH = 128;        // keys a chunk of the gathered reference sparse decode
 constexpr int kIndexChunk = 2048;         // keys a workgroup of the MFMA indexer
 constexpr int kPrefillSplits = 4;       // most key-range splits of a prefill chunk (workspace sizing)
 
@@ -155,6 +156,39 @@ int embla_attn_full8(const void* qraw, const void* g1, const void* g2, const voi
     a.relu2 = true; a.scale32 = true; a.out_bf16 = true;
     (void)need;
     return launch_full_decode(a, stream);
+}
+
+int embla_attn_sparse8(const void* qraw, const void* g1, const void* g2, const void* kc, const void* vc,
+                       float* part, const uint32_t* idx, uint32_t* counter, void* o, const EmblaAttnParams* p,
+                       hipStream_t stream) {
+    if (!p || !part || !counter) return EMBLA_ERR_INVALID;
+    if (p->S <= 0 || p->maxS <= 0 || p->maxS % 32 || p->S > p->maxS) return EMBLA_ERR_INVALID;
+    Workspace w = carve(part, p->maxS, 16);
+    int rc = embla_q_prep(qraw, g1, g2, p->ng, 16 * 128, 1, 16, w.qprep, EMBLA_F16, stream);
+    if (rc) return rc;
+    (void)counter;   // no counters: the partials are merged by a second kernel
+    if (!idx) {      // SEL = 0: every key 0 .. S-1, softmax (attention.metal:448-584)
+        const int ch = p->CH > 0 ? p->CH : decode_chunk(p->S, 2);
+        if (ch % 32 || (p->S + ch - 1) / ch > kMaxChunks) return EMBLA_ERR_INVALID;
+        FullDecodeArgs a;
+        a.q = w.qprep;
+        a.kc = (const int8_t*)kc;
+        a.vc = (const int8_t*)vc;
+        a.part = w.part;
+        a.scores = nullptr;
+        a.o = (uint16_t*)o;
+        a.S = p->S; a.CH = ch; a.C = (p->S + ch - 1) / ch; a.max_s = p->maxS; a.n_q = 16; a.n_kv = 2;
+        a.relu2 = false; a.scale32 = true; a.out_bf16 = true;
+        return launch_full_decode(a, stream);
+    }
+    // SEL: the rows idx[kv head][0 .. S) of the tile cache, gathered
+    const int ch = p->CH > 0 ? p->CH : kSparseRefCH;
+    if (ch % 32 || ch > kTopK + kRecent) return EMBLA_ERR_INVALID;
+    const int C = (p->S + ch - 1) / ch;
+    if (C > kMaxChunks) return EMBLA_ERR_INVALID;
+    SparseRows8Args a{w.qprep, 0, (const int8_t*)kc, (const int8_t*)vc, idx, 0, p->S, p->S, p->S, 1,
+                      (uint16_t*)o, 0, w.part, ch, C, p->maxS, 16, 2, false, true, true, true};
+    return launch_sparse_rows8(a, stream);
 }
 
 int embla_kv_quant_append(const void* k, const void* v, int in_dtype, int stride, int T, int p0,
@@ -419,8 +453,9 @@ int embla_prefill_sparse(const void* q, const void* k, const void* v, const void
                       T, p0, kTopK, kRecent};
     if ((rc = launch_select_band(ba, stream))) return rc;
     SparseRows8Args sa{(const uint16_t*)q, (long)n_q * 128, (const int8_t*)kc, (const int8_t*)vc, sel,
-                       kTopK + kRecent, kTopK + kRecent, p0, T, (uint16_t*)o, (long)n_q * 128, max_s, n_q, n_kv,
-                       true, true};
+                       kTopK + kRecent, 0, kTopK + kRecent, p0, T, (uint16_t*)o, (long)n_q * 128, nullptr,
+                       p0 + T > kTopK + kRecent ? kTopK + kRecent : p0 + T, 1, max_s, n_q, n_kv,
+                       true, true, false, false};
     return launch_sparse_rows8(sa, stream);
 }
 

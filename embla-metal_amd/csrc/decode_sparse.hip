@@ -188,26 +188,35 @@ int launch_sparse_decode(const SparseArgs& a, hipStream_t st) {
     return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
 }
 
-/// Batched gathered attention over a row-major int8 cache: one workgroup a (query row, kv head),
-/// its 4 waves taking interleaved 32-key steps of the row's key list. A wave gathers 32 rows of K
-/// and V (each 16-byte load covers eight 128-byte rows), widens them to fp16 (exact) into its LDS
+/// Gathered attention over an int8 cache: one workgroup a (key chunk, kv head, query row), its 4
+/// waves taking interleaved 32-key steps of the chunk's key list (held in LDS, so gathers need no
+/// dependent load). A wave gathers 32 keys of K and V, widens them to fp16 (exact) into its LDS
 /// stage, and runs the same MFMA scheme as sparse_decode_kernel; each key's scale multiplies its
-/// score, each value row's scale (x 64, into fp16's normal range) its weight. Follows the sparse
-/// layer's softmax over the selected rows of an int8 cache (attention.metal:448-584), one query
-/// row at a time, for the batched prefill chunk.
-template <int GQ>
+/// score, each value row's scale (x 64, into fp16's normal range) its weight.
+///  - row-major cache (the sparse prefill's): each 16-byte load covers eight 128-byte rows, and the
+///    next step's gather is in flight during this step's products;
+///  - MFMA tile cache (the full layer's, for the reference's attn_sparse8 with SEL,
+///    attention.metal:448-584): a key's K row is 8 whole 16-byte pieces of its tile; its V row is
+///    interleaved with 7 other keys' (2 bytes of each of 64 pieces), so V is gathered 8x over.
+template <int GQ, bool TILES, bool SCALE32>
 __global__ __launch_bounds__(256) void sparse_rows8_kernel(SparseRows8Args a) {
-    const int kvh = blockIdx.y, r = blockIdx.z;
+    const int c = blockIdx.x, kvh = blockIdx.y, r = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
     const int pos = a.p0 + r;
     const bool sel = a.idx && pos + 1 > a.nsel;
-    const int nk = sel ? a.nsel : pos + 1;
-    const int8_t* kb = a.kc + (size_t)kvh * a.max_s * HD;
-    const int8_t* vb = a.vc + (size_t)kvh * a.max_s * HD;
+    const int nk_all = sel ? a.nsel : pos + 1;
+    const int j0 = c * a.CH, nk = min(nk_all, j0 + a.CH) - j0;   // this chunk's keys
     const size_t nrow = (size_t)a.n_kv * a.max_s * HD;
-    const uint16_t* ksc = (const uint16_t*)(a.kc + nrow) + (size_t)kvh * a.max_s;
-    const uint16_t* vsc = (const uint16_t*)(a.vc + nrow) + (size_t)kvh * a.max_s;
+    const int8_t* kb = TILES ? a.kc : a.kc + (size_t)kvh * a.max_s * HD;
+    const int8_t* vb = TILES ? a.vc : a.vc + (size_t)kvh * a.max_s * HD;
+    constexpr int ES = SCALE32 ? 4 : 2;
+    const char* ksc = (const char*)(a.kc + nrow) + (size_t)kvh * a.max_s * ES;
+    const char* vsc = (const char*)(a.vc + nrow) + (size_t)kvh * a.max_s * ES;
+    auto scale_at = [&](const char* base, size_t row) -> float {
+        if constexpr (SCALE32) return *(const float*)(base + row * 4);
+        else return h2f(*(const uint16_t*)(base + row * 2));
+    };
 
     // the stage (per wave: 32 K and 32 V rows as fp16) and, after the loop, the merge buffers
     constexpr int STAGE = 4 * 2 * 32 * SROW * 2;
@@ -218,8 +227,9 @@ __global__ __launch_bounds__(256) void sparse_rows8_kernel(SparseRows8Args a) {
     uint16_t* Ks = (uint16_t*)smem + (2 * w) * 32 * SROW;
     uint16_t* Vs = Ks + 32 * SROW;
 
-    // the row's key list into LDS (rows clamped in range), so gathers need no dependent load
-    for (int p = tid; p < nk; p += 256) sidx[p] = (uint32_t)min(sel ? (int)a.idx[(size_t)r * a.idx_row_stride + p] : p, a.max_s - 1);
+    // the chunk's key list into LDS (rows clamped in range)
+    const uint32_t* rows = sel ? a.idx + (size_t)r * a.idx_row_stride + (size_t)kvh * a.idx_kv_stride : nullptr;
+    for (int p = tid; p < nk; p += 256) sidx[p] = (uint32_t)min(rows ? (int)rows[j0 + p] : j0 + p, a.max_s - 1);
     __syncthreads();
 
     // q^T, B operand (fp16): lane (head n, group g), MFMA u: dims 32g + 8u .. + 7
@@ -239,11 +249,11 @@ __global__ __launch_bounds__(256) void sparse_rows8_kernel(SparseRows8Args a) {
 #pragma unroll
     for (int u = 0; u < 8; u++) O[u] = (f4_t){0, 0, 0, 0};
 
-    // gather of one 32-key step: load j covers keys t0 + 8j .. + 7, lane l: key t0 + 8j + l / 8,
-    // dims 16 (l % 8) ..; lanes < 32 also fetch key t0 + l's two scales
+    // row-major gather of one 32-key step: load j covers keys t0 + 8j .. + 7, lane l: key
+    // t0 + 8j + l / 8, dims 16 (l % 8) ..; lanes < 32 also fetch key t0 + l's two scales
     u4_t kr[4], vr[4];
-    uint16_t s_k = 0, s_v = 0;
-    auto gather = [&](int t0) {
+    float s_k = 0.0f, s_v = 0.0f;
+    auto gather_rows = [&](int t0) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int p = t0 + 8 * j + (lane >> 3);
@@ -251,27 +261,74 @@ __global__ __launch_bounds__(256) void sparse_rows8_kernel(SparseRows8Args a) {
             kr[j] = ld16(kb + row * HD + 16 * (lane & 7));
             vr[j] = ld16(vb + row * HD + 16 * (lane & 7));
         }
+    };
+    auto gather_scales = [&](int t0) {
         if (lane < 32) {
             const int p = t0 + lane;
             const size_t row = p < nk ? sidx[p] : 0;
-            s_k = ksc[row];
-            s_v = vsc[row];
+            s_k = scale_at(ksc, row);
+            s_v = scale_at(vsc, row);
         }
     };
-    if (32 * w < nk) gather(32 * w);
-    for (int t0 = 32 * w; t0 < nk; t0 += 128) {
+    // tile gather straight into the stage: lane l takes key slot l / 2, half l % 2 (64 dims)
+    auto gather_tiles = [&](int t0) {
+        const int s = lane >> 1, hf = lane & 1, p = t0 + s;
+        const int row = p < nk ? (int)sidx[p] : 0;
+        const int m16 = row & 15, t = (row >> 4) & 1, gq = (row >> 2) & 3, i = row & 3;
+        const int8_t* kt = kb + tile_base(kvh, a.max_s, row, 1);
+        const int8_t* vt = vb + tile_base(kvh, a.max_s, row, 1);
+        u4_t kp[4];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int rr = 8 * j + (lane >> 3);
-            uint16_t* kd = Ks + rr * SROW + 16 * (lane & 7);
-            uint16_t* vd = Vs + rr * SROW + 16 * (lane & 7);
-            *(h8_t*)kd = i8x8_to_h8(kr[j][0], kr[j][1]);
-            *(h8_t*)(kd + 8) = i8x8_to_h8(kr[j][2], kr[j][3]);
-            *(h8_t*)vd = i8x8_to_h8(vr[j][0], vr[j][1]);
-            *(h8_t*)(vd + 8) = i8x8_to_h8(vr[j][2], vr[j][3]);
+        for (int e = 0; e < 4; e++) {   // dims 32 (2hf + e/2) + 16 (e%2) .. + 15
+            const int gg = 2 * hf + (e >> 1), jj = e & 1;
+            kp[e] = ld16(kt + ((2 * t + jj) * 64 + m16 + 16 * gg) * 16);
         }
-        if (lane < 32) { sks[w][lane] = h2f(s_k) * sc; svs[w][lane] = h2f(s_v) * 64.0f; }
-        if (t0 + 128 < nk) gather(t0 + 128);   // in flight during this step's products
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            uint16_t* kd = Ks + s * SROW + 32 * (2 * hf + (e >> 1)) + 16 * (e & 1);
+            *(h8_t*)kd = i8x8_to_h8(kp[e][0], kp[e][1]);
+            *(h8_t*)(kd + 8) = i8x8_to_h8(kp[e][2], kp[e][3]);
+        }
+#pragma unroll
+        for (int nn = 0; nn < 8; nn++) {   // dims 8 (8hf + nn) + u, u = 0..7: 4 pieces, 2 bytes each
+            const int n2 = 8 * hf + nn;
+            u4_t vp[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) vp[j] = ld16(vt + (j * 64 + n2 + 16 * gq) * 16);
+            uint32_t lo = 0, hi = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t b0 = (vp[j][t] >> (8 * i)) & 0xFF, b1 = (vp[j][2 + t] >> (8 * i)) & 0xFF;
+                const uint32_t pair = b0 | (b1 << 8);   // dims 2j, 2j + 1
+                if (j < 2) lo |= pair << (16 * j);
+                else hi |= pair << (16 * (j - 2));
+            }
+            *(h8_t*)(Vs + s * SROW + 8 * n2) = i8x8_to_h8(lo, hi);
+        }
+    };
+    if constexpr (!TILES) {
+        if (32 * w < nk) { gather_rows(32 * w); gather_scales(32 * w); }
+    }
+    for (int t0 = 32 * w; t0 < nk; t0 += 128) {
+        if constexpr (TILES) {
+            gather_scales(t0);
+            gather_tiles(t0);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int rr = 8 * j + (lane >> 3);
+                uint16_t* kd = Ks + rr * SROW + 16 * (lane & 7);
+                uint16_t* vd = Vs + rr * SROW + 16 * (lane & 7);
+                *(h8_t*)kd = i8x8_to_h8(kr[j][0], kr[j][1]);
+                *(h8_t*)(kd + 8) = i8x8_to_h8(kr[j][2], kr[j][3]);
+                *(h8_t*)vd = i8x8_to_h8(vr[j][0], vr[j][1]);
+                *(h8_t*)(vd + 8) = i8x8_to_h8(vr[j][2], vr[j][3]);
+            }
+        }
+        if (lane < 32) { sks[w][lane] = s_k * sc; svs[w][lane] = s_v * 64.0f; }
+        if constexpr (!TILES) {
+            if (t0 + 128 < nk) { gather_rows(t0 + 128); gather_scales(t0 + 128); }   // in flight during the products
+        }
         wave_lds_sync();
         // S^T: lane (head n, group g) item i of half t = key 16t + 4g + i
         float x[8];
@@ -336,7 +393,7 @@ __global__ __launch_bounds__(256) void sparse_rows8_kernel(SparseRows8Args a) {
         wave_lds_sync();   // the next step's stores come after every lane's reads
     }
 
-    // ---- merge the 4 waves (LDS, over the stage) and write the row's output
+    // ---- merge the 4 waves (LDS, over the stage), then the row's output or this chunk's partial
     __syncthreads();
     float (*om)[GQ][HD] = (float (*)[GQ][HD])smem;
     float (*mm)[GQ] = (float (*)[GQ])(smem + 4 * GQ * HD * 4);
@@ -359,8 +416,21 @@ __global__ __launch_bounds__(256) void sparse_rows8_kernel(SparseRows8Args a) {
         f[ww] = mm[ww][oh] == NEG_INF ? 0.0f : exp2f(mm[ww][oh] - M);
         L += ll[ww][oh] * f[ww];
     }
+    const int hq = kvh * GQ + oh;
+    if (a.C > 1) {   // partial: O x 64 unnormalised, m, l (decode_merge_kernel with oscale 64)
+        float* pp = a.part + ((size_t)c * a.n_q + hq) * SPS;
+#pragma unroll
+        for (int e = 0; e < PER; e++) {
+            float s = 0.0f;
+#pragma unroll
+            for (int ww = 0; ww < 4; ww++) s += om[ww][oh][od + e] * f[ww];
+            pp[od + e] = s;
+        }
+        if (od == 0) { pp[HD] = M; pp[HD + 1] = L; }
+        return;
+    }
     const float inv = 1.0f / (64.0f * L);
-    uint16_t* orow = a.o + (size_t)r * a.o_row_stride + (size_t)(kvh * GQ + oh) * HD + od;
+    uint16_t* orow = a.o + (size_t)r * a.o_row_stride + (size_t)hq * HD + od;
 #pragma unroll
     for (int e = 0; e < PER; e++) {
         float s = 0.0f;
@@ -371,13 +441,18 @@ __global__ __launch_bounds__(256) void sparse_rows8_kernel(SparseRows8Args a) {
 }
 
 int launch_sparse_rows8(const SparseRows8Args& a, hipStream_t st) {
-    if (a.idx && a.nsel > SPR_MAXSEL) return EMBLA_ERR_UNSUPPORTED;
-    if (a.p0 + a.R > SPR_MAXSEL && !a.idx) return EMBLA_ERR_UNSUPPORTED;   // a row's keys must fit the list
-    const dim3 grid(1, a.n_kv, a.R), block(256);
+    if (a.CH > SPR_MAXSEL || a.CH <= 0 || a.C <= 0) return EMBLA_ERR_UNSUPPORTED;   // a chunk's keys fit the list
+    if (a.C > 1 && (a.R != 1 || !a.part)) return EMBLA_ERR_INVALID;
+    const dim3 grid(a.C, a.n_kv, a.R), block(256);
     const int gq = a.n_q / a.n_kv;
-    if (gq == 4) hipLaunchKernelGGL((sparse_rows8_kernel<4>), grid, block, 0, st, a);
-    else if (gq == 8) hipLaunchKernelGGL((sparse_rows8_kernel<8>), grid, block, 0, st, a);
+#define EMBLA_SR(GQ, TL, S32) hipLaunchKernelGGL((sparse_rows8_kernel<GQ, TL, S32>), grid, block, 0, st, a)
+    if (gq == 4 && !a.tiles && !a.scale32) EMBLA_SR(4, false, false);
+    else if (gq == 8 && !a.tiles && !a.scale32) EMBLA_SR(8, false, false);
+    else if (gq == 8 && a.tiles && a.scale32) EMBLA_SR(8, true, true);
+    else if (gq == 4 && a.tiles && !a.scale32) EMBLA_SR(4, true, false);
     else return EMBLA_ERR_UNSUPPORTED;
+#undef EMBLA_SR
+    if (a.C > 1) return launch_decode_merge(a.part, a.o, a.C, a.n_q, false, a.o_bf16, 64.0f, st);
     return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
 }
 

@@ -51,20 +51,25 @@ struct SparseArgs {
 };
 int launch_sparse_decode(const SparseArgs& a, hipStream_t st);
 
-/// Batched gathered attention over a row-major int8 cache (fp16 scales after the rows): query row r
-/// (position p0 + r) attends the keys idx[r][0 .. nsel) when p0 + r + 1 > nsel, else keys 0 .. p0 + r.
+/// Gathered softmax attention over an int8 cache: query row r (position p0 + r) attends the keys
+/// idx[r][0 .. nsel) (at idx + r * idx_row_stride + kv head * idx_kv_stride) when p0 + r + 1 > nsel,
+/// else keys 0 .. p0 + r. The cache is row-major ([n_kv][max_s][128] int8, the sparse prefill's) or
+/// MFMA tiles (the full layer's decode cache: tiles), then the scales (fp16, or fp32 with
+/// scale32). Keys split into C chunks of CH: C > 1 writes partials (one row, R == 1) for the merge.
 struct SparseRows8Args {
     const uint16_t* q;       // row r, head h at q + r * q_row_stride + h * 128 (fp16 or bf16)
     long q_row_stride;
-    const int8_t* kc;        // [n_kv][max_s][128] int8, then fp16 scales [n_kv][max_s]
+    const int8_t* kc;
     const int8_t* vc;
-    const uint32_t* idx;     // [R][idx_row_stride], one set a row shared by the kv heads
-    long idx_row_stride;
+    const uint32_t* idx;
+    long idx_row_stride, idx_kv_stride;
     int nsel, p0, R;
     uint16_t* o;             // row r, head h at o + r * o_row_stride + h * 128
     long o_row_stride;
+    float* part;             // [C][n_q][132] when C > 1
+    int CH, C;
     int max_s, n_q, n_kv;
-    bool q_bf16, o_bf16;
+    bool q_bf16, o_bf16, tiles, scale32;
 };
 int launch_sparse_rows8(const SparseRows8Args& a, hipStream_t st);
 

@@ -59,6 +59,7 @@ SIGNATURES = {
     "embla_prefill_workspace_bytes": (sz, [i32, i32]),
     "embla_prefill_full": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp, sz, vp]),
     "embla_relu2_prefill": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
+    "embla_attn_sparse8": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
     "embla_sparse_prefill_workspace_bytes": (sz, [i32, i32]),
     "embla_prefill_sparse": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp, sz, vp]),
     "embla_ring_append": (i32, [vp, vp, i32, i32, i32, i32, i32, vp, vp, i32, vp, vp]),

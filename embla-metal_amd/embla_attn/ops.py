@@ -72,6 +72,13 @@ def attn_full8(qraw, g1, g2, kc, vc, part, scores, counter, o, S, maxS, ng=2, CH
          _p(counter), _p(o), C.byref(p), stream_handle(stream))
 
 
+def attn_sparse8(qraw, g1, g2, kc, vc, part, idx, counter, o, S, maxS, ng=2, CH=0, stream=None):
+    """Reference-signature sparse layer (attention.metal:448-584): idx None = every key 0 .. S-1."""
+    p = _lib.AttnParams(S, CH, 0, maxS, S - 1, ng, 0, 0)
+    call("embla_attn_sparse8", _p(qraw), _p(g1), _p(g2), _p(kc), _p(vc), _p(part), _p(idx),
+         _p(counter), _p(o), C.byref(p), stream_handle(stream))
+
+
 def sliding_decode(q, k_new, v_new, kring, vring, pos, window, ring, n_kv, dtype=F16, chunk=0,
                    ws: Workspace | None = None, out=None, stream=None):
     """One decode step over a 16-bit ring: appends (k_new, v_new) at pos, attends the window."""

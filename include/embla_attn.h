@@ -228,6 +228,15 @@ int embla_kv_quant_append(const void* k, const void* v, int in_dtype, int stride
                           int n_kv, void* kc, void* vc, int max_s, int scale_dtype, int norm_k,
                           hipStream_t stream);
 
+/* Reference-signature sparse layer decode (attn_sparse8, attention.metal:448-584; Engine.swift:
+ * 799-818): q as embla_attn_full8 (raw bf16 with ng gains), 2 kv heads of the block's full layer's
+ * int8 cache (tile layout, fp32 scales), softmax. idx == NULL (SEL = 0): keys 0 .. p->S-1; else
+ * (SEL = 1) the rows idx[kv head][0 .. p->S) (u32 [2][p->S], as select_keys writes them), gathered
+ * from the tiles. part/counter as embla_attn_full8; o bf16 [16][128]. */
+int embla_attn_sparse8(const void* qraw, const void* g1, const void* g2, const void* kc, const void* vc,
+                       float* part, const uint32_t* idx, uint32_t* counter, void* o, const EmblaAttnParams* p,
+                       hipStream_t stream);
+
 /* Reference-signature kv_append (attention.metal:113-140 / prefill.metal:182-212, bound at
  * Engine.swift:782-793, Prefill.swift:315-322): T tokens of qkv rows (4096 bf16 each, position
  * pm_pos + t), njobs jobs of 2 kv heads, int8 cache with fp32 scales at byte offsets

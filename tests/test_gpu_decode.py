@@ -95,3 +95,45 @@ def test_full8_reference_mode(torch_gpu, orc):
     # scores carry q's 15-bit fixed point (|q error| <= absmax(q)/64000): 1e-3 of their scale
     assert_close(scores.cpu().numpy()[:, :S], ref_sc, atol=1e-3 * np.abs(ref_sc).max(), rtol=0, what="full8 scores")
     assert not counter.cpu().numpy().any()
+
+
+@pytest.mark.parametrize("sel", [True, False])
+def test_sparse8_reference_mode(torch_gpu, orc, sel):
+    """attn_sparse8: raw bf16 q with two gains, 2 kv heads of the full layer's tile cache (fp32
+    scales), softmax over the selected rows idx[kv head][0 .. 1152) (SEL) or every key."""
+    import torch
+    from embla_attn import ops, _lib
+    say(f"attn_sparse8 reference mode sel={sel}")
+    S_cache, max_s = 5000, 5024
+    g = synth.SplitMix64(41)
+    qraw = synth.bf16_bits(g.normal(16 * 128) * 2)
+    g1 = synth.bf16_bits(g.normal(128) * 0.2)
+    g2 = synth.bf16_bits(g.normal(128) * 0.2)
+    K = g.int8(2 * S_cache * 128).reshape(2, S_cache, 128)
+    V = g.int8(2 * S_cache * 128).reshape(2, S_cache, 128)
+    ks = (0.02 + 0.01 * g.uniform(2 * S_cache)).astype(np.float32).reshape(2, S_cache)
+    vs = (0.02 + 0.01 * g.uniform(2 * S_cache)).astype(np.float32).reshape(2, S_cache)
+    kc = dev(layout.pack_region(K, ks, max_s, "k"))
+    vc = dev(layout.pack_region(V, vs, max_s, "v"))
+    part = torch.zeros(_lib.lib().embla_workspace_bytes(max_s, 16), dtype=torch.uint8, device="cuda")
+    counter = torch.zeros(2, dtype=torch.int32, device="cuda")
+    o = torch.empty((16, 128), dtype=torch.bfloat16, device="cuda")
+    qn = np.stack([orc.head_norm(synth.bf16_val(qraw.reshape(16, 128)[h]), synth.bf16_val(g1), synth.bf16_val(g2), 2)
+                   for h in range(16)])
+    if sel:
+        # per kv head: 1024 distinct rows in shuffled order (every tile position, both halves), then
+        # the latest 128; the order of the list is irrelevant to the result
+        rows = np.zeros((2, 1152), np.uint32)
+        for h in range(2):
+            r = (g.next(S_cache - 128) % np.uint64(1 << 62)).astype(np.float64)
+            rows[h, :1024] = np.argsort(r)[:1024].astype(np.uint32)
+            rows[h, 1024:] = np.arange(S_cache - 128, S_cache, dtype=np.uint32)
+        ops.attn_sparse8(dev(qraw, torch.bfloat16), dev(g1, torch.bfloat16), dev(g2, torch.bfloat16), kc, vc, part,
+                         dev(rows.view(np.int32)), counter, o, 1152, max_s)
+        ref = orc.decode_int8(qn, K, ks, V, vs, weights=0, rows=rows, n_sel=1152)
+    else:
+        ops.attn_sparse8(dev(qraw, torch.bfloat16), dev(g1, torch.bfloat16), dev(g2, torch.bfloat16), kc, vc, part,
+                         None, counter, o, S_cache, max_s)
+        ref = orc.decode_int8(qn, K, ks, V, vs, weights=0)
+    torch.cuda.synchronize()
+    assert_close(bf16_host(o), ref, what=f"sparse8 sel={sel}")
