@@ -23,8 +23,8 @@ constexpr int kPrefillSplits = 4;       // most key-range splits of a prefill ch
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 /// Key-range splits of a prefill launch: as many as keep every split >= 4 key tiles while the grid
-/// is under 512 workgroups (2 a CU: the kernel runs 2 waves a SIMD), at most kPrefillSplits, and
-/// only with a workspace for the partial rows. EMBLA_PREFILL_SPLITS caps it (tuning).
+/// is under 256 workgroups (one a CU: 8 waves, 2 a SIMD), at most kPrefillSplits, and only with a
+/// workspace for the partial rows. EMBLA_PREFILL_SPLITS caps it (tuning).
 int prefill_splits(const void* ws, size_t ws_bytes, int T, int n_q, int blocks, int tiles) {
     if (!ws || ws_bytes < (size_t)kPrefillSplits * T * n_q * kPartStride * 4) return 1;
     static const int cap = [] {
@@ -32,7 +32,7 @@ int prefill_splits(const void* ws, size_t ws_bytes, int T, int n_q, int blocks, 
         return e ? atoi(e) : 2;
     }();
     int ns = 1;
-    while (ns * 2 <= cap && ns * 2 <= kPrefillSplits && blocks * ns < 512 && tiles / (ns * 2) >= 4) ns *= 2;
+    while (ns * 2 <= cap && ns * 2 <= kPrefillSplits && blocks * ns < 256 && tiles / (ns * 2) >= 4) ns *= 2;
     return ns;
 }
 
@@ -345,7 +345,8 @@ int embla_prefill_int8(const void* q, int q_dtype, long q_tok_stride, long q_hea
     a.T = T; a.p0 = p0; a.max_s = max_s; a.n_q = n_q; a.n_kv = n_kv; a.window = window;
     // two key-range splits when a workspace is given and the blocks are too few to fill the GPU
     // with two waves a SIMD (the split partials cost one merge pass)
-    const int blocks = (T + 31) / 32 * n_kv;
+    const int gqw = n_q / n_kv, rows_wg = gqw >= 1 && gqw <= 8 ? 32 * (8 / gqw) : 32;   // query rows a workgroup
+    const int blocks = (T + rows_wg - 1) / rows_wg * n_kv;
     a.nsplit = prefill_splits(ws, ws_bytes, T, n_q, blocks,
                               window > 0 ? min((p0 + T) / 64, (window + 63) / 64 + 1) : (p0 + T) / 64);
     a.part = (float*)ws;
@@ -393,7 +394,8 @@ int embla_prefill_ring(const void* q, int dtype, long q_tok_stride, long q_head_
     a.kc = nullptr; a.vc = nullptr;
     a.o = (uint16_t*)o; a.o_tok_stride = o_tok_stride; a.o_head_stride = o_head_stride;
     a.T = T; a.p0 = p0; a.max_s = ring; a.n_q = n_q; a.n_kv = n_kv; a.window = window;
-    const int blocks = (T + 31) / 32 * n_kv;
+    const int gqw = n_q / n_kv, rows_wg = gqw >= 1 && gqw <= 8 ? 32 * (8 / gqw) : 32;   // query rows a workgroup
+    const int blocks = (T + rows_wg - 1) / rows_wg * n_kv;
     a.nsplit = prefill_splits(ws, ws_bytes, T, n_q, blocks, (window + 63) / 64 + 1);
     a.part = (float*)ws;
     a.relu2 = false; a.scale32 = false; a.q_bf16 = dtype == EMBLA_BF16; a.out_bf16 = dtype == EMBLA_BF16;

@@ -29,8 +29,9 @@ constexpr int PBK = 64;            // keys a staged tile
 constexpr int KROW = HD + 8;       // LDS row stride of K (fp16 elements): conflict-free 16 B reads
 // V is staged as an fp16 copy of its global tile order: a 32-key tile is 8 rows u (dim % 8) of 64
 // lane slots (n + 16g) of 16 bytes, each slot the 8 keys {16t + 4g + i} of dim 8n + u. Rows are
-// padded by 16 bytes so the A-operand reads (8 lanes, rows u = 0..7) hit distinct banks.
-constexpr int VUROW = 64 * 8 + 8;  // fp16 elements a padded row u
+// padded by 32 bytes: a 128-bit LDS read is served 16 lanes a pass over 64 banks, and the A-operand
+// reads of 16 lanes (rows u = 0..7, slots n and n + 1) then sit at 16-byte offsets distinct mod 16.
+constexpr int VUROW = 64 * 8 + 16; // fp16 elements a padded row u
 constexpr int VTILE = 8 * VUROW;   // fp16 elements a staged 32-key V tile
 
 __device__ __forceinline__ f16_t mfma32(h8v a, h8v b, f16_t c) {
@@ -46,29 +47,59 @@ __device__ __forceinline__ f16_t mfma32x(u4_t a, u4_t b, f16_t c) {
 struct __attribute__((aligned(16))) PrefillSmem {
     _Float16 k[2][PBK * KROW];
     _Float16 vt[2][2 * VTILE];
-    float ks[2][PBK], vs[2][PBK];
 };
 
 constexpr int PPS = HD + 4;        // floats a split partial row: O[128], m, l, pad
+constexpr int PF_WAVES = 8;        // waves a workgroup: GQ query heads x (8 / GQ) 32-row blocks
 int launch_prefill_tail(const PrefillArgs& a, hipStream_t st);
 
+/// Scales of the four keys kt + 4g .. + 3 (fp16 pair or fp32 quad) as fp32.
+template <bool SCALE32>
+__device__ __forceinline__ void scales4(const char* base, size_t idx, float* out) {
+    if constexpr (SCALE32) {
+        const u4_t r = ld16(base + idx * 4);
+#pragma unroll
+        for (int i = 0; i < 4; i++) out[i] = __uint_as_float(r[i]);
+    } else {
+        const u2_t r = ld8(base + idx * 2);
+        out[0] = h2f((uint16_t)(r[0] & 0xFFFF));
+        out[1] = h2f((uint16_t)(r[0] >> 16));
+        out[2] = h2f((uint16_t)(r[1] & 0xFFFF));
+        out[3] = h2f((uint16_t)(r[1] >> 16));
+    }
+}
+/// 16 int8 as fp16, each times its scale (pairs of fp16 scales), into two 16-byte halves.
+__device__ __forceinline__ h8_t i8x8_scaled(uint32_t a, uint32_t b, h2_t s01, h2_t s23, h2_t s45, h2_t s67) {
+    h8_t x = i8x8_to_h8(a, b);
+    h2_t* p = (h2_t*)&x;
+    p[0] = p[0] * s01;
+    p[1] = p[1] * s23;
+    p[2] = p[2] * s45;
+    p[3] = p[3] * s67;
+    return x;
+}
+
 // RING: K/V from a 16-bit ring (no scales; S = K·Q^T on the MFMA in the ring's type, BF = bf16;
-// V staged as fp16); else from an int8 region (fp16 MFMA). PRE: q normed with gains, rotated, bf16-rounded in-kernel.
+// V staged as fp16); else from an int8 region (fp16 MFMA), each key's K scale (with 1/√128, and
+// log2 e for softmax) and V scale multiplied into its staged fp16 row. PRE: q normed with gains,
+// rotated, bf16-rounded in-kernel.
 template <int GQ, bool RELU2, bool SCALE32, bool QBF, bool OBF, bool RING = false, bool BF = false, bool PRE = false>
-__global__ __launch_bounds__(64 * GQ, 2) void prefill_int8_kernel(PrefillArgs a) {
-    constexpr int NT = 64 * GQ;
+__global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillArgs a) {
+    constexpr int NT = 64 * PF_WAVES;
+    constexpr int RB = PF_WAVES / GQ;                       // 32-row blocks a workgroup
     __shared__ PrefillSmem sm;
     const int tb = blockIdx.x, kvh = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int r = lane & 31, h = lane >> 5;
-    const int hq = kvh * GQ + w;
-    const int tok0 = tb * 32, tok = tok0 + r;                 // this lane's query row
+    const int hq = kvh * GQ + w % GQ;
+    const int wt0 = tb * 32 * RB;                             // the workgroup's first token
+    const int tok0 = wt0 + 32 * (w / GQ), tok = tok0 + r;     // this wave's rows, this lane's row
     const bool row_ok = tok < a.T;
     const int pos = a.p0 + min(tok, a.T - 1);                  // its position
-    const int last_tok = min(tok0 + 31, a.T - 1);
-    const int hi = a.p0 + last_tok;                            // last key the block needs
+    const int last_tok = min(tok0 + 31, a.T - 1);              // the wave's last row
+    const int hi = a.p0 + min(wt0 + 32 * RB - 1, a.T - 1);     // last key the workgroup needs
     int lo = 0;
-    if (a.window > 0) lo = max(0, a.p0 + tok0 - a.window + 1);
+    if (a.window > 0) lo = max(0, a.p0 + wt0 - a.window + 1);
     const int kfirst = lo & ~(PBK - 1);
     const int ntot = (hi - kfirst) / PBK + 1;
     // split z of nsplit takes an equal share of the block's key tiles (the prefix splits evenly)
@@ -76,49 +107,63 @@ __global__ __launch_bounds__(64 * GQ, 2) void prefill_int8_kernel(PrefillArgs a)
     const int kstart = kfirst + t_lo * PBK;
     const int ntiles = t_hi - t_lo;
 
+    // score scale: folded into the staged K rows for int8, applied to S for a ring
     const float c = RELU2 ? 0.08838834764831845f : 0.08838834764831845f * 1.4426950408889634f;
     const size_t nrow = (size_t)a.n_kv * a.max_s * HD;
     const char* ksb = (const char*)(a.kc + nrow);
     const char* vsb = (const char*)(a.vc + nrow);
+    constexpr int ES = SCALE32 ? 4 : 2;
 
     // ---- staging: each thread moves 16-byte pieces of the two 32-key global tiles of a 64-key tile
-    constexpr int ES = RING ? 2 : 1;
-    constexpr int PIECES = 2 * 256 * ES;          // 16-byte pieces a 64-key tile, K (same for V)
+    constexpr int EB = RING ? 2 : 1;
+    constexpr int PIECES = 2 * 256 * EB;          // 16-byte pieces a 64-key tile, K (same for V)
     constexpr int PER = PIECES / NT;              // pieces a thread
-    u4_t kr[PER], vr[PER];
-    uint32_t sr = 0;                              // a scale (threads 0 .. 2*PBK-1)
-    auto tile_addr = [&](int key) -> size_t {     // byte offset of the 32-key tile holding key
-        if constexpr (RING) return tile_base(kvh, a.R, key % a.R, 2);
-        // a 64-key tile's second half may lie past max_s (max_s % 64 == 32): read the first
-        // half again; those keys are past every row's position and masked
-        else return tile_base(kvh, a.max_s, min(key, a.max_s - 32), 1);
+    static_assert(PER >= 1, "a piece a thread at least");
+    struct Stage {
+        u4_t kr[PER], vr[PER];
+        float ksr[PER], vsr[PER][8];              // int8: the pieces' scales
     };
-    auto gload = [&](int k0) {
+    Stage SA, SB;                                 // two tiles' loads in flight
+    auto tile_key = [&](int key) -> int {         // the 32-key tile's first key, clamped in range
+        // a 64-key tile's second half may lie past max_s (max_s % 64 == 32): read the first half
+        // again; those keys are past every row's position and masked
+        return RING ? key : min(key, a.max_s - 32);
+    };
+    auto gload = [&](int k0, Stage& S) {
+        u4_t* kr = S.kr;
+        u4_t* vr = S.vr;
+        float* ksr = S.ksr;
+        float (*vsr)[8] = S.vsr;
 #pragma unroll
         for (int i = 0; i < PER; i++) {
-            const int q = tid + NT * i, gt = q / (256 * ES);
-            const size_t off = tile_addr(k0 + 32 * gt) + (size_t)(q % (256 * ES)) * 16;
+            const int q = tid + NT * i, gt = q / (256 * EB), jl = q % (256 * EB);
             if constexpr (RING) {
+                const size_t off = tile_base(kvh, a.R, (k0 + 32 * gt) % a.R, 2) + (size_t)jl * 16;
                 kr[i] = ld16((const char*)a.kring + off);
                 vr[i] = ld16((const char*)a.vring + off);
             } else {
+                const int kt = tile_key(k0 + 32 * gt);
+                const size_t off = tile_base(kvh, a.max_s, kt, 1) + (size_t)jl * 16;
                 kr[i] = ld16(a.kc + off);
                 vr[i] = ld16(a.vc + off);
-            }
-        }
-        if constexpr (!RING) {
-            if (tid < 2 * PBK) {
-                const int key = k0 + (tid & (PBK - 1));
-                const char* sb = tid < PBK ? ksb : vsb;
-                const size_t si = (size_t)kvh * a.max_s + min(key, a.max_s - 1);
-                sr = SCALE32 ? *(const uint32_t*)(sb + si * 4) : (uint32_t)*(const uint16_t*)(sb + si * 2);
+                const int j = jl >> 6, l = jl & 63;
+                // K piece: key kt + 16 (j / 2) + l % 16; V piece: keys kt + 16t + 4 (l / 16) + i
+                const size_t kidx = (size_t)kvh * a.max_s + kt + 16 * (j >> 1) + (l & 15);
+                ksr[i] = SCALE32 ? *(const float*)(ksb + kidx * 4) : h2f(*(const uint16_t*)(ksb + kidx * 2));
+                const size_t vidx = (size_t)kvh * a.max_s + kt + 4 * (l >> 4);
+                scales4<SCALE32>(vsb, vidx, vsr[i]);
+                scales4<SCALE32>(vsb, vidx + 16, vsr[i] + 4);
             }
         }
     };
-    auto sstore = [&](int b) {
+    auto sstore = [&](int b, const Stage& S) {
+        const u4_t* kr = S.kr;
+        const u4_t* vr = S.vr;
+        const float* ksr = S.ksr;
+        const float (*vsr)[8] = S.vsr;
 #pragma unroll
         for (int i = 0; i < PER; i++) {
-            const int q = tid + NT * i, gt = q / (256 * ES), j = (q % (256 * ES)) >> 6, l = q & 63;
+            const int q = tid + NT * i, gt = q / (256 * EB), j = (q % (256 * EB)) >> 6, l = q & 63;
             if constexpr (RING) {
                 // K piece (j, l): key 16 (j / 4) + l % 16, dims 32 (l / 16) + 8 (j % 4) .. + 7
                 const int key = 32 * gt + 16 * (j >> 2) + (l & 15), d0 = 32 * (l >> 4) + 8 * (j & 3);
@@ -129,21 +174,21 @@ __global__ __launch_bounds__(64 * GQ, 2) void prefill_int8_kernel(PrefillArgs a)
                 if constexpr (BF) vv = __builtin_bit_cast(u4_t, bf8_to_h8(vv));
                 *(u4_t*)(sm.vt[b] + gt * VTILE + j * VUROW + l * 8) = vv;
             } else {
-                // K piece (j, l): key 16 (j / 2) + l % 16, dims 32 (l / 16) + 16 (j % 2) .. + 15
+                // K piece (j, l): key 16 (j / 2) + l % 16, dims 32 (l / 16) + 16 (j % 2) .. + 15,
+                // times its scale · c
                 const int key = 32 * gt + 16 * (j >> 1) + (l & 15), d0 = 32 * (l >> 4) + 16 * (j & 1);
-                *(h8_t*)(sm.k[b] + key * KROW + d0) = i8x8_to_h8(kr[i][0], kr[i][1]);
-                *(h8_t*)(sm.k[b] + key * KROW + d0 + 8) = i8x8_to_h8(kr[i][2], kr[i][3]);
-                // V piece (j, l): rows u = 2j, 2j + 1 of slot l, 8 keys each: straight copies as fp16
+                const _Float16 sk = (_Float16)(ksr[i] * c);
+                const h2_t s2 = {sk, sk};
+                *(h8_t*)(sm.k[b] + key * KROW + d0) = i8x8_scaled(kr[i][0], kr[i][1], s2, s2, s2, s2);
+                *(h8_t*)(sm.k[b] + key * KROW + d0 + 8) = i8x8_scaled(kr[i][2], kr[i][3], s2, s2, s2, s2);
+                // V piece (j, l): rows u = 2j, 2j + 1 of slot l, 8 keys {16t + 4g + i} each (item
+                // 4t + i), times their scales
+                const h2_t v01 = {(_Float16)vsr[i][0], (_Float16)vsr[i][1]}, v23 = {(_Float16)vsr[i][2], (_Float16)vsr[i][3]};
+                const h2_t v45 = {(_Float16)vsr[i][4], (_Float16)vsr[i][5]}, v67 = {(_Float16)vsr[i][6], (_Float16)vsr[i][7]};
                 _Float16* base = sm.vt[b] + gt * VTILE + l * 8;
-                *(h8_t*)(base + (2 * j) * VUROW) = i8x8_to_h8(vr[i][0], vr[i][1]);
-                *(h8_t*)(base + (2 * j + 1) * VUROW) = i8x8_to_h8(vr[i][2], vr[i][3]);
+                *(h8_t*)(base + (2 * j) * VUROW) = i8x8_scaled(vr[i][0], vr[i][1], v01, v23, v45, v67);
+                *(h8_t*)(base + (2 * j + 1) * VUROW) = i8x8_scaled(vr[i][2], vr[i][3], v01, v23, v45, v67);
             }
-        }
-        if (tid < 2 * PBK) {
-            const float v = RING ? 1.0f : (SCALE32 ? __uint_as_float(sr) : h2f((uint16_t)sr));
-            // scores: scale_k * (1/sqrt(128)) [* log2 e]; weights: scale_v [* 64 into fp16's range]
-            if (tid < PBK) sm.ks[b][tid] = v * c;
-            else sm.vs[b][tid - PBK] = RELU2 ? v : v * 64.0f;
         }
     };
 
@@ -204,15 +249,17 @@ __global__ __launch_bounds__(64 * GQ, 2) void prefill_int8_kernel(PrefillArgs a)
 #pragma unroll
         for (int e = 0; e < 16; e++) O[i][e] = 0.0f;
 
-    if (ntiles > 0) {
-        gload(kstart);
-        sstore(0);
-    }
+    if (ntiles > 0) gload(kstart, SA);
+    if (ntiles > 1) gload(kstart + PBK, SB);
+    if (ntiles > 0) sstore(0, SA);
     __syncthreads();
-    for (int it = 0; it < ntiles; it++) {
+    // tile it: products from LDS buffer it % 2; tile it + 2's loads go out first (into the set
+    // tile it was staged from), tile it + 1 is staged at the end: two tiles of latency hidden
+    auto iteration = [&](int it, Stage& ld_set, const Stage& st_set) {
         const int b = it & 1, k0 = kstart + it * PBK;
-        if (it + 1 < ntiles) gload(k0 + PBK);   // in flight during this tile's products
+        if (it + 2 < ntiles) gload(k0 + 2 * PBK, ld_set);
         const bool full_tile = k0 + PBK - 1 <= a.p0 + tok0 && (a.window == 0 || k0 >= a.p0 + last_tok - a.window + 1);
+        const bool dead = k0 > a.p0 + last_tok;   // past every row of this wave: nothing to add
         // keys above kmax or at/below kmin are masked; a tile every row sees whole masks nothing
         const int kmax = full_tile ? 0x7FFFFFFF : pos;
         const int kmin = (full_tile || a.window == 0) ? -0x7FFFFFFF : pos - a.window;
@@ -226,48 +273,51 @@ __global__ __launch_bounds__(64 * GQ, 2) void prefill_int8_kernel(PrefillArgs a)
             for (int s = 1; s < 8; s++) st = mfma32x<BF>(krow[2 * s], qb[s], st);
             return st;
         };
-        auto run_block = [&](int kb, const f16_t& st) {
-            const f4_t* ks4 = (const f4_t*)(sm.ks[b] + 32 * kb + 4 * h);   // [2b]: keys 8b + 4h ..
-            const f4_t* vs4 = (const f4_t*)(sm.vs[b] + 32 * kb + 4 * h);
-            float pw[16];   // P^T values (with the V scales), item e
-            if constexpr (RELU2) {
+        // P^T B operands (fp16) of a block's two 16-key k-steps: step s = items b = s (slots
+        // 0..3) and b = 2 + s (slots 4..7)
+        auto pack = [&](const float* pw, u4_t* pb) {
 #pragma unroll
-                for (int bb = 0; bb < 4; bb++) {
-                    const f4_t kq = ks4[2 * bb], vq = vs4[2 * bb];
+            for (int s = 0; s < 2; s++)
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const int e = 4 * bb + i;
-                        const int key = k0 + 32 * kb + 8 * bb + 4 * h + i;
-                        const bool ok = key <= kmax && key > kmin;
-                        const float t = fmaxf(st[e] * kq[i], 0.0f);
-                        const float p = ok ? t * t : 0.0f;
-                        lsum += p;
-                        pw[4 * bb + i] = p * vq[i];
-                    }
+                for (int q2 = 0; q2 < 4; q2++) {
+                    const int e0 = (q2 < 2 ? 4 * s : 4 * (2 + s)) + 2 * (q2 & 1);
+                    pb[s][q2] = __builtin_bit_cast(uint32_t, (h2_t){(_Float16)pw[e0], (_Float16)pw[e0 + 1]});
                 }
-            } else {
-                float x[16];
+        };
+        // O^T (dims 32i + {8b + 4h + i}) += V^T P^T over two 16-key k-steps: in step s lane
+        // (dim 32i + r, h) takes slot (n = dim / 8, g = 2s + h) of row u = dim % 8, whose 8 keys
+        // {8s + 4h + i, 16 + 8s + 4h + i} are the P^T items b = s and b = 2 + s
+        auto pv = [&](int kb, const u4_t* pb) {
+            const u4_t* vt = (const u4_t*)(sm.vt[b] + kb * VTILE);
 #pragma unroll
-                for (int bb = 0; bb < 4; bb++) {
-                    const f4_t kq = ks4[2 * bb];
+            for (int s = 0; s < 2; s++)
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        x[4 * bb + i] = st[4 * bb + i] * kq[i];
-                    }
+                for (int i = 0; i < 4; i++) {
+                    const int dim = 32 * i + r;
+                    O[i] = mfma32x<false>(vt[(dim & 7) * (VUROW / 8) + (dim >> 3) + 16 * (2 * s + h)], pb[s], O[i]);
                 }
-                if (!full_tile) {   // uniform: only the diagonal (and window-edge) tiles
+        };
+        if (!dead) {   // uniform a wave
+            const f16_t s0 = s_block(0), s1 = s_block(1);
+            // scores of the tile's 64 keys: item e of block kb is x[16 kb + e]
+            float x[32];
 #pragma unroll
-                    for (int e = 0; e < 16; e++) {
-                        const int key = k0 + 32 * kb + 8 * (e >> 2) + 4 * h + (e & 3);
-                        x[e] = key <= kmax && key > kmin ? x[e] : NEG_INF;
-                    }
+            for (int e = 0; e < 16; e++) { x[e] = RING ? s0[e] * c : s0[e]; x[16 + e] = RING ? s1[e] * c : s1[e]; }
+            if (!full_tile) {   // uniform: only the diagonal (and window-edge) tiles
+#pragma unroll
+                for (int e = 0; e < 32; e++) {
+                    const int key = k0 + 32 * (e >> 4) + 8 * ((e & 15) >> 2) + 4 * h + (e & 3);
+                    x[e] = key <= kmax && key > kmin ? x[e] : (RELU2 ? 0.0f : NEG_INF);
                 }
+            }
+            float msub = 0.0f;
+            if constexpr (!RELU2) {
                 float mt = fmaxf(x[0], x[1]);
 #pragma unroll
-                for (int e = 2; e < 16; e += 2) mt = fmaxf(mt, fmaxf(x[e], x[e + 1]));
+                for (int e = 2; e < 32; e += 2) mt = fmaxf(mt, fmaxf(x[e], x[e + 1]));
                 mt = fmaxf(mt, shfl_xor(mt, 32));
                 // the running maximum moves only when a row's grows by more than 2^8: weights stay
-                // <= 256 (fp16-safe after the 64 * scale_v prescale), O and l share the stale m
+                // <= 256 (fp16-safe), O and l share the stale m
                 if (__any(mt > m + 8.0f)) {
                     const float mn = fmaxf(m, mt);
                     const float corr = m == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
@@ -280,50 +330,44 @@ __global__ __launch_bounds__(64 * GQ, 2) void prefill_int8_kernel(PrefillArgs a)
                 }
                 // a masked key gives exp2(-inf) = 0; a row whose every key so far is masked keeps
                 // m = -inf: subtracting +inf instead keeps its weights 0 (not exp2(-inf + inf))
-                const float msub = m == NEG_INF ? -NEG_INF : m;
-#pragma unroll
-                for (int bb = 0; bb < 4; bb++) {
-                    const f4_t vq = vs4[2 * bb];
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const float p = __builtin_amdgcn_exp2f(x[4 * bb + i] - msub);
-                        lsum += p;
-                        pw[4 * bb + i] = p * vq[i];
-                    }
-                }
+                msub = m == NEG_INF ? -NEG_INF : m;
             }
-            // P^T B operands (fp16) of the two 16-key k-steps: step s = items b = s (slots 0..3)
-            // and b = 2 + s (slots 4..7)
-            u4_t pb[2];
-#pragma unroll
-            for (int s = 0; s < 2; s++)
-#pragma unroll
-                for (int q2 = 0; q2 < 4; q2++) {
-                    const int e0 = (q2 < 2 ? 4 * s : 4 * (2 + s)) + 2 * (q2 & 1);
-                    pb[s][q2] = __builtin_bit_cast(uint32_t, (h2_t){(_Float16)pw[e0], (_Float16)pw[e0 + 1]});
+            auto weight = [&](float v) -> float {
+                if constexpr (RELU2) {
+                    const float t = fmaxf(v, 0.0f);
+                    return t * t;
+                } else {
+                    return __builtin_amdgcn_exp2f(v - msub);
                 }
-            // O^T (dims 32i + {8b + 4h + i}) += V^T P^T over two 16-key k-steps: in step s lane
-            // (dim 32i + r, h) takes slot (n = dim / 8, g = 2s + h) of row u = dim % 8, whose 8 keys
-            // {8s + 4h + i, 16 + 8s + 4h + i} are the P^T items b = s and b = 2 + s
-            const u4_t* vt = (const u4_t*)(sm.vt[b] + kb * VTILE);
+            };
+            float pw[16];
+            u4_t pb0[2], pb1[2];
 #pragma unroll
-            for (int s = 0; s < 2; s++) {
+            for (int e = 0; e < 16; e++) { pw[e] = weight(x[e]); lsum += pw[e]; }
+            pack(pw, pb0);
+            // block 0's products run while block 1's weights are computed: one MFMA, then VALU
+            pv(0, pb0);
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int dim = 32 * i + r;
-                    O[i] = mfma32x<false>(vt[(dim & 7) * (VUROW / 8) + (dim >> 3) + 16 * (2 * s + h)], pb[s], O[i]);
-                }
+            for (int e = 0; e < 16; e++) { pw[e] = weight(x[16 + e]); lsum += pw[e]; }
+            pack(pw, pb1);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // a V operand read
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // an MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);   // six VALU
             }
-        };
-        const f16_t s0 = s_block(0), s1 = s_block(1);
-        run_block(0, s0);
-        run_block(1, s1);
+            pv(1, pb1);
+        }
         if (it + 1 < ntiles) {
             // buffer b ^ 1 was last read in the previous iteration, which every wave finished
             // before that iteration's barrier: one barrier a tile
-            sstore(b ^ 1);
+            sstore(b ^ 1, st_set);
             __syncthreads();
         }
+    };
+    for (int it = 0; it < ntiles; it += 2) {
+        iteration(it, SA, SB);
+        if (it + 1 < ntiles) iteration(it + 1, SB, SA);
     }
 
     // ---- normalise and store: lane (row r, half h) holds dims 32i + 8b + 4h .. + 3
@@ -339,7 +383,7 @@ __global__ __launch_bounds__(64 * GQ, 2) void prefill_int8_kernel(PrefillArgs a)
         if (h == 0) { pp[HD] = m; pp[HD + 1] = lsum; }
         return;
     }
-    const float inv = RELU2 ? 1.0f / (11.313708498984761f + lsum) : 1.0f / (64.0f * lsum);
+    const float inv = RELU2 ? 1.0f / (11.313708498984761f + lsum) : 1.0f / lsum;
     uint16_t* orow = a.o + (size_t)tok * a.o_tok_stride + (size_t)hq * a.o_head_stride;
 #pragma unroll
     for (int i = 0; i < 4; i++)
@@ -371,16 +415,16 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
         o0 += pp[2 * lane] * f;
         o1 += pp[2 * lane + 1] * f;
     }
-    const float inv = RELU2 ? 1.0f / (11.313708498984761f + L) : 1.0f / (64.0f * L);
+    const float inv = RELU2 ? 1.0f / (11.313708498984761f + L) : 1.0f / L;
     uint16_t* orow = a.o + (size_t)tok * a.o_tok_stride + (size_t)hq * a.o_head_stride;
     *(uint32_t*)(orow + 2 * lane) = (uint32_t)f2a<OBF>(o0 * inv) | ((uint32_t)f2a<OBF>(o1 * inv) << 16);
 }
 
 int launch_prefill_int8(const PrefillArgs& a, hipStream_t st) {
     const int gq = a.n_q / a.n_kv;
-    const dim3 grid((a.T + 31) / 32, a.n_kv, a.nsplit);
+    const dim3 grid((a.T + 32 * (PF_WAVES / gq) - 1) / (32 * (PF_WAVES / gq)), a.n_kv, a.nsplit);
 #define EMBLA_PF(GQ, R, S32, QBF, OBF) \
-    hipLaunchKernelGGL((prefill_int8_kernel<GQ, R, S32, QBF, OBF>), grid, dim3(64 * GQ), 0, st, a)
+    hipLaunchKernelGGL((prefill_int8_kernel<GQ, R, S32, QBF, OBF>), grid, dim3(64 * PF_WAVES), 0, st, a)
     if (gq == 4 && !a.relu2 && !a.scale32 && a.q_bf16 && a.out_bf16) EMBLA_PF(4, false, false, true, true);
     else if (gq == 4 && !a.relu2 && !a.scale32 && !a.q_bf16 && !a.out_bf16) EMBLA_PF(4, false, false, false, false);
     else if (gq == 8 && a.relu2 && a.scale32 && a.q_bf16 && a.out_bf16) EMBLA_PF(8, true, true, true, true);
@@ -392,9 +436,9 @@ int launch_prefill_int8(const PrefillArgs& a, hipStream_t st) {
 
 int launch_prefill_ring(const PrefillArgs& a, hipStream_t st) {
     const int gq = a.n_q / a.n_kv;
-    const dim3 grid((a.T + 31) / 32, a.n_kv, a.nsplit);
+    const dim3 grid((a.T + 32 * (PF_WAVES / gq) - 1) / (32 * (PF_WAVES / gq)), a.n_kv, a.nsplit);
 #define EMBLA_PR(BF, PRE) \
-    hipLaunchKernelGGL((prefill_int8_kernel<4, false, false, BF, BF, true, BF, PRE>), grid, dim3(256), 0, st, a)
+    hipLaunchKernelGGL((prefill_int8_kernel<4, false, false, BF, BF, true, BF, PRE>), grid, dim3(64 * PF_WAVES), 0, st, a)
     if (gq != 4 || a.relu2) return EMBLA_ERR_UNSUPPORTED;
     if (a.q_bf16 && a.out_bf16 && a.qg) EMBLA_PR(true, true);
     else if (a.q_bf16 && a.out_bf16) EMBLA_PR(true, false);
