@@ -57,8 +57,10 @@ __device__ __forceinline__ void scales8(const u4_t* r, float* out) {
     }
 }
 
+constexpr int DW = 8;            // waves a workgroup: one 32-key tile each a round
+
 template <int GQ, bool RELU2, bool SCALE32, bool OBF, bool SCORES>
-__global__ __launch_bounds__(256, 2) void full_decode_kernel(
+__global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
     const uint16_t* __restrict__ q,   // [n_kv * GQ][128] fp16, prepared
     const int8_t* __restrict__ kc, const int8_t* __restrict__ vc,
     float* __restrict__ part, float* __restrict__ scores, uint16_t* __restrict__ o, int S, int CH,
@@ -222,7 +224,7 @@ __global__ __launch_bounds__(256, 2) void full_decode_kernel(
             }
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                const float p = exp2f(x[e] - m);   // x = -inf -> 0; m finite once a key is valid
+                const float p = __builtin_amdgcn_exp2f(x[e] - m);   // x = -inf -> 0; m finite once a key is valid
                 l += p;
                 wa[e] = (_Float16)(p * vs[e] * WSCALE);
             }
@@ -236,27 +238,24 @@ __global__ __launch_bounds__(256, 2) void full_decode_kernel(
         }
     };
 
-    // two tiles in flight a wave: tile i+2's loads go out before tile i+1 is computed
+    // one tile a wave a round, the next tile's load going out after this one is computed. The
+    // host's chunk gives a wave two tiles at 32k (256 workgroups); with one tile's registers the
+    // kernel runs 4 waves a SIMD (two workgroups a CU) whenever the grid is larger.
     {
-        constexpr int step = 32 * 4;
+        constexpr int step = 32 * DW;
         const int t0 = j0 + 32 * w;
-        Tile8 A, B;
+        Tile8 A;
         if (t0 < j1) load_tile(t0, A);
-        if (t0 + step < j1) load_tile(t0 + step, B);
         setup_q();   // after the first loads are out: the q math overlaps their latency
-        for (int t = t0; t < j1; t += 2 * step) {
+        for (int t = t0; t < j1; t += step) {
             compute_tile(t, A);
-            if (t + 2 * step < j1) load_tile(t + 2 * step, A);
-            if (t + step < j1) {
-                compute_tile(t + step, B);
-                if (t + 3 * step < j1) load_tile(t + 3 * step, B);
-            }
+            if (t + step < j1) load_tile(t + step, A);
         }
     }
 
-    // ---- merge the 4 waves (LDS)
-    __shared__ float om[4][GQ][HD];
-    __shared__ float mm[4][GQ], ll[4][GQ];
+    // ---- merge the waves (LDS)
+    __shared__ float om[DW][GQ][HD];
+    __shared__ float mm[DW][GQ], ll[DW][GQ];
     l += shfl_xor(l, 16);
     l += shfl_xor(l, 32);
     if (g == 0 && n < GQ) { mm[w][n] = m; ll[w][n] = l; }
@@ -267,20 +266,29 @@ __global__ __launch_bounds__(256, 2) void full_decode_kernel(
             if (4 * g + i < GQ) om[w][4 * g + i][8 * n + u] = O[u][i];
     __syncthreads();
 
-    constexpr int PER = GQ * HD / 256;   // outputs a thread: 2 or 4 (one head, consecutive dims)
+    constexpr int PER = GQ * HD / (64 * DW);   // outputs a thread: 1 or 2 (one head, consecutive dims)
     const int oh = tid * PER / HD, od = tid * PER % HD;
     float acc[PER], M, L;
     if constexpr (RELU2) {
         M = 0.0f;
-        L = ll[0][oh] + ll[1][oh] + ll[2][oh] + ll[3][oh];
-#pragma unroll
-        for (int e = 0; e < PER; e++) acc[e] = om[0][oh][od + e] + om[1][oh][od + e] + om[2][oh][od + e] + om[3][oh][od + e];
-    } else {
-        M = fmaxf(fmaxf(mm[0][oh], mm[1][oh]), fmaxf(mm[2][oh], mm[3][oh]));
-        float f[4];
         L = 0.0f;
 #pragma unroll
-        for (int ww = 0; ww < 4; ww++) {
+        for (int ww = 0; ww < DW; ww++) L += ll[ww][oh];
+#pragma unroll
+        for (int e = 0; e < PER; e++) {
+            float a = 0.0f;
+#pragma unroll
+            for (int ww = 0; ww < DW; ww++) a += om[ww][oh][od + e];
+            acc[e] = a;
+        }
+    } else {
+        M = NEG_INF;
+#pragma unroll
+        for (int ww = 0; ww < DW; ww++) M = fmaxf(M, mm[ww][oh]);
+        float f[DW];
+        L = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < DW; ww++) {
             f[ww] = mm[ww][oh] == NEG_INF ? 0.0f : exp2f(mm[ww][oh] - M);
             L += ll[ww][oh] * f[ww];
         }
@@ -288,7 +296,7 @@ __global__ __launch_bounds__(256, 2) void full_decode_kernel(
         for (int e = 0; e < PER; e++) {
             float a = 0.0f;
 #pragma unroll
-            for (int ww = 0; ww < 4; ww++) a += om[ww][oh][od + e] * f[ww];
+            for (int ww = 0; ww < DW; ww++) a += om[ww][oh][od + e] * f[ww];
             acc[e] = a;
         }
     }
@@ -363,7 +371,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
 
 // ------------------------------------------------------------------ host launch
 int launch_full_decode(const FullDecodeArgs& a, hipStream_t st) {
-    const dim3 grid(a.C, a.n_kv), block(256);
+    const dim3 grid(a.C, a.n_kv), block(64 * DW);
     const float qs = 0.08838834764831845f;   // 1/sqrt(128)
     const float sink = 11.313708498984761f;   // sqrt(128)
 #define EMBLA_FD(GQ, R, S32, OBF, SC)                                                              \
