@@ -270,6 +270,9 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="time only the headline (C3 at 32k, 16-layer graph) and print its JSON line; "
+                         "for kernel-trace profiles of the headline alone")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only dispatch C3 decode layers and a 64 MB copy (each after a cache-evicting "
                          "fill) for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs; prints nothing else")
@@ -290,6 +293,12 @@ def main():
         return
 
     L = 32768
+    if args.headline_only:
+        res, case, out0, _ = bench_c3(torch, args.steps, args.warmup, contexts=(L,))
+        h = res[L]
+        print(json.dumps({"metric": METRIC, "value": round(h["gbs"], 1), "unit": "GB/s",
+                          "us_per_layer": round(h["us_per_layer"], 3), "steps": args.steps}))
+        return
     res, case, out0, _ = bench_c3(torch, args.steps, args.warmup)
     c2 = bench_c2(torch)
     c4 = bench_c4(torch)
