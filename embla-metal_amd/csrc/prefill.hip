@@ -25,7 +25,8 @@ namespace embla {
 
 typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 
-constexpr int PBK = 64;            // keys a staged tile
+constexpr int PBK = 128;           // keys a staged tile
+constexpr int NSUB = PBK / 32;     // 32-key global tiles (and MFMA key blocks) a staged tile
 constexpr int KROW = HD + 8;       // LDS row stride of K (fp16 elements): conflict-free 16 B reads
 // V is staged as an fp16 copy of its global tile order: a 32-key tile is 8 rows u (dim % 8) of 64
 // lane slots (n + 16g) of 16 bytes, each slot the 8 keys {16t + 4g + i} of dim 8n + u. Rows are
@@ -46,7 +47,7 @@ __device__ __forceinline__ f16_t mfma32x(u4_t a, u4_t b, f16_t c) {
 
 struct __attribute__((aligned(16))) PrefillSmem {
     _Float16 k[2][PBK * KROW];
-    _Float16 vt[2][2 * VTILE];
+    _Float16 vt[2][NSUB * VTILE];
 };
 
 constexpr int PPS = HD + 4;        // floats a split partial row: O[128], m, l, pad
@@ -116,14 +117,14 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
 
     // ---- staging: each thread moves 16-byte pieces of the two 32-key global tiles of a 64-key tile
     constexpr int EB = RING ? 2 : 1;
-    constexpr int PIECES = 2 * 256 * EB;          // 16-byte pieces a 64-key tile, K (same for V)
+    constexpr int PIECES = NSUB * 256 * EB;       // 16-byte pieces a staged tile, K (same for V)
     constexpr int PER = PIECES / NT;              // pieces a thread
     static_assert(PER >= 1, "a piece a thread at least");
     struct Stage {
         u4_t kr[PER], vr[PER];
         float ksr[PER], vsr[PER][8];              // int8: the pieces' scales
     };
-    Stage SA, SB;                                 // two tiles' loads in flight
+    Stage SA;                                     // the next tile's loads
     auto tile_key = [&](int key) -> int {         // the 32-key tile's first key, clamped in range
         // a 64-key tile's second half may lie past max_s (max_s % 64 == 32): read the first half
         // again; those keys are past every row's position and masked
@@ -249,15 +250,16 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
 #pragma unroll
         for (int e = 0; e < 16; e++) O[i][e] = 0.0f;
 
-    if (ntiles > 0) gload(kstart, SA);
-    if (ntiles > 1) gload(kstart + PBK, SB);
-    if (ntiles > 0) sstore(0, SA);
+    if (ntiles > 0) {
+        gload(kstart, SA);
+        sstore(0, SA);
+    }
     __syncthreads();
-    // tile it: products from LDS buffer it % 2; tile it + 2's loads go out first (into the set
-    // tile it was staged from), tile it + 1 is staged at the end: two tiles of latency hidden
+    // tile it: products from LDS buffer it % 2 while tile it + 1's loads are in flight; tile it + 1
+    // is staged into the other buffer at the end
     auto iteration = [&](int it, Stage& ld_set, const Stage& st_set) {
         const int b = it & 1, k0 = kstart + it * PBK;
-        if (it + 2 < ntiles) gload(k0 + 2 * PBK, ld_set);
+        if (it + 1 < ntiles) gload(k0 + PBK, ld_set);
         const bool full_tile = k0 + PBK - 1 <= a.p0 + tok0 && (a.window == 0 || k0 >= a.p0 + last_tok - a.window + 1);
         const bool dead = k0 > a.p0 + last_tok;   // past every row of this wave: nothing to add
         // keys above kmax or at/below kmin are masked; a tile every row sees whole masks nothing
@@ -297,8 +299,9 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
                     O[i] = mfma32x<false>(vt[(dim & 7) * (VUROW / 8) + (dim >> 3) + 16 * (2 * s + h)], pb[s], O[i]);
                 }
         };
-        if (!dead) {   // uniform a wave
-            const f16_t s0 = s_block(0), s1 = s_block(1);
+        // two 32-key blocks kb0, kb0 + 1 of the staged tile: one max and rescale decision
+        auto pair = [&](int kb0) {
+            const f16_t s0 = s_block(kb0), s1 = s_block(kb0 + 1);
             // scores of the tile's 64 keys: item e of block kb is x[16 kb + e]
             float x[32];
 #pragma unroll
@@ -306,7 +309,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
             if (!full_tile) {   // uniform: only the diagonal (and window-edge) tiles
 #pragma unroll
                 for (int e = 0; e < 32; e++) {
-                    const int key = k0 + 32 * (e >> 4) + 8 * ((e & 15) >> 2) + 4 * h + (e & 3);
+                    const int key = k0 + 32 * (kb0 + (e >> 4)) + 8 * ((e & 15) >> 2) + 4 * h + (e & 3);
                     x[e] = key <= kmax && key > kmin ? x[e] : (RELU2 ? 0.0f : NEG_INF);
                 }
             }
@@ -346,7 +349,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
             for (int e = 0; e < 16; e++) { pw[e] = weight(x[e]); lsum += pw[e]; }
             pack(pw, pb0);
             // block 0's products run while block 1's weights are computed: one MFMA, then VALU
-            pv(0, pb0);
+            pv(kb0, pb0);
 #pragma unroll
             for (int e = 0; e < 16; e++) { pw[e] = weight(x[16 + e]); lsum += pw[e]; }
             pack(pw, pb1);
@@ -356,7 +359,11 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // an MFMA
                 __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);   // six VALU
             }
-            pv(1, pb1);
+            pv(kb0 + 1, pb1);
+        };
+        if (!dead) {   // uniform a wave
+#pragma unroll
+            for (int kb0 = 0; kb0 < NSUB; kb0 += 2) pair(kb0);
         }
         if (it + 1 < ntiles) {
             // buffer b ^ 1 was last read in the previous iteration, which every wave finished
@@ -365,10 +372,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
             __syncthreads();
         }
     };
-    for (int it = 0; it < ntiles; it += 2) {
-        iteration(it, SA, SB);
-        if (it + 1 < ntiles) iteration(it + 1, SB, SA);
-    }
+    for (int it = 0; it < ntiles; it++) iteration(it, SA, SA);
 
     // ---- normalise and store: lane (row r, half h) holds dims 32i + 8b + 4h .. + 3
     lsum += shfl_xor(lsum, 32);
