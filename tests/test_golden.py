@@ -1,0 +1,23 @@
+"""The golden fixtures (tests/golden/*.npz, written by tests/golden/make_golden.py) against the
+current input generator and oracle: the input digests and every stored output must reproduce."""
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+sys.path.insert(0, str(GOLDEN))
+import make_golden  # noqa: E402
+
+
+@pytest.mark.parametrize("name", sorted(make_golden.FIXTURES))
+def test_golden_fixture_reproduces(orc, name):
+    from embla_attn import synth
+    want = np.load(GOLDEN / f"{name}.npz", allow_pickle=False)
+    got = make_golden.FIXTURES[name](orc, synth)
+    assert str(want["digest"]) == got["digest"], f"{name}: the seeded inputs changed"
+    for k in want.files:
+        if k == "digest":
+            continue
+        np.testing.assert_array_equal(got[k], want[k], err_msg=f"{name}.{k}")
