@@ -8,9 +8,9 @@
 // internal summation order is not the spec's. MI355X design, in three kernels:
 //
 //  1. index_mfma_kernel: approximate scores on v_mfma_f32_32x32x16_f16 (8 rows × 4 index heads as
-//     the A operand, 32 keys as B; fp16 products are exact, the fp32 sums differ from the spec's
-//     by a bounded amount), stored as the top 16 bits of their order bits (134 MB for C5 in place
-//     of 268), plus each key chunk's largest key norm for the error bound.
+//     an A tile, 32 keys as B; fp16 products are exact, the fp32 sums differ from the spec's by a
+//     bounded amount), stored as the top 16 bits of their order bits (134 MB for C5 in place of
+//     268), plus each key chunk's largest key norm for the error bound.
 //  2. select_band_kernel, a workgroup a row: a 2-pass radix select on the 16-bit keys gives the
 //     k-th largest truncated key T. With ε bounding |approximate − spec| for every key of the row
 //     (from the row's query norms, weights and the key norm maximum), the spec's k-th largest
@@ -38,41 +38,48 @@ __device__ __forceinline__ float ob_to_float(uint32_t o) {
 typedef _Float16 h8v_t __attribute__((ext_vector_type(8)));
 
 // ------------------------------------------------------------------ 1. approximate scores (MFMA)
-/// Workgroup (8-row block rb, key chunk ch), 4 waves; a wave takes 32 keys a step. A operand: A row
-/// R = 4ρ + h (row 8 rb + ρ, index head h), lane l: R = l % 32, dims 16 s + 8 (l / 32) .. + 7 of
-/// k-step s. B: lane l: key l % 32, the same dims. D lane (key l % 32, half hh = l / 32) item e:
-/// A row 8 (e / 4) + 4 hh + e % 4, i.e. row ρ = 2 (e / 4) + hh, head e % 4: the 4 heads of a
-/// (row, key) score sit in one lane.
+/// Workgroup (64-row block rb, key chunk ch), 4 waves; wave w takes rows 64 rb + 16 w .. + 15 as
+/// two A tiles (8 rows × 4 index heads each) and sweeps every key of the chunk 32 at a time, so a
+/// key fragment feeds two MFMAs and the workgroup's waves read the same keys (L1 hits after the
+/// first). A tile: A row R = 4ρ + h (row ρ, index head h), lane l: R = l % 32, dims 16 s + 8 (l / 32)
+/// .. + 7 of k-step s. B: lane l: key l % 32, the same dims. D lane (key l % 32, half hh = l / 32)
+/// item e: A row 8 (e / 4) + 4 hh + e % 4, i.e. row ρ = 2 (e / 4) + hh, head e % 4: the 4 heads of
+/// a (row, key) score sit in one lane.
 __global__ __launch_bounds__(256) void index_mfma_kernel(IndexMfmaArgs a) {
     const int rb = blockIdx.x, ch = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int c = lane & 31, hh = lane >> 5;
-    h8v_t qa[4];
-    {
-        const int R = lane & 31, row = min(8 * rb + (R >> 2), a.T - 1), h = R & 3;
+    const int r0 = 64 * rb + 16 * w;   // the wave's first row
+    h8v_t qa[2][4];
+    float wq[2][4][4];
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++) {
+        const int R = lane & 31, row = min(r0 + 8 * rt + (R >> 2), a.T - 1), h = R & 3;
         const uint16_t* qr = a.qi + ((size_t)row * 4 + h) * 64;
 #pragma unroll
-        for (int s = 0; s < 4; s++) qa[s] = __builtin_bit_cast(h8v_t, ld16(qr + 16 * s + 8 * hh));
-    }
-    float wq[4][4];
+        for (int s = 0; s < 4; s++) qa[rt][s] = __builtin_bit_cast(h8v_t, ld16(qr + 16 * s + 8 * hh));
 #pragma unroll
-    for (int b = 0; b < 4; b++) {
-        const int row = min(8 * rb + 2 * b + hh, a.T - 1);
+        for (int b = 0; b < 4; b++) {
+            const int rw = min(r0 + 8 * rt + 2 * b + hh, a.T - 1);
 #pragma unroll
-        for (int i = 0; i < 4; i++) wq[b][i] = a.w[row * 4 + i];
+            for (int i = 0; i < 4; i++) wq[rt][b][i] = a.w[rw * 4 + i];
+        }
     }
     const int k0 = ch * a.kchunk, k1 = min(a.ld, k0 + a.kchunk);
+    const bool norms = rb == 0 && w == 0;   // one wave a chunk takes the key norms
     float nmax = 0.0f;
-    for (int kb = k0 + 32 * w; kb < k1; kb += 128) {
+    for (int kb = k0; kb < k1; kb += 32) {
         const int key = kb + c;
         u4_t kr[4];
 #pragma unroll
         for (int s = 0; s < 4; s++) kr[s] = key < a.nk ? ld16(a.ki + (size_t)key * 64 + 16 * s + 8 * hh) : (u4_t){0, 0, 0, 0};
-        f16_t d = {};
+        f16_t d[2] = {};
 #pragma unroll
         for (int s = 0; s < 4; s++)
-            d = __builtin_amdgcn_mfma_f32_32x32x16_f16(qa[s], __builtin_bit_cast(h8v_t, kr[s]), d, 0, 0, 0);
-        if (rb == 0) {   // this key's squared norm (half the dims a lane), for the chunk maximum
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++)
+                d[rt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(qa[rt][s], __builtin_bit_cast(h8v_t, kr[s]), d[rt], 0, 0, 0);
+        if (norms) {   // this key's squared norm (half the dims a lane), for the chunk maximum
             float ss = 0.0f;
 #pragma unroll
             for (int s = 0; s < 4; s++)
@@ -86,33 +93,29 @@ __global__ __launch_bounds__(256) void index_mfma_kernel(IndexMfmaArgs a) {
             nmax = fmaxf(nmax, ss);
         }
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
-            float sc = 0.0f;
+        for (int rt = 0; rt < 2; rt++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float r = fmaxf(d[4 * b + i], 0.0f);
-                sc = __builtin_fmaf(wq[b][i], r * r, sc);
+            for (int b = 0; b < 4; b++) {
+                float sc = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float r = fmaxf(d[rt][4 * b + i], 0.0f);
+                    sc = __builtin_fmaf(wq[rt][b][i], r * r, sc);
+                }
+                const int row = r0 + 8 * rt + 2 * b + hh;
+                if (row < a.T) a.keys[(size_t)row * a.ld + key] = (uint16_t)(ob32(sc) >> 16);
             }
-            const int row = 8 * rb + 2 * b + hh;
-            if (row < a.T) a.keys[(size_t)row * a.ld + key] = (uint16_t)(ob32(sc) >> 16);
-        }
     }
-    if (rb == 0) {
-        __shared__ float red[4];
+    if (norms) {
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) nmax = fmaxf(nmax, shfl_xor(nmax, o));
-        if (lane == 0) red[w] = nmax;
-        __syncthreads();
-        if (tid == 0) {
-            const float m2 = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-            // the fp32 sum of 64 exact squares is within 64 units of 2^-24 of the true sum
-            a.kmax[ch] = sqrtf(m2 * (1.0f + 0x1p-16f)) * (1.0f + 0x1p-16f);
-        }
+        // the fp32 sum of 64 exact squares is within 64 units of 2^-24 of the true sum
+        if (lane == 0) a.kmax[ch] = sqrtf(nmax * (1.0f + 0x1p-16f)) * (1.0f + 0x1p-16f);
     }
 }
 
 int launch_index_mfma(const IndexMfmaArgs& a, hipStream_t st) {
-    const dim3 grid((a.T + 7) / 8, (a.ld + a.kchunk - 1) / a.kchunk);
+    const dim3 grid((a.T + 63) / 64, (a.ld + a.kchunk - 1) / a.kchunk);
     hipLaunchKernelGGL(index_mfma_kernel, grid, dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
 }
