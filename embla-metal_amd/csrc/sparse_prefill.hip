@@ -306,7 +306,11 @@ __global__ __launch_bounds__(BS_T) void select_band_kernel(BandSelectArgs a) {
         for (int o = 32; o >= 1; o >>= 1) sa += __shfl_xor(sa, o, 64);
         uint32_t base = 0;
         if (lane == 63) base = atomicAdd(&sm.cnt[0], incl);
-        if (lane == 0 && sa) atomicAdd(&sm.cnt[1], sa);
+        if (lane == 0) {   // the compaction's counts: sure-above keys now, the band's added later
+            sm.tab[0][8 * r + w] = sa;
+            sm.tab[1][8 * r + w] = 0;
+            if (sa) atomicAdd(&sm.cnt[1], sa);
+        }
         base = __shfl(base, 63, 64);
         if (nb) {
             uint32_t p = base + incl - nb;
@@ -355,43 +359,28 @@ __global__ __launch_bounds__(BS_T) void select_band_kernel(BandSelectArgs a) {
     }
     const uint32_t E = pre;   // the spec's k-th largest score; k = ties to take, first by index
     // ---- mark the band keys with their class
+    // a band key's class into its slot and into the compaction count of its (round, wave): key j is
+    // in round j / 4096, wave (j % 4096) / 512
+    auto mark = [&](int j, uint32_t x) {
+        const uint16_t cl = x > E ? K_GT : (x == E ? K_EQ : 0);
+        sm.keys[j] = cl;
+        if (cl) atomicAdd(&sm.tab[cl == K_GT ? 0 : 1][8 * (j >> 12) + ((j & 4095) >> 9)], 1u);
+    };
     if (listed) {
-        for (uint32_t q = tid; q < nband; q += BS_T) {
-            const uint32_t x = sm.bx[q];
-            sm.keys[sm.bj[q]] = x > E ? K_GT : (x == E ? K_EQ : 0);
-        }
+        for (uint32_t q = tid; q < nband; q += BS_T) mark((int)sm.bj[q], sm.bx[q]);
     } else {
         for (int j = tid; j < n; j += BS_T) {
             const uint32_t key = sm.keys[j];
-            if (key >= kout && key < kin) {
-                const uint32_t x = ob32(spec_score(sm, a.ki, j));
-                sm.keys[j] = x > E ? K_GT : (x == E ? K_EQ : 0);
-            }
+            if (key >= kout && key < kin) mark(j, ob32(spec_score(sm, a.ki, j)));
         }
     }
     __syncthreads();
     // ---- ordered compaction: above (sure or marked), then the first k equal, by index. Round r,
-    // wave w holds keys 4096 r + 512 w .. + 511: table entry 8 r + w.
+    // wave w holds keys 4096 r + 512 w .. + 511: table entry 8 r + w, counted above.
     auto cls = [&](uint32_t key, bool real, bool& g, bool& e) {
         g = real && (key == K_GT || (key >= kin && key < K_EQ));
         e = real && key == K_EQ;
     };
-    for (int r = 0; r < rounds; r++) {
-        const int j = 8 * tid + 8 * BS_T * r;
-        const u4_t v = *(const u4_t*)(sm.keys + j);
-        uint32_t cg = 0, ce = 0;
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            bool g, q;
-            cls((v[e >> 1] >> (16 * (e & 1))) & 0xFFFF, j + e < n, g, q);
-            cg += g;
-            ce += q;
-        }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) { cg += __shfl_xor(cg, o, 64); ce += __shfl_xor(ce, o, 64); }
-        if (lane == 0) { sm.tab[0][8 * r + w] = cg; sm.tab[1][8 * r + w] = ce; }
-    }
-    __syncthreads();
     if (w < 2) {
         uint32_t* tb = sm.tab[w];
         const int m = 8 * rounds;
