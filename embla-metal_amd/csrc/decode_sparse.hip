@@ -440,13 +440,261 @@ __global__ __launch_bounds__(256) void sparse_rows8_kernel(SparseRows8Args a) {
     }
 }
 
+
+/// Gathered attention over a row-major int8 cache held entirely in registers (the sparse prefill's
+/// cache): one workgroup a (key chunk, kv head, query row), its 4 waves taking interleaved 32-key
+/// steps of the chunk's key list (in LDS). No stage: S^T = K q^T runs on v_mfma_i32_16x16x64_i8
+/// straight on the gathered K bytes, q being a 15-bit fixed point split exactly into int8 halves
+/// (hi in column n, lo in column n + GQ of the B operand; the scheme of full_decode_kernel), so the
+/// scores are exact integers times the fixed point's step. A lane (head n, group g) of the score
+/// tile holds keys {16t + 4g + i}, the A-operand slice of O += W V; it gathers those 8 keys' V
+/// bytes for dims 8n .. 8n + 7 (8 bytes a key, a row's 128 bytes over 16 lanes) and transposes
+/// them into the fp16 B operand in registers. The next step's K gather is in flight during this
+/// step's products, its V gather from the end of this step's.
+template <int GQ>
+__global__ __launch_bounds__(256, 4) void sparse_rows8_rm_kernel(SparseRows8Args a) {
+    typedef int i4_t __attribute__((ext_vector_type(4)));
+    constexpr float QFIX = 32000.0f;   // |q_int| <= 32000: |hi| <= 125
+    const int c = blockIdx.x, kvh = blockIdx.y, r = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int n = lane & 15, g = lane >> 4;
+    const int pos = a.p0 + r;
+    const bool sel = a.idx && pos + 1 > a.nsel;
+    const int nk_all = sel ? a.nsel : pos + 1;
+    const int j0 = c * a.CH, nk = min(nk_all, j0 + a.CH) - j0;   // this chunk's keys
+    const size_t nrow = (size_t)a.n_kv * a.max_s * HD;
+    const int8_t* kb = a.kc + (size_t)kvh * a.max_s * HD;
+    const int8_t* vb = a.vc + (size_t)kvh * a.max_s * HD;
+    const uint16_t* ksc = (const uint16_t*)(a.kc + nrow) + (size_t)kvh * a.max_s;
+    const uint16_t* vsc = (const uint16_t*)(a.vc + nrow) + (size_t)kvh * a.max_s;
+
+    constexpr int MERGE = (4 * GQ * HD + 8 * GQ) * 4;
+    __shared__ __attribute__((aligned(16))) char smem[MERGE];
+    __shared__ uint32_t sidx[SPR_MAXSEL];
+    __shared__ __attribute__((aligned(16))) float sks[4][2][32];   // per wave: k scales, v scales
+
+    // the key list: every load issued before the first store (rows clamped in range)
+    const uint32_t* rows = sel ? a.idx + (size_t)r * a.idx_row_stride + (size_t)kvh * a.idx_kv_stride : nullptr;
+    constexpr int LP = (SPR_MAXSEL + 255) / 256;
+    int lr[LP];
+#pragma unroll
+    for (int i = 0; i < LP; i++) {
+        const int p = tid + 256 * i;
+        lr[i] = p < nk ? (rows ? (int)rows[j0 + p] : j0 + p) : 0;
+    }
+
+    // q^T as the B operand: column n < GQ hi of head n, column GQ + n lo; lane (n, g), MFMA h:
+    // dims 64h + 16g .. + 15 (the K slice's dims)
+    i4_t qb[2];
+    float qsc;
+    {
+        const int hn = n % GQ;
+        const bool live = n < 2 * GQ, is_lo = n >= GQ;
+        const uint16_t* qr = a.q + (size_t)r * a.q_row_stride + (size_t)(kvh * GQ + hn) * HD + 16 * g;
+        u4_t qv[4];
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int u = 0; u < 2; u++) qv[2 * h + u] = ld16(qr + 64 * h + 8 * u);
+#pragma unroll
+        for (int i = 0; i < LP; i++)
+            if (tid + 256 * i < nk) sidx[tid + 256 * i] = (uint32_t)min(lr[i], a.max_s - 1);
+        float qf[32];
+        const bool qbf = a.q_bf16;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t x = qv[j][i];
+                const float bl = __uint_as_float(x << 16), bh = __uint_as_float(x & 0xFFFF0000u);
+                const float hl = h2f((uint16_t)(x & 0xFFFF)), hh = h2f((uint16_t)(x >> 16));
+                qf[8 * j + 2 * i] = qbf ? bl : hl;
+                qf[8 * j + 2 * i + 1] = qbf ? bh : hh;
+            }
+        float am = 0.0f;
+#pragma unroll
+        for (int d = 0; d < 32; d++) am = fmaxf(am, fabsf(qf[d]));
+        am = fmaxf(am, shfl_xor(am, 16));
+        am = fmaxf(am, shfl_xor(am, 32));
+        const float inv = am > 0.0f ? QFIX / am : 0.0f;
+        qsc = am / QFIX * (0.08838834764831845f * 1.4426950408889634f);   // step x 1/sqrt(128) x log2(e)
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                uint32_t word = 0;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int qi = (int)rintf(qf[16 * h + 4 * k + e] * inv);
+                    const int hi = (qi + 128) >> 8, lo = qi - hi * 256;
+                    const int byte = live ? (is_lo ? lo : hi) : 0;
+                    word |= (uint32_t)(byte & 0xFF) << (8 * e);
+                }
+                qb[h][k] = (int)word;
+            }
+    }
+    __syncthreads();   // the key list
+
+    float m = NEG_INF, l = 0.0f;
+    f4_t O[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) O[u] = (f4_t){0, 0, 0, 0};
+
+    // one 32-key step's raw bytes: K[2t + h] = key 16t + n, dims 64h + 16g ..; V[e] = key
+    // 16(e / 4) + 4g + e % 4, dims 8n .. 8n + 7; lanes < 32 hold key t0 + lane's two scales
+    struct Raw { u4_t k[4]; u2_t v[8]; uint32_t s; };
+    auto gather_k = [&](int t0, Raw& R) {
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int p = t0 + 16 * t + n;
+            const size_t row = p < nk ? sidx[p] : 0;
+#pragma unroll
+            for (int h = 0; h < 2; h++) R.k[2 * t + h] = ld16(kb + row * HD + 64 * h + 16 * g);
+        }
+        const int p = t0 + (lane & 31);
+        const size_t row = p < nk ? sidx[p] : 0;
+        R.s = lane < 32 ? ksc[row] : vsc[row];
+    };
+    auto gather_v = [&](int t0, Raw& R) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int p = t0 + 16 * (e >> 2) + 4 * g + (e & 3);
+            const size_t row = p < nk ? sidx[p] : 0;
+            R.v[e] = ld8(vb + row * HD + 8 * n);
+        }
+    };
+    Raw A;
+    if (32 * w < nk) { gather_k(32 * w, A); gather_v(32 * w, A); }
+    for (int t0 = 32 * w; t0 < nk; t0 += 128) {
+        // scales to LDS: k scale of key j at [0][j], v scale (x 64) at [1][j]
+        sks[w][lane >> 5][lane & 31] = lane < 32 ? h2f((uint16_t)A.s) : 64.0f * h2f((uint16_t)A.s);
+        wave_lds_sync();
+        i4_t st[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            st[t] = (i4_t){0, 0, 0, 0};
+            st[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i4_t, A.k[2 * t]), qb[0], st[t], 0, 0, 0);
+            st[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i4_t, A.k[2 * t + 1]), qb[1], st[t], 0, 0, 0);
+        }
+        if (t0 + 128 < nk) gather_k(t0 + 128, A);   // in flight during the products
+        const f4_t kq0 = *(const f4_t*)(&sks[w][0][4 * g]), kq1 = *(const f4_t*)(&sks[w][0][16 + 4 * g]);
+        const f4_t vq0 = *(const f4_t*)(&sks[w][1][4 * g]), vq1 = *(const f4_t*)(&sks[w][1][16 + 4 * g]);
+        float x[8];
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int lo = __shfl_xor(st[t][i], GQ, 64);
+                const float kq = t == 0 ? kq0[i] : kq1[i];
+                x[4 * t + i] = t0 + 16 * t + 4 * g + i < nk ? (float)(st[t][i] * 256 + lo) * qsc * kq : NEG_INF;
+            }
+        float mt = NEG_INF;
+#pragma unroll
+        for (int e = 0; e < 8; e++) mt = fmaxf(mt, x[e]);
+        mt = fmaxf(mt, shfl_xor(mt, 16));
+        mt = fmaxf(mt, shfl_xor(mt, 32));
+        const float mn = fmaxf(m, mt);
+        if (__any(n < GQ && mn > m)) {
+            if (__any(n < GQ && m != NEG_INF)) {
+                const float corr = m == NEG_INF ? 0.0f : exp2f(m - mn);
+                l *= corr;
+                float cf[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float c0 = readlane(corr, i);
+                    if constexpr (GQ == 8) cf[i] = g == 1 ? readlane(corr, 4 + i) : c0;
+                    else cf[i] = c0;
+                }
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) O[u][i] *= cf[i];
+            }
+            m = mn;
+        }
+        h8_t wa;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float p = __builtin_amdgcn_exp2f(x[e] - m);   // x = -inf -> 0
+            l += p;
+            wa[e] = (_Float16)(p * (e < 4 ? vq0[e & 3] : vq1[e & 3]));
+        }
+        // B operand of MFMA u: halves (V[e][8n + u], V[e + 1][8n + u]) a dword: byte u of keys e
+        // and e + 1 into bytes 0 and 2, then XOR 0x80 into them and 0x64 into bytes 1 and 3 gives
+        // the fp16 pair 1152 + x; minus 1152 (exact in fp16)
+        const h2_t bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            u4_t b;
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                const uint32_t sel = (u & 3) | (((u & 3) + 4) << 16) | 0x0C000C00u;
+                const uint32_t d = __builtin_amdgcn_perm(A.v[e + 1][u >> 2], A.v[e][u >> 2], sel) ^ 0x64806480u;
+                b[e / 2] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, d) + bias);
+            }
+            O[u] = mfma16(wa, __builtin_bit_cast(h8_t, b), O[u]);
+        }
+        if (t0 + 128 < nk) gather_v(t0 + 128, A);
+        wave_lds_sync();   // the next step's scale stores come after every lane's reads
+    }
+
+    // ---- merge the 4 waves (LDS), then the row's output or this chunk's partial
+    float (*om)[GQ][HD] = (float (*)[GQ][HD])smem;
+    float (*mm)[GQ] = (float (*)[GQ])(smem + 4 * GQ * HD * 4);
+    float (*ll)[GQ] = (float (*)[GQ])(smem + (4 * GQ * HD + 4 * GQ) * 4);
+    l += shfl_xor(l, 16);
+    l += shfl_xor(l, 32);
+    if (g == 0 && n < GQ) { mm[w][n] = m; ll[w][n] = l; }
+#pragma unroll
+    for (int u = 0; u < 8; u++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (4 * g + i < GQ) om[w][4 * g + i][8 * n + u] = O[u][i];
+    __syncthreads();
+    constexpr int PER = GQ * HD / 256;
+    const int oh = tid * PER / HD, od = tid * PER % HD;
+    const float M = fmaxf(fmaxf(mm[0][oh], mm[1][oh]), fmaxf(mm[2][oh], mm[3][oh]));
+    float f[4], L = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ww++) {
+        f[ww] = mm[ww][oh] == NEG_INF ? 0.0f : exp2f(mm[ww][oh] - M);
+        L += ll[ww][oh] * f[ww];
+    }
+    const int hq = kvh * GQ + oh;
+    if (a.C > 1) {   // partial: O x 64 unnormalised, m, l (decode_merge_kernel with oscale 64)
+        float* pp = a.part + ((size_t)c * a.n_q + hq) * SPS;
+#pragma unroll
+        for (int e = 0; e < PER; e++) {
+            float s = 0.0f;
+#pragma unroll
+            for (int ww = 0; ww < 4; ww++) s += om[ww][oh][od + e] * f[ww];
+            pp[od + e] = s;
+        }
+        if (od == 0) { pp[HD] = M; pp[HD + 1] = L; }
+        return;
+    }
+    const float inv = 1.0f / (64.0f * L);
+    uint16_t* orow = a.o + (size_t)r * a.o_row_stride + (size_t)hq * HD + od;
+#pragma unroll
+    for (int e = 0; e < PER; e++) {
+        float s = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < 4; ww++) s += om[ww][oh][od + e] * f[ww];
+        orow[e] = a.o_bf16 ? f2bf(s * inv) : f2h(s * inv);
+    }
+}
+
 int launch_sparse_rows8(const SparseRows8Args& a, hipStream_t st) {
     if (a.CH > SPR_MAXSEL || a.CH <= 0 || a.C <= 0) return EMBLA_ERR_UNSUPPORTED;   // a chunk's keys fit the list
     if (a.C > 1 && (a.R != 1 || !a.part)) return EMBLA_ERR_INVALID;
     const dim3 grid(a.C, a.n_kv, a.R), block(256);
     const int gq = a.n_q / a.n_kv;
 #define EMBLA_SR(GQ, TL, S32) hipLaunchKernelGGL((sparse_rows8_kernel<GQ, TL, S32>), grid, block, 0, st, a)
-    if (gq == 4 && !a.tiles && !a.scale32) EMBLA_SR(4, false, false);
+    if (gq == 4 && !a.tiles && !a.scale32 && !getenv("EMBLA_SPR_STAGE"))
+        hipLaunchKernelGGL((sparse_rows8_rm_kernel<4>), grid, block, 0, st, a);
+    else if (gq == 8 && !a.tiles && !a.scale32 && !getenv("EMBLA_SPR_STAGE"))
+        hipLaunchKernelGGL((sparse_rows8_rm_kernel<8>), grid, block, 0, st, a);
+    else if (gq == 4 && !a.tiles && !a.scale32) EMBLA_SR(4, false, false);
     else if (gq == 8 && !a.tiles && !a.scale32) EMBLA_SR(8, false, false);
     else if (gq == 8 && a.tiles && a.scale32) EMBLA_SR(8, true, true);
     else if (gq == 4 && a.tiles && !a.scale32) EMBLA_SR(4, true, false);
