@@ -450,7 +450,8 @@ int embla_prefill_sparse(const void* q, const void* k, const void* v, const void
                    (int8_t*)kc, (int8_t*)vc, true, false, false, true};
     int rc = launch_kv_quant(qa, stream);
     if (rc) return rc;
-    IndexMfmaArgs ia{(const uint16_t*)qi, w, (const uint16_t*)ki, keys, kmax, T, p0 + T, ld, kIndexChunk};
+    IndexMfmaArgs ia{(const uint16_t*)qi, w, (const uint16_t*)ki, keys, kmax, T, p0 + T, ld, kIndexChunk,
+                     p0 + 1 - kRecent};
     if ((rc = launch_index_mfma(ia, stream))) return rc;
     BandSelectArgs ba{keys, ld, (const uint16_t*)qi, w, (const uint16_t*)ki, kmax, nch, sel, kTopK + kRecent,
                       T, p0, kTopK, kRecent};

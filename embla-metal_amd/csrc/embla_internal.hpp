@@ -83,6 +83,7 @@ struct IndexMfmaArgs {
     uint16_t* keys;       // [T][ld]
     float* kmax;          // [ld / kchunk]
     int T, nk, ld, kchunk;
+    int lim0;             // row t's candidates are keys < t + lim0; the rest are stored as 0
 };
 int launch_index_mfma(const IndexMfmaArgs& a, hipStream_t st);
 

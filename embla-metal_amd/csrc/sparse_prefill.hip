@@ -103,7 +103,7 @@ __global__ __launch_bounds__(256) void index_mfma_kernel(IndexMfmaArgs a) {
                     sc = __builtin_fmaf(wq[rt][b][i], r * r, sc);
                 }
                 const int row = r0 + 8 * rt + 2 * b + hh;
-                if (row < a.T) a.keys[(size_t)row * a.ld + key] = (uint16_t)(ob32(sc) >> 16);
+                if (row < a.T) a.keys[(size_t)row * a.ld + key] = key < row + a.lim0 ? (uint16_t)(ob32(sc) >> 16) : 0;
             }
     }
     if (norms) {
@@ -123,21 +123,29 @@ int launch_index_mfma(const IndexMfmaArgs& a, hipStream_t st) {
 // ------------------------------------------------------------------ 2. exact selection by band
 constexpr int BS_T = 512;               // threads (8 waves)
 constexpr int BS_MAXN = 32768;          // candidate keys a row
-constexpr int BS_LB = 1024;             // band capacity (else the band is ranked from the keys)
+constexpr int BS_LB = 768;              // band capacity (else the band is ranked from the keys)
 constexpr int BS_HC = 4, BS_HS = 257;   // 256-bin histogram copies, stride
-constexpr uint16_t K_GT = 0xFFFF, K_EQ = 0xFFFE;   // class marks (no finite score truncates to them)
 
 struct BandSmem {
-    uint16_t keys[BS_MAXN];
-    uint32_t hist[BS_HC * BS_HS];
-    uint32_t bj[BS_LB];      // band key indices; the staged output at the end
-    uint32_t bx[BS_LB];      // their spec scores' order bits
-    uint32_t tab[2][64];     // compaction: counts, then offsets, a (round, wave)
+    uint16_t keys[BS_MAXN];   // a row's 16-bit keys; 0 past its candidates (below every score's key)
+    union {
+        uint32_t h1[1024];   // first digit (the key's top 11 bits): bin d in half d & 1 of dword d / 2
+        struct {
+            uint32_t bj[BS_LB];   // band key indices, in no order
+            uint32_t bx[BS_LB];   // their spec scores' order bits
+        } b;
+    } u;
+    union {
+        uint32_t hist[BS_HC * BS_HS];
+        uint32_t eq[BS_MAXN / 32];   // bitmap of the band keys whose spec score equals the k-th's
+    } v;
+    uint32_t gt[BS_MAXN / 32];       // bitmap of the selected keys above the k-th's score
     float qf[4][64];
     float wq[4];
-    uint32_t buf[9];
+    double eps;
     uint32_t sel[2];
     uint32_t cnt[2];         // band size, keys surely above
+    uint32_t wsum[8];        // the output scan's wave totals
     uint32_t kin, kout;
 };
 
@@ -180,7 +188,7 @@ __device__ void bs_pick(BandSmem& sm, int nc, uint32_t k) {
         for (int i = 0; i < 4; i++) {
             const int d = 255 - (4 * lane + i);
             uint32_t t = 0;
-            for (int c = 0; c < nc; c++) t += sm.hist[c * BS_HS + d];
+            for (int c = 0; c < nc; c++) t += sm.v.hist[c * BS_HS + d];
             cc[i] = t;
             s += t;
         }
@@ -200,6 +208,43 @@ __device__ void bs_pick(BandSmem& sm, int nc, uint32_t k) {
     __syncthreads();
 }
 
+/// Bin (of 2048) holding the k-th largest key, from the packed first-digit counts: sel = {bin,
+/// keys in bins above}. Wave 0: each lane sums 32 bins from the top; the lane whose bins hold the
+/// k-th is found by a scan and a ballot, then its 32 bins go one a lane through a second scan.
+__device__ void bs_pick1(BandSmem& sm, uint32_t k) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    if (tid < 64) {
+        const u4_t* hp = (const u4_t*)(sm.u.h1 + 1008 - 16 * lane);   // bins 2016 - 32 lane .. + 31
+        uint32_t s = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const u4_t x = hp[i];
+#pragma unroll
+            for (int c = 0; c < 4; c++) s += (x[c] & 0xFFFF) + (x[c] >> 16);
+        }
+        uint32_t above = s;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t x = __shfl_up(above, o, 64);
+            if (lane >= o) above += x;
+        }
+        above -= s;
+        const int L = __ffsll((long long)__ballot(above < k && above + s >= k)) - 1;
+        const uint32_t base = __shfl(above, L, 64);
+        const int d = 2047 - 32 * L - (lane & 31);   // bins of lane L, from the top
+        const uint32_t x = sm.u.h1[d >> 1];
+        const uint32_t c = lane >= 32 ? 0u : (d & 1) ? x >> 16 : x & 0xFFFF;
+        uint32_t incl = c;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t y = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += y;
+        }
+        if (base + incl - c < k && base + incl >= k) { sm.sel[0] = (uint32_t)d; sm.sel[1] = base + incl - c; }
+    }
+    __syncthreads();
+}
+
 __global__ __launch_bounds__(BS_T) void select_band_kernel(BandSelectArgs a) {
     __shared__ BandSmem sm;
     const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -208,22 +253,48 @@ __global__ __launch_bounds__(BS_T) void select_band_kernel(BandSelectArgs a) {
     const int n = S - a.recent;
     uint32_t* out = a.idx + (size_t)t * a.idx_stride;
     const uint16_t* kr = a.keys + (size_t)t * a.ld;
-    const int rounds = (n + 8 * BS_T - 1) / (8 * BS_T);   // 4096 keys a round, 8 a lane
+    // 4096 keys a round, 8 a lane. The index kernel stores 0 for every key past n, and a real
+    // score's key is >= 0x8000, so keys past n need no test anywhere below: they fall in bin 0 of
+    // the first digit (never the k-th's bin), below kout and below kin.
+    const int rounds = (n + 8 * BS_T - 1) / (8 * BS_T);
 
-    for (int q = tid; q < BS_HC * BS_HS; q += BS_T) sm.hist[q] = 0;
+    for (int q = tid; q < 1024; q += BS_T) sm.u.h1[q] = 0;
+    for (int q = tid; q < BS_MAXN / 32; q += BS_T) sm.gt[q] = 0;
+    for (int q = tid; q < BS_HS; q += BS_T) sm.v.hist[q] = 0;
     if (tid < 2) sm.cnt[tid] = 0;
     if (tid < 256) sm.qf[tid >> 6][tid & 63] = h2f(a.qi[(size_t)t * 256 + tid]);
     if (tid < 4) sm.wq[tid] = a.w[t * 4 + tid];
     __syncthreads();
-    // ---- load (every load in flight), top-byte histogram; keys past n are 0 and not counted
+    // ---- load (every load in flight), first-digit histogram
     {
         u4_t v[BS_MAXN / (8 * BS_T)];
 #pragma unroll
         for (int r = 0; r < BS_MAXN / (8 * BS_T); r++) {
             const int j = 8 * tid + 8 * BS_T * r;
-            v[r] = j < n ? ld16(kr + j) : (u4_t){0, 0, 0, 0};
+            v[r] = j < n ? ld16(kr + j) : (u4_t){0, 0, 0, 0};   // j + 8 <= ld: ld, j multiples of 8
         }
-        uint32_t* hc = sm.hist + (lane & (BS_HC - 1)) * BS_HS;
+        if (w == 1) {
+            // ε, while the keys are in flight: it bounds |approximate − spec| for every key of
+            // this row, from the row's query norms, weights and the key norm maximum
+            float km = 0.0f;
+            for (int c = lane; c < a.nchunks; c += 64) km = fmaxf(km, a.kmax[c]);
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) km = fmaxf(km, shfl_xor(km, o));
+            double eps = 0.0, mag = 0.0;
+#pragma unroll
+            for (int h = 0; h < 4; h++) {
+                double qn = (double)sm.qf[h][lane] * sm.qf[h][lane];   // exact products
+#pragma unroll
+                for (int o = 32; o >= 1; o >>= 1) qn += __shfl_xor(qn, o, 64);
+                const double R = sqrt(qn) * km * (1.0 + 1e-6);   // |q·k| <= |q||k|
+                const double del = R * 0x1p-16;                  // both fp32 sums of 64 exact products
+                const double wa = fabs((double)sm.wq[h]);
+                eps += wa * del * (2.0 * R + del);
+                mag += wa * (R + del) * (R + del);
+            }
+            eps += mag * 0x1p-20;   // the fp32 squares, products and the sum over heads, both sides
+            if (lane == 0) sm.eps = eps * (1.0 + 0x1p-10) + 1e-30;
+        }
 #pragma unroll
         for (int r = 0; r < BS_MAXN / (8 * BS_T); r++) {
             const int j = 8 * tid + 8 * BS_T * r;
@@ -231,8 +302,7 @@ __global__ __launch_bounds__(BS_T) void select_band_kernel(BandSelectArgs a) {
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
                     const uint32_t key = (v[r][e >> 1] >> (16 * (e & 1))) & 0xFFFF;
-                    if (j + e < n) atomicAdd(&hc[key >> 8], 1u);
-                    else v[r][e >> 1] &= ~(0xFFFFu << (16 * (e & 1)));
+                    atomicAdd(&sm.u.h1[key >> 6], 1u << ((key >> 1) & 16));   // half (key >> 5) & 1
                 }
                 *(u4_t*)(sm.keys + j) = v[r];
             }
@@ -240,41 +310,29 @@ __global__ __launch_bounds__(BS_T) void select_band_kernel(BandSelectArgs a) {
     }
     __syncthreads();
     uint32_t k = (uint32_t)a.topk;
-    bs_pick(sm, BS_HC, k);
+    bs_pick1(sm, k);
     const uint32_t d1 = sm.sel[0];
     k -= sm.sel[1];
-    __syncthreads();
-    for (int q = tid; q < BS_HS; q += BS_T) sm.hist[q] = 0;
-    __syncthreads();
-    for (int r = 0; r < rounds; r++) {
-        const int j = 8 * tid + 8 * BS_T * r;
-        const u4_t v = *(const u4_t*)(sm.keys + j);
+    // second digit: the low 5 bits of the keys in bin d1
+    {
+        const uint32_t base = d1 << 5;
+        for (int r = 0; r < rounds; r++) {
+            const u4_t v = *(const u4_t*)(sm.keys + 8 * tid + 8 * BS_T * r);
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const uint32_t key = (v[e >> 1] >> (16 * (e & 1))) & 0xFFFF;
-            if ((key >> 8) == d1 && j + e < n) atomicAdd(&sm.hist[key & 255], 1u);
+            for (int i = 0; i < 4; i++) {
+                const uint32_t x0 = (v[i] & 0xFFFF) - base, x1 = (v[i] >> 16) - base;
+                if (x0 < 32) atomicAdd(&sm.v.hist[x0], 1u);
+                if (x1 < 32) atomicAdd(&sm.v.hist[x1], 1u);
+            }
         }
     }
     __syncthreads();
     bs_pick(sm, 1, k);
-    const uint32_t T16 = (d1 << 8) | sm.sel[0];
+    const uint32_t T16 = (d1 << 5) | sm.sel[0];
 
-    // ---- the band: ε bounds |approximate − spec| for every key of this row
+    // ---- the band: keys within 2ε of T's interval
     if (tid == 0) {
-        float km = 0.0f;
-        for (int c = 0; c < a.nchunks; c++) km = fmaxf(km, a.kmax[c]);
-        double eps = 0.0, mag = 0.0;
-        for (int h = 0; h < 4; h++) {
-            double qn = 0.0;
-            for (int d = 0; d < 64; d++) qn += (double)sm.qf[h][d] * sm.qf[h][d];
-            const double R = sqrt(qn) * km * (1.0 + 1e-6);   // |q·k| <= |q||k|
-            const double del = R * 0x1p-16;                  // both fp32 sums of 64 exact products
-            const double wa = fabs((double)sm.wq[h]);
-            eps += wa * del * (2.0 * R + del);
-            mag += wa * (R + del) * (R + del);
-        }
-        eps += mag * 0x1p-20;   // the fp32 squares, products and the sum over heads, both sides
-        eps = eps * (1.0 + 0x1p-10) + 1e-30;
+        const double eps = sm.eps;
         const double lo = ob_to_float(T16 << 16), hi = ob_to_float((T16 << 16) | 0xFFFFu);
         const float fin = __double2float_rd(hi + 2.0 * eps);    // largest float <= hi(T) + 2ε
         const float fout = __double2float_ru(lo - 2.0 * eps);   // smallest float >= lo(T) - 2ε
@@ -283,70 +341,49 @@ __global__ __launch_bounds__(BS_T) void select_band_kernel(BandSelectArgs a) {
     }
     __syncthreads();
     const uint32_t kin = sm.kin, kout = sm.kout;
-    // ---- classify: count the keys surely above, list the band (one atomic a wave)
+    // ---- classify: the keys surely above into the bitmap (a byte a lane) and their count (by
+    // ballots); the band into a list (an LDS atomic a band key, in no order)
     for (int r = 0; r < rounds; r++) {
         const int j = 8 * tid + 8 * BS_T * r;
         const u4_t v = *(const u4_t*)(sm.keys + j);
-        uint32_t nb = 0, na = 0;
+        uint32_t sa = 0, bits = 0;
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             const uint32_t key = (v[e >> 1] >> (16 * (e & 1))) & 0xFFFF;
-            const bool real = j + e < n;
-            na += real && key >= kin;
-            nb += real && key >= kout && key < kin;
-        }
-        uint32_t incl = nb;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t x = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += x;
-        }
-        uint32_t sa = na;
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) sa += __shfl_xor(sa, o, 64);
-        uint32_t base = 0;
-        if (lane == 63) base = atomicAdd(&sm.cnt[0], incl);
-        if (lane == 0) {   // the compaction's counts: sure-above keys now, the band's added later
-            sm.tab[0][8 * r + w] = sa;
-            sm.tab[1][8 * r + w] = 0;
-            if (sa) atomicAdd(&sm.cnt[1], sa);
-        }
-        base = __shfl(base, 63, 64);
-        if (nb) {
-            uint32_t p = base + incl - nb;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const uint32_t key = (v[e >> 1] >> (16 * (e & 1))) & 0xFFFF;
-                if (j + e < n && key >= kout && key < kin) {
-                    if (p < BS_LB) sm.bj[p] = (uint32_t)(j + e);
-                    p++;
-                }
+            const bool above = key >= kin;
+            sa += (uint32_t)__popcll(__ballot(above));
+            bits |= (uint32_t)above << e;
+            if (key >= kout && !above) {
+                const uint32_t p = atomicAdd(&sm.cnt[0], 1u);
+                if (p < BS_LB) sm.u.b.bj[p] = (uint32_t)(j + e);
             }
         }
+        ((uint8_t*)sm.gt)[j >> 3] = (uint8_t)bits;
+        if (lane == 0 && sa) atomicAdd(&sm.cnt[1], sa);
     }
     __syncthreads();
     const uint32_t nband = sm.cnt[0];
     k = (uint32_t)a.topk - sm.cnt[1];   // rank of the spec's k-th largest among the band
     const bool listed = nband <= BS_LB;
     if (listed)
-        for (uint32_t q = tid; q < nband; q += BS_T) sm.bx[q] = ob32(spec_score(sm, a.ki, sm.bj[q]));
+        for (uint32_t q = tid; q < nband; q += BS_T) sm.u.b.bx[q] = ob32(spec_score(sm, a.ki, sm.u.b.bj[q]));
     __syncthreads();
     // ---- exact rank within the band: four 8-bit passes over the band's spec scores
     uint32_t pre = 0, msk = 0;
     for (int shift = 24; shift >= 0; shift -= 8) {
-        for (int q = tid; q < BS_HS; q += BS_T) sm.hist[q] = 0;
+        for (int q = tid; q < BS_HS; q += BS_T) sm.v.hist[q] = 0;
         __syncthreads();
         if (listed) {
             for (uint32_t q = tid; q < nband; q += BS_T) {
-                const uint32_t x = sm.bx[q];
-                if ((x & msk) == pre) atomicAdd(&sm.hist[(x >> shift) & 255u], 1u);
+                const uint32_t x = sm.u.b.bx[q];
+                if ((x & msk) == pre) atomicAdd(&sm.v.hist[(x >> shift) & 255u], 1u);
             }
         } else {   // a band too large to list: rescore it from the keys on every pass
             for (int j = tid; j < n; j += BS_T) {
                 const uint32_t key = sm.keys[j];
                 if (key >= kout && key < kin) {
                     const uint32_t x = ob32(spec_score(sm, a.ki, j));
-                    if ((x & msk) == pre) atomicAdd(&sm.hist[(x >> shift) & 255u], 1u);
+                    if ((x & msk) == pre) atomicAdd(&sm.v.hist[(x >> shift) & 255u], 1u);
                 }
             }
         }
@@ -358,16 +395,15 @@ __global__ __launch_bounds__(BS_T) void select_band_kernel(BandSelectArgs a) {
         __syncthreads();
     }
     const uint32_t E = pre;   // the spec's k-th largest score; k = ties to take, first by index
-    // ---- mark the band keys with their class
-    // a band key's class into its slot and into the compaction count of its (round, wave): key j is
-    // in round j / 4096, wave (j % 4096) / 512
+    // ---- band keys above E into the selection bitmap, those equal to E into the tie bitmap
+    for (int q = tid; q < BS_MAXN / 32; q += BS_T) sm.v.eq[q] = 0;
+    __syncthreads();
     auto mark = [&](int j, uint32_t x) {
-        const uint16_t cl = x > E ? K_GT : (x == E ? K_EQ : 0);
-        sm.keys[j] = cl;
-        if (cl) atomicAdd(&sm.tab[cl == K_GT ? 0 : 1][8 * (j >> 12) + ((j & 4095) >> 9)], 1u);
+        if (x > E) atomicOr(&sm.gt[j >> 5], 1u << (j & 31));
+        else if (x == E) atomicOr(&sm.v.eq[j >> 5], 1u << (j & 31));
     };
     if (listed) {
-        for (uint32_t q = tid; q < nband; q += BS_T) mark((int)sm.bj[q], sm.bx[q]);
+        for (uint32_t q = tid; q < nband; q += BS_T) mark((int)sm.u.b.bj[q], sm.u.b.bx[q]);
     } else {
         for (int j = tid; j < n; j += BS_T) {
             const uint32_t key = sm.keys[j];
@@ -375,63 +411,43 @@ __global__ __launch_bounds__(BS_T) void select_band_kernel(BandSelectArgs a) {
         }
     }
     __syncthreads();
-    // ---- ordered compaction: above (sure or marked), then the first k equal, by index. Round r,
-    // wave w holds keys 4096 r + 512 w .. + 511: table entry 8 r + w, counted above.
-    auto cls = [&](uint32_t key, bool real, bool& g, bool& e) {
-        g = real && (key == K_GT || (key >= kin && key < K_EQ));
-        e = real && key == K_EQ;
-    };
-    if (w < 2) {
-        uint32_t* tb = sm.tab[w];
-        const int m = 8 * rounds;
-        const uint32_t v = lane < m ? tb[lane] : 0u;
-        uint32_t incl = v;
+    // ---- the output in select_keys' order: the keys above E by index, then the first k equal
+    // to E by index. Thread i holds keys 64 i .. + 63 of each bitmap; a block scan of the counts
+    // gives its first slot.
+    auto block_scan = [&](uint32_t c, uint32_t& total) -> uint32_t {
+        uint32_t incl = c;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
             const uint32_t x = __shfl_up(incl, o, 64);
             if (lane >= o) incl += x;
         }
-        if (lane < m) tb[lane] = incl - v;
-        if (lane == 63) sm.sel[w] = incl;
+        if (lane == 63) sm.wsum[w] = incl;
+        __syncthreads();
+        uint32_t before = 0;
+        total = 0;
+#pragma unroll
+        for (int i = 0; i < BS_T / 64; i++) {
+            const uint32_t x = sm.wsum[i];
+            before += i < w ? x : 0u;
+            total += x;
+        }
+        __syncthreads();   // wsum is reused by the next scan
+        return before + incl - c;
+    };
+    uint32_t ngt;
+    {
+        uint32_t g0 = sm.gt[2 * tid], g1 = sm.gt[2 * tid + 1];
+        uint32_t p = block_scan(__popc(g0) + __popc(g1), ngt);
+        for (; g0; g0 &= g0 - 1) out[p++] = 64u * tid + __ffs(g0) - 1;
+        for (; g1; g1 &= g1 - 1) out[p++] = 64u * tid + 32u + __ffs(g1) - 1;
     }
-    __syncthreads();
-    const uint32_t ngt = sm.sel[0];
-    uint32_t* sout = a.topk <= BS_LB ? sm.bj : out;
-    for (int r = 0; r < rounds; r++) {
-        const int j = 8 * tid + 8 * BS_T * r;
-        const u4_t v = *(const u4_t*)(sm.keys + j);
-        bool g[8], q[8];
-        uint32_t cg = 0, ce = 0;
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            cls((v[e >> 1] >> (16 * (e & 1))) & 0xFFFF, j + e < n, g[e], q[e]);
-            cg += g[e];
-            ce += q[e];
-        }
-        uint32_t ig = cg, ie = ce;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t xg = __shfl_up(ig, o, 64), xe = __shfl_up(ie, o, 64);
-            if (lane >= o) { ig += xg; ie += xe; }
-        }
-        uint32_t pg = sm.tab[0][8 * r + w] + ig - cg, pe = sm.tab[1][8 * r + w] + ie - ce;
-        if (cg | ce) {
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                if (g[e]) {
-                    if (pg < (uint32_t)a.topk) sout[pg] = (uint32_t)(j + e);
-                    pg++;
-                }
-                if (q[e]) {
-                    if (pe < k && ngt + pe < (uint32_t)a.topk) sout[ngt + pe] = (uint32_t)(j + e);
-                    pe++;
-                }
-            }
-        }
+    if (k > 0) {   // ties (k is uniform)
+        uint32_t e0 = sm.v.eq[2 * tid], e1 = sm.v.eq[2 * tid + 1];
+        uint32_t neq;
+        uint32_t p = block_scan(__popc(e0) + __popc(e1), neq);
+        for (; e0 && p < k; e0 &= e0 - 1) out[ngt + p++] = 64u * tid + __ffs(e0) - 1;
+        for (; e1 && p < k; e1 &= e1 - 1) out[ngt + p++] = 64u * tid + 32u + __ffs(e1) - 1;
     }
-    __syncthreads();
-    if (sout != out)
-        for (int j = tid; j < a.topk; j += BS_T) out[j] = sout[j];
     for (int j = tid; j < a.recent; j += BS_T) out[a.topk + j] = (uint32_t)(n + j);
 }
 
