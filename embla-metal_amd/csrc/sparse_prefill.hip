@@ -123,23 +123,17 @@ int launch_index_mfma(const IndexMfmaArgs& a, hipStream_t st) {
 // ------------------------------------------------------------------ 2. exact selection by band
 constexpr int BS_T = 512;               // threads (8 waves)
 constexpr int BS_MAXN = 32768;          // candidate keys a row
-constexpr int BS_LB = 768;              // band capacity (else the band is ranked from the keys)
-constexpr int BS_HC = 4, BS_HS = 257;   // 256-bin histogram copies, stride
+constexpr int BS_LB = 1024;             // band capacity (else the band is ranked from the keys)
+constexpr int BS_HS = 257;              // band radix histogram (256 bins) stride
+constexpr int BS_R = BS_MAXN / (8 * BS_T);   // rounds of 4096 keys, 8 a lane
 
 struct BandSmem {
-    uint16_t keys[BS_MAXN];   // a row's 16-bit keys; 0 past its candidates (below every score's key)
-    union {
-        uint32_t h1[1024];   // first digit (the key's top 11 bits): bin d in half d & 1 of dword d / 2
-        struct {
-            uint32_t bj[BS_LB];   // band key indices, in no order
-            uint32_t bx[BS_LB];   // their spec scores' order bits
-        } b;
-    } u;
-    union {
-        uint32_t hist[BS_HC * BS_HS];
-        uint32_t eq[BS_MAXN / 32];   // bitmap of the band keys whose spec score equals the k-th's
-    } v;
-    uint32_t gt[BS_MAXN / 32];       // bitmap of the selected keys above the k-th's score
+    uint32_t h1[2][4096];   // first digit (the key's top 12 bits), two copies (by lane parity)
+    uint32_t bj[BS_LB];     // band key indices, in no order
+    uint32_t bx[BS_LB];     // their spec scores' order bits
+    uint32_t hist[BS_HS];
+    uint32_t gt[BS_MAXN / 32];   // bitmap of the selected keys above the k-th's score
+    uint32_t eq[BS_MAXN / 32];   // bitmap of the band keys whose spec score equals the k-th's
     float qf[4][64];
     float wq[4];
     double eps;
@@ -188,7 +182,7 @@ __device__ void bs_pick(BandSmem& sm, int nc, uint32_t k) {
         for (int i = 0; i < 4; i++) {
             const int d = 255 - (4 * lane + i);
             uint32_t t = 0;
-            for (int c = 0; c < nc; c++) t += sm.v.hist[c * BS_HS + d];
+            for (int c = 0; c < nc; c++) t += sm.hist[c * BS_HS + d];
             cc[i] = t;
             s += t;
         }
@@ -208,20 +202,22 @@ __device__ void bs_pick(BandSmem& sm, int nc, uint32_t k) {
     __syncthreads();
 }
 
-/// Bin (of 2048) holding the k-th largest key, from the packed first-digit counts: sel = {bin,
-/// keys in bins above}. Wave 0: each lane sums 32 bins from the top; the lane whose bins hold the
-/// k-th is found by a scan and a ballot, then its 32 bins go one a lane through a second scan.
+/// Bin (of 4096) holding the k-th largest key, from the first-digit counts: sel = {bin, keys in
+/// bins above}. Wave 0: each lane sums 64 bins (both copies) from the top; the lane whose bins
+/// hold the k-th is found by a scan and a ballot, then its 64 bins go one a lane through a second
+/// scan.
 __device__ void bs_pick1(BandSmem& sm, uint32_t k) {
     const int tid = threadIdx.x, lane = tid & 63;
     if (tid < 64) {
-        const u4_t* hp = (const u4_t*)(sm.u.h1 + 1008 - 16 * lane);   // bins 2016 - 32 lane .. + 31
+        const int b0 = 4032 - 64 * lane;   // the lane's bins b0 .. b0 + 63
         uint32_t s = 0;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const u4_t x = hp[i];
+        for (int c = 0; c < 2; c++)
 #pragma unroll
-            for (int c = 0; c < 4; c++) s += (x[c] & 0xFFFF) + (x[c] >> 16);
-        }
+            for (int i = 0; i < 16; i++) {
+                const u4_t x = *(const u4_t*)(sm.h1[c] + b0 + 4 * i);
+                s += (x[0] + x[1]) + (x[2] + x[3]);
+            }
         uint32_t above = s;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
@@ -231,9 +227,8 @@ __device__ void bs_pick1(BandSmem& sm, uint32_t k) {
         above -= s;
         const int L = __ffsll((long long)__ballot(above < k && above + s >= k)) - 1;
         const uint32_t base = __shfl(above, L, 64);
-        const int d = 2047 - 32 * L - (lane & 31);   // bins of lane L, from the top
-        const uint32_t x = sm.u.h1[d >> 1];
-        const uint32_t c = lane >= 32 ? 0u : (d & 1) ? x >> 16 : x & 0xFFFF;
+        const int d = 4095 - 64 * L - lane;   // bins of lane L, from the top
+        const uint32_t c = sm.h1[0][d] + sm.h1[1][d];
         uint32_t incl = c;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
@@ -245,7 +240,7 @@ __device__ void bs_pick1(BandSmem& sm, uint32_t k) {
     __syncthreads();
 }
 
-__global__ __launch_bounds__(BS_T) void select_band_kernel(BandSelectArgs a) {
+__global__ __launch_bounds__(BS_T) __attribute__((amdgpu_waves_per_eu(6))) void select_band_kernel(BandSelectArgs a) {
     __shared__ BandSmem sm;
     const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int S = a.p0 + t + 1;
@@ -258,53 +253,50 @@ __global__ __launch_bounds__(BS_T) void select_band_kernel(BandSelectArgs a) {
     // the first digit (never the k-th's bin), below kout and below kin.
     const int rounds = (n + 8 * BS_T - 1) / (8 * BS_T);
 
-    for (int q = tid; q < 1024; q += BS_T) sm.u.h1[q] = 0;
+    for (int q = tid; q < 2 * 4096; q += BS_T) (&sm.h1[0][0])[q] = 0;
     for (int q = tid; q < BS_MAXN / 32; q += BS_T) sm.gt[q] = 0;
-    for (int q = tid; q < BS_HS; q += BS_T) sm.v.hist[q] = 0;
+    for (int q = tid; q < BS_HS; q += BS_T) sm.hist[q] = 0;
     if (tid < 2) sm.cnt[tid] = 0;
     if (tid < 256) sm.qf[tid >> 6][tid & 63] = h2f(a.qi[(size_t)t * 256 + tid]);
     if (tid < 4) sm.wq[tid] = a.w[t * 4 + tid];
     __syncthreads();
-    // ---- load (every load in flight), first-digit histogram
+    // ---- the row's keys, held in registers: v[r] = keys 8 tid + 4096 r .. + 7 (every load in
+    // flight); first-digit histogram
+    u4_t v[BS_R];
+#pragma unroll
+    for (int r = 0; r < BS_R; r++) {
+        const int j = 8 * tid + 8 * BS_T * r;
+        v[r] = j < n ? ld16(kr + j) : (u4_t){0, 0, 0, 0};   // j + 8 <= ld: ld, j multiples of 8
+    }
+    if (w == 1) {
+        // ε, while the keys are in flight: it bounds |approximate − spec| for every key of this
+        // row, from the row's query norms, weights and the key norm maximum
+        float km = 0.0f;
+        for (int c = lane; c < a.nchunks; c += 64) km = fmaxf(km, a.kmax[c]);
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) km = fmaxf(km, shfl_xor(km, o));
+        double eps = 0.0, mag = 0.0;
+#pragma unroll
+        for (int h = 0; h < 4; h++) {
+            double qn = (double)sm.qf[h][lane] * sm.qf[h][lane];   // exact products
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) qn += __shfl_xor(qn, o, 64);
+            const double R = sqrt(qn) * km * (1.0 + 1e-6);   // |q·k| <= |q||k|
+            const double del = R * 0x1p-16;                  // both fp32 sums of 64 exact products
+            const double wa = fabs((double)sm.wq[h]);
+            eps += wa * del * (2.0 * R + del);
+            mag += wa * (R + del) * (R + del);
+        }
+        eps += mag * 0x1p-20;   // the fp32 squares, products and the sum over heads, both sides
+        if (lane == 0) sm.eps = eps * (1.0 + 0x1p-10) + 1e-30;
+    }
     {
-        u4_t v[BS_MAXN / (8 * BS_T)];
+        uint32_t* hc = sm.h1[lane & 1];
 #pragma unroll
-        for (int r = 0; r < BS_MAXN / (8 * BS_T); r++) {
-            const int j = 8 * tid + 8 * BS_T * r;
-            v[r] = j < n ? ld16(kr + j) : (u4_t){0, 0, 0, 0};   // j + 8 <= ld: ld, j multiples of 8
-        }
-        if (w == 1) {
-            // ε, while the keys are in flight: it bounds |approximate − spec| for every key of
-            // this row, from the row's query norms, weights and the key norm maximum
-            float km = 0.0f;
-            for (int c = lane; c < a.nchunks; c += 64) km = fmaxf(km, a.kmax[c]);
-#pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) km = fmaxf(km, shfl_xor(km, o));
-            double eps = 0.0, mag = 0.0;
-#pragma unroll
-            for (int h = 0; h < 4; h++) {
-                double qn = (double)sm.qf[h][lane] * sm.qf[h][lane];   // exact products
-#pragma unroll
-                for (int o = 32; o >= 1; o >>= 1) qn += __shfl_xor(qn, o, 64);
-                const double R = sqrt(qn) * km * (1.0 + 1e-6);   // |q·k| <= |q||k|
-                const double del = R * 0x1p-16;                  // both fp32 sums of 64 exact products
-                const double wa = fabs((double)sm.wq[h]);
-                eps += wa * del * (2.0 * R + del);
-                mag += wa * (R + del) * (R + del);
-            }
-            eps += mag * 0x1p-20;   // the fp32 squares, products and the sum over heads, both sides
-            if (lane == 0) sm.eps = eps * (1.0 + 0x1p-10) + 1e-30;
-        }
-#pragma unroll
-        for (int r = 0; r < BS_MAXN / (8 * BS_T); r++) {
-            const int j = 8 * tid + 8 * BS_T * r;
+        for (int r = 0; r < BS_R; r++) {
             if (r < rounds) {
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const uint32_t key = (v[r][e >> 1] >> (16 * (e & 1))) & 0xFFFF;
-                    atomicAdd(&sm.u.h1[key >> 6], 1u << ((key >> 1) & 16));   // half (key >> 5) & 1
-                }
-                *(u4_t*)(sm.keys + j) = v[r];
+                for (int e = 0; e < 8; e++) atomicAdd(&hc[((v[r][e >> 1] >> (16 * (e & 1))) & 0xFFFF) >> 4], 1u);
             }
         }
     }
@@ -313,22 +305,24 @@ __global__ __launch_bounds__(BS_T) void select_band_kernel(BandSelectArgs a) {
     bs_pick1(sm, k);
     const uint32_t d1 = sm.sel[0];
     k -= sm.sel[1];
-    // second digit: the low 5 bits of the keys in bin d1
+    // second digit: the low 4 bits of the keys in bin d1
     {
-        const uint32_t base = d1 << 5;
-        for (int r = 0; r < rounds; r++) {
-            const u4_t v = *(const u4_t*)(sm.keys + 8 * tid + 8 * BS_T * r);
+        const uint32_t base = d1 << 4;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t x0 = (v[i] & 0xFFFF) - base, x1 = (v[i] >> 16) - base;
-                if (x0 < 32) atomicAdd(&sm.v.hist[x0], 1u);
-                if (x1 < 32) atomicAdd(&sm.v.hist[x1], 1u);
+        for (int r = 0; r < BS_R; r++) {
+            if (r < rounds) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t x0 = (v[r][i] & 0xFFFF) - base, x1 = (v[r][i] >> 16) - base;
+                    if (x0 < 16) atomicAdd(&sm.hist[x0], 1u);
+                    if (x1 < 16) atomicAdd(&sm.hist[x1], 1u);
+                }
             }
         }
     }
     __syncthreads();
     bs_pick(sm, 1, k);
-    const uint32_t T16 = (d1 << 5) | sm.sel[0];
+    const uint32_t T16 = (d1 << 4) | sm.sel[0];
 
     // ---- the band: keys within 2ε of T's interval
     if (tid == 0) {
@@ -343,47 +337,49 @@ __global__ __launch_bounds__(BS_T) void select_band_kernel(BandSelectArgs a) {
     const uint32_t kin = sm.kin, kout = sm.kout;
     // ---- classify: the keys surely above into the bitmap (a byte a lane) and their count (by
     // ballots); the band into a list (an LDS atomic a band key, in no order)
-    for (int r = 0; r < rounds; r++) {
-        const int j = 8 * tid + 8 * BS_T * r;
-        const u4_t v = *(const u4_t*)(sm.keys + j);
-        uint32_t sa = 0, bits = 0;
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const uint32_t key = (v[e >> 1] >> (16 * (e & 1))) & 0xFFFF;
-            const bool above = key >= kin;
-            sa += (uint32_t)__popcll(__ballot(above));
-            bits |= (uint32_t)above << e;
-            if (key >= kout && !above) {
-                const uint32_t p = atomicAdd(&sm.cnt[0], 1u);
-                if (p < BS_LB) sm.u.b.bj[p] = (uint32_t)(j + e);
+    for (int r = 0; r < BS_R; r++) {
+        if (r < rounds) {
+            const int j = 8 * tid + 8 * BS_T * r;
+            uint32_t sa = 0, bits = 0;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const uint32_t key = (v[r][e >> 1] >> (16 * (e & 1))) & 0xFFFF;
+                const bool above = key >= kin;
+                sa += (uint32_t)__popcll(__ballot(above));
+                bits |= (uint32_t)above << e;
+                if (key >= kout && !above) {
+                    const uint32_t p = atomicAdd(&sm.cnt[0], 1u);
+                    if (p < BS_LB) sm.bj[p] = (uint32_t)(j + e);
+                }
             }
+            ((uint8_t*)sm.gt)[j >> 3] = (uint8_t)bits;
+            if (lane == 0 && sa) atomicAdd(&sm.cnt[1], sa);
         }
-        ((uint8_t*)sm.gt)[j >> 3] = (uint8_t)bits;
-        if (lane == 0 && sa) atomicAdd(&sm.cnt[1], sa);
     }
     __syncthreads();
     const uint32_t nband = sm.cnt[0];
     k = (uint32_t)a.topk - sm.cnt[1];   // rank of the spec's k-th largest among the band
     const bool listed = nband <= BS_LB;
     if (listed)
-        for (uint32_t q = tid; q < nband; q += BS_T) sm.u.b.bx[q] = ob32(spec_score(sm, a.ki, sm.u.b.bj[q]));
+        for (uint32_t q = tid; q < nband; q += BS_T) sm.bx[q] = ob32(spec_score(sm, a.ki, sm.bj[q]));
     __syncthreads();
     // ---- exact rank within the band: four 8-bit passes over the band's spec scores
     uint32_t pre = 0, msk = 0;
     for (int shift = 24; shift >= 0; shift -= 8) {
-        for (int q = tid; q < BS_HS; q += BS_T) sm.v.hist[q] = 0;
+        for (int q = tid; q < BS_HS; q += BS_T) sm.hist[q] = 0;
         __syncthreads();
         if (listed) {
             for (uint32_t q = tid; q < nband; q += BS_T) {
-                const uint32_t x = sm.u.b.bx[q];
-                if ((x & msk) == pre) atomicAdd(&sm.v.hist[(x >> shift) & 255u], 1u);
+                const uint32_t x = sm.bx[q];
+                if ((x & msk) == pre) atomicAdd(&sm.hist[(x >> shift) & 255u], 1u);
             }
         } else {   // a band too large to list: rescore it from the keys on every pass
             for (int j = tid; j < n; j += BS_T) {
-                const uint32_t key = sm.keys[j];
+                const uint32_t key = kr[j];
                 if (key >= kout && key < kin) {
                     const uint32_t x = ob32(spec_score(sm, a.ki, j));
-                    if ((x & msk) == pre) atomicAdd(&sm.v.hist[(x >> shift) & 255u], 1u);
+                    if ((x & msk) == pre) atomicAdd(&sm.hist[(x >> shift) & 255u], 1u);
                 }
             }
         }
@@ -396,17 +392,17 @@ __global__ __launch_bounds__(BS_T) void select_band_kernel(BandSelectArgs a) {
     }
     const uint32_t E = pre;   // the spec's k-th largest score; k = ties to take, first by index
     // ---- band keys above E into the selection bitmap, those equal to E into the tie bitmap
-    for (int q = tid; q < BS_MAXN / 32; q += BS_T) sm.v.eq[q] = 0;
+    for (int q = tid; q < BS_MAXN / 32; q += BS_T) sm.eq[q] = 0;
     __syncthreads();
     auto mark = [&](int j, uint32_t x) {
         if (x > E) atomicOr(&sm.gt[j >> 5], 1u << (j & 31));
-        else if (x == E) atomicOr(&sm.v.eq[j >> 5], 1u << (j & 31));
+        else if (x == E) atomicOr(&sm.eq[j >> 5], 1u << (j & 31));
     };
     if (listed) {
-        for (uint32_t q = tid; q < nband; q += BS_T) mark((int)sm.u.b.bj[q], sm.u.b.bx[q]);
+        for (uint32_t q = tid; q < nband; q += BS_T) mark((int)sm.bj[q], sm.bx[q]);
     } else {
         for (int j = tid; j < n; j += BS_T) {
-            const uint32_t key = sm.keys[j];
+            const uint32_t key = kr[j];
             if (key >= kout && key < kin) mark(j, ob32(spec_score(sm, a.ki, j)));
         }
     }
@@ -442,7 +438,7 @@ __global__ __launch_bounds__(BS_T) void select_band_kernel(BandSelectArgs a) {
         for (; g1; g1 &= g1 - 1) out[p++] = 64u * tid + 32u + __ffs(g1) - 1;
     }
     if (k > 0) {   // ties (k is uniform)
-        uint32_t e0 = sm.v.eq[2 * tid], e1 = sm.v.eq[2 * tid + 1];
+        uint32_t e0 = sm.eq[2 * tid], e1 = sm.eq[2 * tid + 1];
         uint32_t neq;
         uint32_t p = block_scan(__popc(e0) + __popc(e1), neq);
         for (; e0 && p < k; e0 &= e0 - 1) out[ngt + p++] = 64u * tid + __ffs(e0) - 1;
