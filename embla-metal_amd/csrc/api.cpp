@@ -304,7 +304,7 @@ int embla_sparse_decode(const void* q, const void* kc, const void* vc, const uin
 size_t embla_sparse_workspace_bytes(int max_s, int n_q) {
     if (max_s <= 0 || n_q <= 0) return 0;
     return round_up((size_t)max_s * 4, 256) + round_up((size_t)(kTopK + kRecent) * 4, 256) +
-           embla_workspace_bytes(kTopK + kRecent, n_q);
+           round_up(embla_workspace_bytes(kTopK + kRecent, n_q), 256) + kWideSelectWords * 4;
 }
 
 int embla_sparse_layer_decode(const void* q, const void* qi, const float* w, const void* ki, const void* kc,
@@ -319,9 +319,12 @@ int embla_sparse_layer_decode(const void* q, const void* qi, const float* w, con
     const size_t abytes = embla_workspace_bytes(kTopK + kRecent, n_q);
     if (S <= kTopK + kRecent)   // every key (Engine.swift:796-799: no selection yet)
         return embla_sparse_decode(q, kc, vc, nullptr, 0, S, o, max_s, n_q, n_kv, dtype, 0, aws, abytes, stream);
-    int rc = embla_index_scores(qi, w, ki, scores, S - kRecent, n_ih, stream);
-    if (rc) return rc;
-    rc = embla_select_topk(scores, 0, idx, 0, S, 1, kTopK, kRecent, stream);
+    if (n_ih != 1 && n_ih != 2 && n_ih != 4) return EMBLA_ERR_UNSUPPORTED;
+    // index scores, then the exact top-k on many workgroups (the select's workspace follows the
+    // decode's; it is zero before the first call and every call leaves it zero)
+    uint32_t* sel_ws = (uint32_t*)((char*)aws + round_up(abytes, 256));
+    const int rc = launch_wide_select((const uint16_t*)qi, w, (const uint16_t*)ki, scores, S, n_ih, kTopK, kRecent,
+                                      sel_ws, idx, stream);
     if (rc) return rc;
     return embla_sparse_decode(q, kc, vc, idx, 0, kTopK + kRecent, o, max_s, n_q, n_kv, dtype, 0, aws, abytes, stream);
 }

@@ -125,7 +125,15 @@ int launch_prefill_int8(const PrefillArgs& a, hipStream_t st);
 int launch_prefill_ring(const PrefillArgs& a, hipStream_t st);
 
 int launch_index_scores(const uint16_t* qi, const float* w, const uint16_t* ki, float* scores, int n, int n_ih,
-                        hipStream_t st);
+                        hipStream_t st, uint32_t* sw = nullptr);
+/// Words (4 bytes) of the wide select's workspace: two histogram buffers (8 copies of 256 coarse
+/// and 4096 fine bins), counters (first digit, keys above it, epoch), the candidate counts of the
+/// classify workgroups, the bitmap and their candidate regions (1024 pairs each).
+constexpr size_t kWideSelectWords = 2 * 8 * (256 + 4096) + 64 + 32768 / 1024 + 32768 / 32 + 2 * 32768;
+/// Index scores of keys [0, S - recent), then their exact top-k + recent into idx, on many
+/// workgroups (one set). sw: kWideSelectWords words, zero before the first call.
+int launch_wide_select(const uint16_t* qi, const float* w, const uint16_t* ki, float* scores, int S, int n_ih,
+                       int topk, int recent, uint32_t* sw, uint32_t* idx, hipStream_t st);
 
 struct KVQuantArgs {
     const uint16_t* k;   // [T] rows of k, row stride `stride` elements, kv head h at h * 128

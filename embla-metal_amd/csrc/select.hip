@@ -28,6 +28,11 @@ constexpr int HCOPIES = 2;                  // copies of the first pass's histog
 constexpr int HSTRIDE = HBINS + 1;          // words a copy (offset by one word: other banks)
 constexpr int LCAP = 2048;                  // bucket list capacity (else passes 2-3 read every key)
 constexpr int SEL_OUTCAP = HCOPIES * HSTRIDE + LCAP;   // topk indices staged in hist + list
+constexpr int DB = 4096;                    // the wide select's 12-bit digits: bits 31..20, 19..8
+constexpr int CB = 256;                     // its coarse first digit: bits 31..24
+constexpr int NCP = 8;                      // histogram copies (scorer workgroup % 8)
+constexpr int HCOPY = CB + DB;              // words a copy: coarse bins, then fine bins
+constexpr int HWORDS = NCP * HCOPY;         // words a histogram buffer (two, by call parity)
 
 __device__ __forceinline__ uint32_t order_bits(float f) {
     const uint32_t u = __float_as_uint(f);
@@ -284,14 +289,291 @@ int launch_select_topk(const float* scores, int score_stride, uint32_t* idx, int
     return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
 }
 
+// ------------------------------------------------------------------ wide select (one set)
+/// Digit (of 4096) holding the k-th largest of h: sel = {digit, keys in digits above}. Wave 0:
+/// each lane sums 64 digits from the top; the lane whose digits hold the k-th is found by a scan
+/// and a ballot, then its 64 digits go one a lane through a second scan.
+__device__ __forceinline__ void pick4096(const uint32_t* h, uint32_t k, uint32_t* sel) {
+    const int lane = threadIdx.x & 63;
+    const int b0 = DB - 64 - 64 * lane;   // the lane's digits b0 .. b0 + 63
+    uint32_t s = 0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const u4_t x = *(const u4_t*)(h + b0 + 4 * i);
+        s += (x[0] + x[1]) + (x[2] + x[3]);
+    }
+    uint32_t above = s;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t x = __shfl_up(above, o, 64);
+        if (lane >= o) above += x;
+    }
+    above -= s;
+    const int L = max(__ffsll((long long)__ballot(above < k && above + s >= k)) - 1, 0);   // 0 if none
+    const uint32_t base = __shfl(above, L, 64);
+    const int d = DB - 1 - 64 * L - lane;
+    const uint32_t c = h[d];
+    uint32_t incl = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += y;
+    }
+    if (base + incl - c < k && base + incl >= k) { sel[0] = (uint32_t)d; sel[1] = base + incl - c; }
+}
+
+/// Digit (of 256) holding the k-th largest: wave 0, 4 digits a lane from the top.
+__device__ __forceinline__ void pick256(const uint32_t* h, uint32_t k, uint32_t* sel) {
+    const int lane = threadIdx.x & 63;
+    uint32_t cc[4], s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) { cc[i] = h[255 - 4 * lane - i]; s += cc[i]; }
+    uint32_t above = s;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t x = __shfl_up(above, o, 64);
+        if (lane >= o) above += x;
+    }
+    above -= s;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if (above < k && above + cc[i] >= k) { sel[0] = 255u - (4 * lane + i); sel[1] = above; }
+        above += cc[i];
+    }
+}
+
+/// The wide select's second step, a 256-thread workgroup a 1024 keys. Every workgroup finds the
+/// 12-bit first digit d1 holding the topk-th largest from the scorer's histograms: the coarse
+/// digit from the 256 coarse bins (summed over the copies), then d1 among that digit's 16 fine
+/// bins (workgroup 0 records d1 and the keys above it). For its keys j = base + t + 256 e it then
+/// writes the bitmap of keys whose digit is above d1 (a ballot covers 64 consecutive keys: two
+/// words, no atomics) and the keys in digit d1 (order bits, index) to its own candidate region
+/// (slots from an LDS counter), whose count it stores for the last step.
+__global__ __launch_bounds__(256) void wsel_classify_kernel(const float* __restrict__ scores, int n, int topk,
+                                                            uint32_t* __restrict__ sw) {
+    __shared__ uint32_t ch[CB], fh[NCP][16], sel[2], lcnt;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    uint32_t* meta = sw + 2 * HWORDS;
+    uint32_t* cnts = meta + 64;
+    uint32_t* gt = cnts + SEL_MAXN / 1024;
+    uint32_t* cand = gt + SEL_MAXN / 32 + 2 * 1024 * blockIdx.x;
+    const uint32_t* H = sw + (meta[3] & 1) * HWORDS;
+    const int base = blockIdx.x * 1024;
+    float sv[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int j = base + tid + 256 * e;
+        sv[e] = j < n ? scores[j] : 0.0f;
+    }
+    uint32_t c = 0;
+#pragma unroll
+    for (int cp = 0; cp < NCP; cp++) c += H[cp * HCOPY + tid];
+    ch[tid] = c;
+    if (tid == 0) { sel[0] = 0; sel[1] = 0; lcnt = 0; }
+    __syncthreads();
+    if (w == 0) pick256(ch, (uint32_t)topk, sel);
+    __syncthreads();
+    const uint32_t cd = sel[0] & (CB - 1), above_c = sel[1];
+    if (tid < NCP * 16) fh[tid >> 4][tid & 15] = H[(tid >> 4) * HCOPY + CB + 16 * cd + (tid & 15)];
+    if (tid == 0) sel[0] = 16 * cd;
+    __syncthreads();
+    if (w == 0) {   // lanes < 16: fine bins 16 cd + 15 - lane, from the top
+        uint32_t v = 0;
+        if (lane < 16)
+#pragma unroll
+            for (int cp = 0; cp < NCP; cp++) v += fh[cp][15 - lane];
+        uint32_t incl = v;
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) {
+            const uint32_t x = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += x;
+        }
+        const uint32_t k1 = (uint32_t)topk - above_c;
+        if (lane < 16 && incl - v < k1 && incl >= k1) { sel[0] = 16 * cd + 15 - lane; sel[1] = above_c + incl - v; }
+    }
+    __syncthreads();
+    const uint32_t d1 = sel[0];
+    if (blockIdx.x == 0 && tid == 0) { meta[1] = d1; meta[2] = sel[1]; }
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int j = base + tid + 256 * e;
+        const bool real = j < n;
+        const uint32_t key = order_bits(sv[e]), dg = key >> 20;
+        const uint64_t bg = __ballot(real && dg > d1), bc = __ballot(real && dg == d1);
+        if (lane == 0) {
+            const int wd = (base + 256 * e + 64 * w) >> 5;
+            gt[wd] = (uint32_t)bg;
+            gt[wd + 1] = (uint32_t)(bg >> 32);
+        }
+        if (bc) {
+            uint32_t p0 = 0;
+            if (lane == 0) p0 = atomicAdd(&lcnt, (uint32_t)__popcll(bc));
+            p0 = __shfl(p0, 0, 64);
+            if (real && dg == d1) {
+                const uint32_t p = p0 + __builtin_amdgcn_mbcnt_hi((uint32_t)(bc >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bc, 0u));
+                cand[2 * p] = key;   // p < 1024: a workgroup has 1024 keys
+                cand[2 * p + 1] = (uint32_t)j;
+            }
+        }
+    }
+    __syncthreads();
+    if (tid == 0) cnts[blockIdx.x] = lcnt;
+}
+
+/// Exclusive prefix sum over a 1024-thread workgroup, and the total.
+__device__ __forceinline__ uint32_t wsel_scan(uint32_t v, uint32_t* wsum, uint32_t& total) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    uint32_t incl = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t x = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += x;
+    }
+    if (lane == 63) wsum[w] = incl;
+    __syncthreads();
+    uint32_t before = 0;
+    total = 0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const uint32_t x = wsum[i];
+        before += i < w ? x : 0u;
+        total += x;
+    }
+    __syncthreads();   // wsum is reused by the next scan
+    return before + incl - v;
+}
+
+/// The wide select's last step, one 1024-thread workgroup: the second (bits 19..8) and third
+/// (7..0) radix levels over the candidate list give the topk-th largest value E and how many
+/// keys equal to it are taken; candidates above E join the bitmap, those equal to E form the tie
+/// bitmap; block scans of the bitmaps' popcounts give the output in select_keys' order. It then
+/// advances the epoch (the next call's histogram buffer). Counts are clamped and every write is
+/// bounded, so a workspace that was not zeroed gives a wrong selection, never a stray access.
+__global__ __launch_bounds__(1024) void wsel_final_kernel(int n, int topk, int recent, uint32_t* __restrict__ sw,
+                                                          uint32_t* __restrict__ out) {
+    __shared__ __attribute__((aligned(16))) uint32_t h2[DB];
+    __shared__ uint32_t gts[SEL_MAXN / 32], eqs[SEL_MAXN / 32], wsum[16], sel[2];
+    const int tid = threadIdx.x, w = tid >> 6;
+    __shared__ uint32_t coff[SEL_MAXN / 1024 + 1];
+    __shared__ __attribute__((aligned(16))) uint32_t cl[2 * SEL_MAXN / 4];   // candidates, when they fit (else in place)
+    uint32_t* meta = sw + 2 * HWORDS;
+    const uint32_t* cnts = meta + 64;
+    const uint32_t* gt = cnts + SEL_MAXN / 1024;
+    const uint32_t* creg = gt + SEL_MAXN / 32;
+    const uint32_t d1 = meta[1] & (DB - 1);
+    uint32_t k = (uint32_t)topk - min(meta[2], (uint32_t)topk - 1);
+    const int nw = (n + 31) / 32, nb = (n + 1023) / 1024;
+    for (int q = tid; q < DB; q += 1024) h2[q] = 0;
+    gts[tid] = tid < nw ? gt[tid] : 0u;
+    eqs[tid] = 0;
+    if (tid == 0) {   // offsets of the workgroups' candidate regions in the list
+        uint32_t o = 0;
+        for (int b = 0; b < nb; b++) { coff[b] = o; o += min(cnts[b], 1024u); }
+        coff[nb] = o;
+    }
+    __syncthreads();
+    const uint32_t cnt = coff[nb];
+    const bool inl = cnt <= SEL_MAXN / 4;
+    // the list: candidate q of region b at creg[2 (1024 b + q - coff[b])]
+    auto cand_at = [&](uint32_t q, uint32_t& key, uint32_t& j) {
+        int b = 0;
+        while (b + 1 < nb && coff[b + 1] <= q) b++;
+        const uint32_t* c2 = creg + 2 * (1024 * b + (q - coff[b]));
+        key = c2[0];
+        j = c2[1];
+    };
+    if (inl) {   // wave w copies regions w, w + 16: no search
+        for (int b = w; b < nb; b += 16) {
+            const uint32_t nc = coff[b + 1] - coff[b];
+            for (uint32_t q = tid & 63; q < nc; q += 64) {
+                const u2_t v = *(const u2_t*)(creg + 2 * (1024 * b + q));
+                *(u2_t*)(cl + 2 * (coff[b] + q)) = v;
+            }
+        }
+        __syncthreads();
+    }
+    auto cand = [&](uint32_t q, uint32_t& key, uint32_t& j) {
+        if (inl) { key = cl[2 * q]; j = cl[2 * q + 1]; }
+        else cand_at(q, key, j);
+    };
+    for (uint32_t q = tid; q < cnt; q += 1024) {
+        uint32_t key, j;
+        cand(q, key, j);
+        atomicAdd(&h2[(key >> 8) & 0xFFF], 1u);
+    }
+    if (tid == 0) { sel[0] = 0; sel[1] = 0; }
+    __syncthreads();
+    if (w == 0) pick4096(h2, k, sel);
+    __syncthreads();
+    const uint32_t p2 = (d1 << 12) | (sel[0] & (DB - 1));
+    k -= sel[1];
+    __syncthreads();
+    if (tid < 256) h2[tid] = 0;
+    __syncthreads();
+    for (uint32_t q = tid; q < cnt; q += 1024) {
+        uint32_t key, j;
+        cand(q, key, j);
+        if ((key >> 8) == p2) atomicAdd(&h2[key & 255], 1u);
+    }
+    if (tid == 0) { sel[0] = 0; sel[1] = 0; }
+    __syncthreads();
+    if (w == 0) pick256(h2, k, sel);
+    __syncthreads();
+    const uint32_t E = (p2 << 8) | (sel[0] & 255);
+    k -= sel[1];   // keys equal to E to take (>= 1)
+    for (uint32_t q = tid; q < cnt; q += 1024) {
+        uint32_t key, j;
+        cand(q, key, j);
+        j &= SEL_MAXN - 1;
+        if (key > E) atomicOr(&gts[j >> 5], 1u << (j & 31));
+        else if (key == E) atomicOr(&eqs[j >> 5], 1u << (j & 31));
+    }
+    __syncthreads();
+    uint32_t ngt, neq;
+    {
+        uint32_t g = gts[tid];
+        uint32_t p = wsel_scan(__popc(g), wsum, ngt);
+        for (; g && p < (uint32_t)topk; g &= g - 1) out[p++] = 32u * tid + __ffs(g) - 1;
+    }
+    {
+        uint32_t e = eqs[tid];
+        uint32_t p = wsel_scan(__popc(e), wsum, neq);
+        for (; e && p < k && ngt + p < (uint32_t)topk; e &= e - 1) out[ngt + p++] = 32u * tid + __ffs(e) - 1;
+    }
+    for (int j = tid; j < recent; j += 1024) out[topk + j] = (uint32_t)(n + j);
+    if (tid == 0) meta[3] += 1;   // the next call uses the other histogram buffer
+}
+
+int launch_wide_select(const uint16_t* qi, const float* w, const uint16_t* ki, float* scores, int S, int n_ih,
+                       int topk, int recent, uint32_t* sw, uint32_t* idx, hipStream_t st) {
+    const int n = S - recent;
+    if (n > SEL_MAXN || n <= topk) return EMBLA_ERR_UNSUPPORTED;
+    int rc = launch_index_scores(qi, w, ki, scores, n, n_ih, st, sw);
+    if (rc) return rc;
+    hipLaunchKernelGGL(wsel_classify_kernel, dim3((n + 1023) / 1024), dim3(256), 0, st, scores, n, topk, sw);
+    hipLaunchKernelGGL(wsel_final_kernel, dim3(1), dim3(1024), 0, st, n, topk, recent, sw, idx);
+    return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
+}
+
 // ------------------------------------------------------------------ index scorer
 /// One set of n_ih (<= 4) fp16 index queries [n_ih][64] and weights; keys ki [n][64] fp16.
 /// A wave takes 64 keys a round: load j (16 bytes a lane) covers keys 8j .. 8j + 7, lane l holding
 /// key 8j + l / 8, dims 8 (l % 8) .. + 7, so every load of the wave reads 1 KB contiguous.
+/// With the wide select's workspace `sw`, each workgroup also counts its scores' top 12 order bits
+/// in LDS and adds them to histogram copy blockIdx % 8 of this call's buffer (sw's epoch word
+/// picks one of two): fine bins (12 bits) and coarse bins (top 8), thread t adding the 16 fine
+/// bins of coarse bin t. It also clears its slice of the other buffer for the next call.
 template <int NIH>
 __global__ __launch_bounds__(256) void index_scores_kernel(const uint16_t* __restrict__ qi, const float* __restrict__ wt,
                                                            const uint16_t* __restrict__ ki, float* __restrict__ scores,
-                                                           int n) {
+                                                           int n, uint32_t* __restrict__ sw) {
+    __shared__ uint32_t lh[DB];
+    uint32_t epoch = 0;
+    if (sw) {
+        epoch = sw[2 * HWORDS + 3];
+        for (int b = threadIdx.x; b < DB; b += 256) lh[b] = 0;
+        __syncthreads();
+    }
     const int lane = threadIdx.x & 63, kq = lane & 7;
     const int wave = blockIdx.x * 4 + (threadIdx.x >> 6), nwaves = gridDim.x * 4;
     float q[NIH][8], w[NIH];
@@ -334,21 +616,38 @@ __global__ __launch_bounds__(256) void index_scores_kernel(const uint16_t* __res
                 s = __builtin_fmaf(w[h], r2, s);
             }
             const int key = base + 8 * j + (lane >> 3);
-            if (kq == 0 && key < n) scores[key] = s;
+            if (kq == 0 && key < n) {
+                scores[key] = s;
+                if (sw) atomicAdd(&lh[order_bits(s) >> 20], 1u);
+            }
         }
+    }
+    if (sw) {
+        __syncthreads();
+        const int t = threadIdx.x;
+        uint32_t* H = sw + (epoch & 1) * HWORDS + (blockIdx.x % NCP) * HCOPY;
+        uint32_t cs = 0;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const uint32_t c = lh[16 * t + i];
+            if (c) { atomicAdd(&H[CB + 16 * t + i], c); cs += c; }
+        }
+        if (cs) atomicAdd(&H[t], cs);
+        uint32_t* Z = sw + ((epoch + 1) & 1) * HWORDS;
+        for (int q = blockIdx.x * 256 + t; q < HWORDS; q += gridDim.x * 256) Z[q] = 0;
     }
 }
 
 int launch_index_scores(const uint16_t* qi, const float* w, const uint16_t* ki, float* scores, int n, int n_ih,
-                        hipStream_t st) {
+                        hipStream_t st, uint32_t* sw) {
     const int waves = (n + 63) / 64;
     int blocks = (waves + 3) / 4;
     if (blocks > 1024) blocks = 1024;
     if (blocks < 1) blocks = 1;
     switch (n_ih) {
-        case 1: hipLaunchKernelGGL(index_scores_kernel<1>, dim3(blocks), dim3(256), 0, st, qi, w, ki, scores, n); break;
-        case 2: hipLaunchKernelGGL(index_scores_kernel<2>, dim3(blocks), dim3(256), 0, st, qi, w, ki, scores, n); break;
-        case 4: hipLaunchKernelGGL(index_scores_kernel<4>, dim3(blocks), dim3(256), 0, st, qi, w, ki, scores, n); break;
+        case 1: hipLaunchKernelGGL(index_scores_kernel<1>, dim3(blocks), dim3(256), 0, st, qi, w, ki, scores, n, sw); break;
+        case 2: hipLaunchKernelGGL(index_scores_kernel<2>, dim3(blocks), dim3(256), 0, st, qi, w, ki, scores, n, sw); break;
+        case 4: hipLaunchKernelGGL(index_scores_kernel<4>, dim3(blocks), dim3(256), 0, st, qi, w, ki, scores, n, sw); break;
         default: return EMBLA_ERR_UNSUPPORTED;
     }
     return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;

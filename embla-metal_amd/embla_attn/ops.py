@@ -127,12 +127,19 @@ def sparse_decode(q, kc, vc, idx, nsel, max_s, n_kv, idx_stride=0, dtype=F16, ch
 
 class SparseWorkspace:
     def __init__(self, max_s: int, n_q: int = 16, device="cuda"):
+        self.max_s = max_s
         self.nbytes = int(lib().embla_sparse_workspace_bytes(max_s, n_q))
         self.buf = torch.zeros(self.nbytes, dtype=torch.uint8, device=device)
 
     @property
     def ptr(self):
         return _p(self.buf)
+
+    def selection(self):
+        """The last sparse_layer_decode call's selected rows (top 1024 + latest 128), int32 [1152]:
+        the workspace region after the scores (embla_sparse_layer_decode's layout)."""
+        off = (self.max_s * 4 + 255) // 256 * 256
+        return self.buf[off:off + 1152 * 4].view(torch.int32)
 
 
 def sparse_layer_decode(q, qi, w, ki, kc, vc, S, max_s, n_kv, ws: SparseWorkspace, dtype=F16, out=None,

@@ -136,7 +136,8 @@ int embla_sparse_decode(const void* q, const void* kc, const void* vc, const uin
                         int nsel, void* o, int max_s, int n_q, int n_kv, int dtype, int chunk, void* ws,
                         size_t ws_bytes, hipStream_t stream);
 
-/* Bytes of workspace for embla_sparse_layer_decode. */
+/* Bytes of workspace for embla_sparse_layer_decode: zero-filled before its first use (every call
+ * leaves its counters zero again). */
 size_t embla_sparse_workspace_bytes(int max_s, int n_q);
 
 /* One sparse-layer decode step (config C4): with S > 1152 keys, index scores of keys

@@ -102,6 +102,42 @@ def test_sparse_layer_end_to_end(torch_gpu, orc, c4, S):
     assert_close(f16_host(o), ref, what=f"S={S}")
 
 
+def test_sparse_layer_selection_bit_exact(torch_gpu, orc, c4):
+    """The layer's selection (scorer histogram, wide classify, final select on the candidates) is
+    select_keys' output bit for bit, over consecutive calls of one workspace at different S (each
+    call leaves the select's counters zero for the next)."""
+    from embla_attn import ops
+    torch = torch_gpu
+    ws = ops.SparseWorkspace(32768, 16)
+    args = [dev(c4["q"], torch.float16), dev(c4["qi"], torch.float16), dev(c4["w"]), dev(c4["ki"], torch.float16),
+            dev(c4["K"], torch.float16), dev(c4["V"], torch.float16)]
+    for S in [32768, 5000, 1153, 32768, 20011]:
+        say(f"sparse layer selection S={S}")
+        ops.sparse_layer_decode(*args, S, 32768, 4, ws)
+        got = ws.selection().cpu().numpy().astype(np.uint32)
+        sc = orc.index_scores(c4["qi"], c4["w"], c4["ki"][:S - 128])
+        ref = orc.select_keys(np.concatenate([sc, np.zeros(128, np.float32)]), S)
+        np.testing.assert_array_equal(got, ref, err_msg=f"S={S}")
+
+
+def test_sparse_layer_selection_ties(torch_gpu, orc, c4):
+    """Index keys repeated 16 times: every score occurs 16 times, so the threshold value is tied
+    and the first of its keys by index are taken."""
+    from embla_attn import ops
+    torch = torch_gpu
+    S = 30000
+    ki = np.repeat(c4["ki"][:2048], 16, axis=0)
+    ws = ops.SparseWorkspace(32768, 16)
+    say("sparse layer selection ties")
+    ops.sparse_layer_decode(dev(c4["q"], torch.float16), dev(c4["qi"], torch.float16), dev(c4["w"]),
+                            dev(ki, torch.float16), dev(c4["K"], torch.float16), dev(c4["V"], torch.float16),
+                            S, 32768, 4, ws)
+    got = ws.selection().cpu().numpy().astype(np.uint32)
+    sc = orc.index_scores(c4["qi"], c4["w"], ki[:S - 128])
+    ref = orc.select_keys(np.concatenate([sc, np.zeros(128, np.float32)]), S)
+    np.testing.assert_array_equal(got, ref)
+
+
 def test_select_topk_many_sets_unaligned(torch_gpu, orc):
     """Several sets at an odd stride (rows not 16-byte aligned), ragged n, a small topk."""
     from embla_attn import ops
