@@ -466,10 +466,17 @@ __global__ __launch_bounds__(1024) void wsel_final_kernel(int n, int topk, int r
     for (int q = tid; q < DB; q += 1024) h2[q] = 0;
     gts[tid] = tid < nw ? gt[tid] : 0u;
     eqs[tid] = 0;
-    if (tid == 0) {   // offsets of the workgroups' candidate regions in the list
-        uint32_t o = 0;
-        for (int b = 0; b < nb; b++) { coff[b] = o; o += min(cnts[b], 1024u); }
-        coff[nb] = o;
+    if (w == 0) {   // offsets of the workgroups' candidate regions in the list (nb <= 32)
+        const int lane = tid & 63;
+        const uint32_t c = lane < nb ? min(cnts[lane], 1024u) : 0u;
+        uint32_t incl = c;
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) {
+            const uint32_t x = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += x;
+        }
+        if (lane < nb) coff[lane] = incl - c;
+        if (lane == nb - 1) coff[nb] = incl;
     }
     __syncthreads();
     const uint32_t cnt = coff[nb];
