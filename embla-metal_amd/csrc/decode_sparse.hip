@@ -470,7 +470,7 @@ __global__ __launch_bounds__(256, 4) void sparse_rows8_rm_kernel(SparseRows8Args
 
     constexpr int MERGE = (4 * GQ * HD + 8 * GQ) * 4;
     __shared__ __attribute__((aligned(16))) char smem[MERGE];
-    __shared__ uint32_t sidx[SPR_MAXSEL];
+    __shared__ __attribute__((aligned(16))) uint32_t sidx[SPR_MAXSEL];   // the key list, padded with row 0
     __shared__ __attribute__((aligned(16))) float sks[4][2][32];   // per wave: k scales, v scales
 
     // the key list: every load issued before the first store (rows clamped in range)
@@ -480,7 +480,7 @@ __global__ __launch_bounds__(256, 4) void sparse_rows8_rm_kernel(SparseRows8Args
 #pragma unroll
     for (int i = 0; i < LP; i++) {
         const int p = tid + 256 * i;
-        lr[i] = p < nk ? (rows ? (int)rows[j0 + p] : j0 + p) : 0;
+        lr[i] = p < nk ? (rows ? (int)rows[j0 + p] : j0 + p) : 0;   // past nk: row 0 (masked by position)
     }
 
     // q^T as the B operand: column n < GQ hi of head n, column GQ + n lo; lane (n, g), MFMA h:
@@ -496,9 +496,10 @@ __global__ __launch_bounds__(256, 4) void sparse_rows8_rm_kernel(SparseRows8Args
         for (int h = 0; h < 2; h++)
 #pragma unroll
             for (int u = 0; u < 2; u++) qv[2 * h + u] = ld16(qr + 64 * h + 8 * u);
+        const int npad = (nk + 31) & ~31;   // whole 32-key steps
 #pragma unroll
         for (int i = 0; i < LP; i++)
-            if (tid + 256 * i < nk) sidx[tid + 256 * i] = (uint32_t)min(lr[i], a.max_s - 1);
+            if (tid + 256 * i < npad) sidx[tid + 256 * i] = (uint32_t)min(max(lr[i], 0), a.max_s - 1);
         float qf[32];
         const bool qbf = a.q_bf16;
 #pragma unroll
@@ -543,25 +544,21 @@ __global__ __launch_bounds__(256, 4) void sparse_rows8_rm_kernel(SparseRows8Args
     // one 32-key step's raw bytes: K[2t + h] = key 16t + n, dims 64h + 16g ..; V[e] = key
     // 16(e / 4) + 4g + e % 4, dims 8n .. 8n + 7; lanes < 32 hold key t0 + lane's two scales
     struct Raw { u4_t k[4]; u2_t v[8]; uint32_t s; };
+    // rows as 32-bit byte offsets from the kv head's base (< 2^31: max_s * 128 a head)
     auto gather_k = [&](int t0, Raw& R) {
 #pragma unroll
         for (int t = 0; t < 2; t++) {
-            const int p = t0 + 16 * t + n;
-            const size_t row = p < nk ? sidx[p] : 0;
+            const uint32_t off = sidx[t0 + 16 * t + n] * (uint32_t)HD + 16 * g;
 #pragma unroll
-            for (int h = 0; h < 2; h++) R.k[2 * t + h] = ld16(kb + row * HD + 64 * h + 16 * g);
+            for (int h = 0; h < 2; h++) R.k[2 * t + h] = ld16(kb + off + 64 * h);
         }
-        const int p = t0 + (lane & 31);
-        const size_t row = p < nk ? sidx[p] : 0;
+        const uint32_t row = sidx[t0 + (lane & 31)];
         R.s = lane < 32 ? ksc[row] : vsc[row];
     };
     auto gather_v = [&](int t0, Raw& R) {
+        const u4_t ra = *(const u4_t*)(sidx + t0 + 4 * g), rb = *(const u4_t*)(sidx + t0 + 16 + 4 * g);
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const int p = t0 + 16 * (e >> 2) + 4 * g + (e & 3);
-            const size_t row = p < nk ? sidx[p] : 0;
-            R.v[e] = ld8(vb + row * HD + 8 * n);
-        }
+        for (int e = 0; e < 8; e++) R.v[e] = ld8(vb + (e < 4 ? ra[e] : rb[e - 4]) * (uint32_t)HD + 8 * n);
     };
     Raw A;
     if (32 * w < nk) { gather_k(32 * w, A); gather_v(32 * w, A); }
