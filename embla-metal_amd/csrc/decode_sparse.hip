@@ -518,7 +518,8 @@ __global__ __launch_bounds__(256, 4) void sparse_rows8_rm_kernel(SparseRows8Args
         am = fmaxf(am, shfl_xor(am, 16));
         am = fmaxf(am, shfl_xor(am, 32));
         const float inv = am > 0.0f ? QFIX / am : 0.0f;
-        qsc = am / QFIX * (0.08838834764831845f * 1.4426950408889634f);   // step x 1/sqrt(128) x log2(e)
+        // step x 1/sqrt(128) x log2(e), applied in the exponent's fma (> 0, so -inf scores stay -inf)
+        qsc = fmaxf(am / QFIX * (0.08838834764831845f * 1.4426950408889634f), 1e-30f);
 #pragma unroll
         for (int h = 0; h < 2; h++)
 #pragma unroll
@@ -540,6 +541,12 @@ __global__ __launch_bounds__(256, 4) void sparse_rows8_rm_kernel(SparseRows8Args
     f4_t O[8];
 #pragma unroll
     for (int u = 0; u < 8; u++) O[u] = (f4_t){0, 0, 0, 0};
+    // V enters the P·V products as fp16 1152 + v (its bytes with 0x80 flipped under an 0x64 high
+    // byte: no subtract a dword); OB accumulates 1152 · Σ w with one more MFMA against a constant
+    // operand, and is subtracted from O at the end. The products are exact and the fp32 sums carry
+    // the bias' rounding at ~2^-24 of 1152 · Σ w a step.
+    f4_t OB = {0, 0, 0, 0};
+    const h8_t c1152 = __builtin_bit_cast(h8_t, (u4_t){0x64806480u, 0x64806480u, 0x64806480u, 0x64806480u});
 
     // one 32-key step's raw bytes: K[2t + h] = key 16t + n, dims 64h + 16g ..; V[e] = key
     // 16(e / 4) + 4g + e % 4, dims 8n .. 8n + 7; lanes < 32 hold key t0 + lane's two scales
@@ -583,14 +590,14 @@ __global__ __launch_bounds__(256, 4) void sparse_rows8_rm_kernel(SparseRows8Args
             for (int i = 0; i < 4; i++) {
                 const int lo = __shfl_xor(st[t][i], GQ, 64);
                 const float kq = t == 0 ? kq0[i] : kq1[i];
-                x[4 * t + i] = t0 + 16 * t + 4 * g + i < nk ? (float)(st[t][i] * 256 + lo) * qsc * kq : NEG_INF;
+                x[4 * t + i] = t0 + 16 * t + 4 * g + i < nk ? (float)(st[t][i] * 256 + lo) * kq : NEG_INF;
             }
         float mt = NEG_INF;
 #pragma unroll
         for (int e = 0; e < 8; e++) mt = fmaxf(mt, x[e]);
         mt = fmaxf(mt, shfl_xor(mt, 16));
         mt = fmaxf(mt, shfl_xor(mt, 32));
-        const float mn = fmaxf(m, mt);
+        const float mn = fmaxf(m, mt * qsc);
         if (__any(n < GQ && mn > m)) {
             if (__any(n < GQ && m != NEG_INF)) {
                 const float corr = m == NEG_INF ? 0.0f : exp2f(m - mn);
@@ -606,34 +613,40 @@ __global__ __launch_bounds__(256, 4) void sparse_rows8_rm_kernel(SparseRows8Args
                 for (int u = 0; u < 8; u++)
 #pragma unroll
                     for (int i = 0; i < 4; i++) O[u][i] *= cf[i];
+#pragma unroll
+                for (int i = 0; i < 4; i++) OB[i] *= cf[i];
             }
             m = mn;
         }
         h8_t wa;
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            const float p = __builtin_amdgcn_exp2f(x[e] - m);   // x = -inf -> 0
+            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(x[e], qsc, -m));   // x = -inf -> 0
             l += p;
             wa[e] = (_Float16)(p * (e < 4 ? vq0[e & 3] : vq1[e & 3]));
         }
         // B operand of MFMA u: halves (V[e][8n + u], V[e + 1][8n + u]) a dword: byte u of keys e
         // and e + 1 into bytes 0 and 2, then XOR 0x80 into them and 0x64 into bytes 1 and 3 gives
-        // the fp16 pair 1152 + x; minus 1152 (exact in fp16)
-        const h2_t bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+        // the fp16 pair 1152 + x
+        OB = mfma16(wa, c1152, OB);
 #pragma unroll
         for (int u = 0; u < 8; u++) {
             u4_t b;
 #pragma unroll
             for (int e = 0; e < 8; e += 2) {
                 const uint32_t sel = (u & 3) | (((u & 3) + 4) << 16) | 0x0C000C00u;
-                const uint32_t d = __builtin_amdgcn_perm(A.v[e + 1][u >> 2], A.v[e][u >> 2], sel) ^ 0x64806480u;
-                b[e / 2] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, d) + bias);
+                b[e / 2] = __builtin_amdgcn_perm(A.v[e + 1][u >> 2], A.v[e][u >> 2], sel) ^ 0x64806480u;
             }
             O[u] = mfma16(wa, __builtin_bit_cast(h8_t, b), O[u]);
         }
         if (t0 + 128 < nk) gather_v(t0 + 128, A);
         wave_lds_sync();   // the next step's scale stores come after every lane's reads
     }
+
+#pragma unroll
+    for (int u = 0; u < 8; u++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) O[u][i] -= OB[i];   // the V bias
 
     // ---- merge the 4 waves (LDS), then the row's output or this chunk's partial
     float (*om)[GQ][HD] = (float (*)[GQ][HD])smem;
