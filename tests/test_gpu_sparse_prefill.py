@@ -55,7 +55,7 @@ def run(torch, c):
     ws = ops.SparsePrefillWorkspace(T, p0)
     o, _ = ops.prefill_sparse(dev(c["q"], torch.bfloat16), dev(c["kn"], torch.bfloat16), dev(c["vn"], torch.bfloat16),
                               dev(c["qi"], torch.float16), dev(c["w"]), dev(c["ki"], torch.float16), kc, vc, T, p0,
-                              max_s, 4, ws, idx=idx)
+                              max_s, c["n_kv"], ws, idx=idx)
     return bf16_host(o), idx.cpu().numpy().astype(np.uint32), kc, max_s
 
 
@@ -78,6 +78,15 @@ def check_rows(orc, c, got, idx, rows, cache):
 def test_prefill_sparse_small(torch_gpu, orc, p0, T):
     say(f"prefill sparse p0={p0} T={T}")
     c = synth.sparse_prefill_case(seed=4, p0=p0, T=T)
+    got, idx, _, _ = run(torch_gpu, c)
+    check_rows(orc, c, got, idx, range(T), oracle_cache(orc, c))
+
+
+def test_prefill_sparse_gq8(torch_gpu, orc):
+    """8 query heads a kv head (32 over 4): the gather kernel's GQ = 8 variant."""
+    p0, T = 1400, 48
+    say("prefill sparse GQ 8")
+    c = synth.sparse_prefill_case(seed=8, p0=p0, T=T, n_q=32, n_kv=4)
     got, idx, _, _ = run(torch_gpu, c)
     check_rows(orc, c, got, idx, range(T), oracle_cache(orc, c))
 
