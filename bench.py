@@ -146,6 +146,30 @@ def bench_c4(torch, reps=20):
                 gbs=nbytes / (ms * 1e-3) / 1e9)
 
 
+def bench_blocks(torch, reps=20):
+    """Prefix-cache block save + restore (§8 next row 2): 16 blocks (positions 16384 + 128 i ..,
+    i < 16) of 16 full layers at C3's shape (4 kv heads, 32768 positions, int8 + fp16 scales), each
+    saved then restored, in one graph (a graph of a single pair would time the graph launch);
+    bytes = each copy's reads and writes."""
+    from embla_attn import layout, ops
+    n_layers, n_kv, max_s, p0 = 16, 4, 32768, 16384
+    rb = (layout.region_bytes(n_kv, max_s, 2) + 255) // 256 * 256
+    cache = torch.zeros(2 * n_layers * rb, dtype=torch.uint8, device="cuda")
+    regions = [[(2 * l) * rb, (2 * l + 1) * rb] for l in range(n_layers)]
+    nbytes = ops.lib().embla_kv_block_bytes(n_layers, n_kv, ops.F16)
+    nblk = 16
+    stored = torch.empty(nblk * nbytes, dtype=torch.uint8, device="cuda")
+
+    def run():
+        for i in range(nblk):
+            ops.kv_block_copy(cache, regions, p0 + 128 * i, max_s, n_kv, stored[i * nbytes:], True)
+            ops.kv_block_copy(cache, regions, p0 + 128 * i, max_s, n_kv, stored[i * nbytes:], False)
+    wall, ms = time_graph(torch, run, reps, 3)
+    us = ms * 1000 / nblk
+    moved = 2 * 2 * nbytes   # a save and a restore, each reading and writing the block
+    return dict(block_bytes=nbytes, us_save_restore=us, gbs=moved / (us * 1e-6) / 1e9)
+
+
 def prefill_flops(p0: int, T: int, n_q: int = 16, window: int = 0) -> float:
     """Algorithmic FLOPs of causal prefill attention: 4·128 a (query row, key) pair (QK and PV)."""
     pairs = 0
@@ -303,6 +327,7 @@ def main():
     c2 = bench_c2(torch)
     c4 = bench_c4(torch)
     c5 = bench_c5(torch)
+    blocks = bench_blocks(torch)
     head = res[L]
     line = {
         "metric": METRIC,
@@ -338,6 +363,7 @@ def main():
         "c5_prefill_full": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c5.items()
                             if k not in ("sliding", "sparse")},
         "c5_prefill_sparse": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c5["sparse"].items()},
+        "kv_block_save_restore": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in blocks.items()},
         "c5_prefill_sliding": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c5["sliding"].items()},
     }
     if not args.no_cpu:

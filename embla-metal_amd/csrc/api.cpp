@@ -466,4 +466,57 @@ int embla_prefill_sparse(const void* q, const void* k, const void* v, const void
     return launch_sparse_rows8(sa, stream);
 }
 
+// ---------------------------------------------------------------- prefix-cache blocks
+size_t embla_kv_block_bytes(int n_layers, int n_kv, int scale_dtype) {
+    if (n_layers <= 0 || n_kv <= 0 || !valid_scale(scale_dtype)) return 0;
+    return (size_t)n_layers * 2 * n_kv * 128 * (128 + (scale_dtype == EMBLA_F32 ? 4 : 2));
+}
+
+int embla_kv_block_copy(void* cache, const unsigned long long* regions, int n_layers, int p0, int max_s, int n_kv,
+                        int scale_dtype, void* stored, int save, hipStream_t stream) {
+    if (!cache || !regions || !stored || n_layers <= 0 || n_layers > kMaxBlockLayers) return EMBLA_ERR_INVALID;
+    if (n_kv <= 0 || n_kv > kMaxKV || max_s <= 0 || max_s % 32 || p0 < 0 || p0 % 128 || p0 + 128 > max_s)
+        return EMBLA_ERR_INVALID;
+    if (!valid_scale(scale_dtype)) return EMBLA_ERR_INVALID;
+    BlockCopyArgs a{};
+    a.cache = (char*)cache;
+    a.stored = (char*)stored;
+    for (int l = 0; l < 2 * n_layers; l++) {
+        if (regions[l] % 16) return EMBLA_ERR_INVALID;
+        a.off[l] = regions[l];
+    }
+    a.n_layers = n_layers; a.n_kv = n_kv; a.max_s = max_s; a.p0 = p0;
+    a.elem = 1;
+    a.row_units = 128 * 128 / 16;
+    a.scale_bytes = scale_dtype == EMBLA_F32 ? 4 : 2;
+    a.scale_units = 128 * a.scale_bytes / 16;
+    a.save = save ? 1 : 0;
+    return launch_block_copy(a, stream);
+}
+
+size_t embla_ring_block_bytes(int n_layers, int n_kv) {
+    if (n_layers <= 0 || n_kv <= 0) return 0;
+    return (size_t)n_layers * 2 * n_kv * 128 * 128 * 2;
+}
+
+int embla_ring_block_copy(void* cache, const unsigned long long* regions, int n_layers, int p0, int ring, int n_kv,
+                          void* stored, int save, hipStream_t stream) {
+    if (!cache || !regions || !stored || n_layers <= 0 || n_layers > kMaxBlockLayers) return EMBLA_ERR_INVALID;
+    if (n_kv <= 0 || n_kv > kMaxKV || ring <= 0 || ring % 128 || p0 < 0 || p0 % 128) return EMBLA_ERR_INVALID;
+    BlockCopyArgs a{};
+    a.cache = (char*)cache;
+    a.stored = (char*)stored;
+    for (int l = 0; l < 2 * n_layers; l++) {
+        if (regions[l] % 16) return EMBLA_ERR_INVALID;
+        a.off[l] = regions[l];
+    }
+    a.n_layers = n_layers; a.n_kv = n_kv; a.max_s = ring; a.p0 = p0 % ring;   // the block's slots
+    a.elem = 2;
+    a.row_units = 128 * 128 * 2 / 16;
+    a.scale_bytes = 0;
+    a.scale_units = 0;
+    a.save = save ? 1 : 0;
+    return launch_block_copy(a, stream);
+}
+
 }  // extern "C"

@@ -167,4 +167,19 @@ struct RingAppendArgs {
 };
 int launch_ring_append(const RingAppendArgs& a, hipStream_t st);
 
+/// A prefix-cache block copy (blocks.hip): 128 positions of every listed layer's K and V region.
+constexpr int kMaxBlockLayers = 64;
+struct BlockCopyArgs {
+    char* cache;
+    char* stored;
+    unsigned long long off[2 * kMaxBlockLayers];   // byte offsets of each layer's K, V region
+    int n_layers, n_kv, max_s, p0;                 // the ring: max_s = ring length, p0 = slot
+    int elem;          // bytes an element: 1 (int8 cache) or 2 (16-bit ring)
+    int row_units;     // 16-byte units of a head's 128 rows: 128 * 128 * elem / 16
+    int scale_bytes;   // bytes a scale (0: none)
+    int scale_units;   // 16-byte units of a head's 128 scales
+    int save;          // cache -> stored, else stored -> cache
+};
+int launch_block_copy(const BlockCopyArgs& a, hipStream_t st);
+
 }  // namespace embla

@@ -63,6 +63,10 @@ SIGNATURES = {
     "embla_sparse_prefill_workspace_bytes": (sz, [i32, i32]),
     "embla_prefill_sparse": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp, sz, vp]),
     "embla_ring_append": (i32, [vp, vp, i32, i32, i32, i32, i32, vp, vp, i32, vp, vp]),
+    "embla_kv_block_bytes": (sz, [i32, i32, i32]),
+    "embla_kv_block_copy": (i32, [vp, vp, i32, i32, i32, i32, i32, vp, i32, vp]),
+    "embla_ring_block_bytes": (sz, [i32, i32]),
+    "embla_ring_block_copy": (i32, [vp, vp, i32, i32, i32, i32, vp, i32, vp]),
     "embla_prefill_ring": (i32, [vp, i32, C.c_long, C.c_long, vp, vp, i32, vp, C.c_long, C.c_long, i32, i32, i32, i32,
                                  i32, vp, vp, sz, vp]),
     "embla_prefill_sliding": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, sz, vp]),

@@ -245,3 +245,22 @@ def prefill_sparse(q, k, v, qi, w, ki, kc, vc, T, p0, max_s, n_kv, ws, out=None,
     call("embla_prefill_sparse", _p(q), _p(k), _p(v), _p(qi), _p(w), _p(ki), _p(kc), _p(vc), _p(out), _p(idx), T, p0,
          max_s, n_q, n_kv, ws.ptr, ws.nbytes, stream_handle(stream))
     return out, idx
+
+
+def kv_block_copy(cache, regions, p0, max_s, n_kv, stored, save, scale_dtype=F16, stream=None):
+    """Prefix-cache block of full layers: positions p0 .. p0+127 of each layer's K and V region
+    (byte offsets `regions` [[k, v], ...] in `cache`) to `stored` (save) or back."""
+    import ctypes as C
+    flat = [int(x) for kv in regions for x in kv]
+    arr = (C.c_ulonglong * len(flat))(*flat)
+    call("embla_kv_block_copy", _p(cache), C.cast(arr, C.c_void_p), len(regions), p0, max_s, n_kv, scale_dtype,
+         _p(stored), 1 if save else 0, stream_handle(stream))
+
+
+def ring_block_copy(cache, regions, p0, ring, n_kv, stored, save, stream=None):
+    """Sliding-layer checkpoint: ring slots p0 % ring .. +127 of each layer's K and V ring."""
+    import ctypes as C
+    flat = [int(x) for kv in regions for x in kv]
+    arr = (C.c_ulonglong * len(flat))(*flat)
+    call("embla_ring_block_copy", _p(cache), C.cast(arr, C.c_void_p), len(regions), p0, ring, n_kv, _p(stored),
+         1 if save else 0, stream_handle(stream))

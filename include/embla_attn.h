@@ -251,6 +251,29 @@ int embla_kv_append(const void* qkv, void* cache, const EmblaKVJob* jobs, int nj
 int embla_q_prep(const void* qraw, const void* g1, const void* g2, int ng, int stride, int T,
                  int n_q, void* out, int out_dtype, hipStream_t stream);
 
+/* ---------------------------------------------------------------- prefix-cache blocks
+ * Save/restore of 128-position blocks between the layer caches and a stored block buffer, one
+ * launch for every layer (Engine.fullSpans / windowSpans / copy, PrefixCache.swift:147-200). The
+ * stored bytes are, per layer, K then V; per kv head its 128 rows (in the cache's tile order),
+ * then each head's 128 scales: the reference's span order. regions: [n_layers][2] byte offsets of
+ * each layer's K and V region in `cache` (16-byte aligned). save != 0 copies cache -> stored,
+ * else stored -> cache. */
+
+/* Bytes of a stored block of n_layers full layers (int8 rows, scales of scale_dtype). */
+size_t embla_kv_block_bytes(int n_layers, int n_kv, int scale_dtype);
+
+/* Positions p0 .. p0+127 (p0 % 128 == 0) of full layers' int8 caches [n_kv][max_s] (fullSpans). */
+int embla_kv_block_copy(void* cache, const unsigned long long* regions, int n_layers, int p0, int max_s, int n_kv,
+                        int scale_dtype, void* stored, int save, hipStream_t stream);
+
+/* Bytes of a stored sliding-layer checkpoint of n_layers rings (16-bit elements). */
+size_t embla_ring_block_bytes(int n_layers, int n_kv);
+
+/* Ring slots (p0 % ring) .. +127 (p0 and ring multiples of 128) of sliding layers' 16-bit rings
+ * [n_kv][ring][128] (windowSpans' K/V spans; the engram rows are outside this library). */
+int embla_ring_block_copy(void* cache, const unsigned long long* regions, int n_layers, int p0, int ring, int n_kv,
+                          void* stored, int save, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

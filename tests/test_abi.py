@@ -55,3 +55,20 @@ def test_kv_append_rejects_out_of_range():
     d = C.c_void_p(16)
     assert L.embla_kv_quant_append(d, d, 1, 512, 10, 1020, 4, d, d, 1024, 0, 0, None) == _lib.EMBLA_ERR_INVALID
     assert L.embla_kv_quant_append(d, d, 1, 100, 1, 0, 4, d, d, 1024, 0, 0, None) == _lib.EMBLA_ERR_INVALID
+
+
+def test_block_copy_rejects_bad_arguments():
+    """Block save/restore: p0 not a multiple of 128, a block past max_s, unaligned regions, too
+    many layers, a ring not a multiple of 128 (no GPU: validation precedes any HIP call)."""
+    L = _lib.lib()
+    d = C.c_void_p(256)
+    regs = (C.c_ulonglong * 4)(0, 4096, 8192, 12288)
+    bad = (C.c_ulonglong * 4)(0, 4100, 8192, 12288)
+    ok = L.embla_kv_block_bytes(2, 4, 0)
+    assert ok == 2 * 2 * 4 * 128 * 130
+    assert L.embla_kv_block_copy(d, regs, 2, 100, 1024, 4, 0, d, 1, None) < 0
+    assert L.embla_kv_block_copy(d, regs, 2, 1024, 1024, 4, 0, d, 1, None) < 0
+    assert L.embla_kv_block_copy(d, bad, 2, 128, 1024, 4, 0, d, 1, None) < 0
+    assert L.embla_kv_block_copy(d, regs, 65, 128, 1024, 4, 0, d, 1, None) < 0
+    assert L.embla_ring_block_copy(d, regs, 2, 128, 1000, 4, d, 0, None) < 0
+    assert L.embla_ring_block_bytes(2, 4) == 2 * 2 * 4 * 128 * 256
