@@ -170,6 +170,47 @@ def bench_blocks(torch, reps=20):
     return dict(block_bytes=nbytes, us_save_restore=us, gbs=moved / (us * 1e-6) / 1e9)
 
 
+def bench_gemv(torch, reps=20):
+    """The decode projections either side of attention (§8 next row 1): per layer q/k/v (3072 rows)
+    and the o-projection (2048 rows, accumulating into an fp32 residual) of one token, K = 2048,
+    4-bit weights in MLX's layout; 48 distinct layers (283 MB of weights, beyond the 256 MB MALL)
+    in one graph. Algorithmic bytes: the weights' words, scales and biases."""
+    from embla_attn import ops
+    n_layers, K = 48, 2048
+    rows_qkv, rows_o = 3072, 2048
+
+    def mat_bytes(O):
+        return O * K // 2, O * K // 64 * 2
+
+    lw = sum(mat_bytes(O)[0] + 2 * mat_bytes(O)[1] for O in (rows_qkv, rows_o))
+    W = torch.randint(0, 256, (n_layers * lw,), dtype=torch.uint8, device="cuda")
+    # scales and biases small and finite: overwrite them with bf16 0.01 and -0.075
+    segs = []
+    at = 0
+    for l in range(n_layers):
+        lay = []
+        for O in (rows_qkv, rows_o):
+            wb, sb = mat_bytes(O)
+            w0, s0, b0 = at, at + wb, at + wb + sb
+            W[s0:s0 + sb].view(torch.bfloat16).fill_(0.01)
+            W[b0:b0 + sb].view(torch.bfloat16).fill_(-0.075)
+            lay.append((w0, s0, b0, O, 0, 0))
+            at += wb + 2 * sb
+        segs.append(lay)
+    x = torch.randn(K, device="cuda").bfloat16()
+    qkv = torch.empty(rows_qkv, dtype=torch.bfloat16, device="cuda")
+    resid = torch.zeros(rows_o, dtype=torch.float32, device="cuda")
+
+    def run():
+        for l in range(n_layers):
+            ops.gemv_q4(W, x, qkv, [segs[l][0]], K, ops.EPI_BF16)
+            ops.gemv_q4(W, x, resid, [segs[l][1]], K, ops.EPI_ADD)
+    wall, ms = time_graph(torch, run, reps, 3)
+    us = ms * 1000 / n_layers
+    return dict(layers=n_layers, weight_bytes_layer=lw, us_per_layer=us, gbs=lw / (us * 1e-6) / 1e9,
+                frac_hbm=lw / (us * 1e-6) / 1e9 / HBM_PEAK_GBS)
+
+
 def prefill_flops(p0: int, T: int, n_q: int = 16, window: int = 0) -> float:
     """Algorithmic FLOPs of causal prefill attention: 4·128 a (query row, key) pair (QK and PV)."""
     pairs = 0
@@ -328,6 +369,7 @@ def main():
     c4 = bench_c4(torch)
     c5 = bench_c5(torch)
     blocks = bench_blocks(torch)
+    gemv = bench_gemv(torch)
     head = res[L]
     line = {
         "metric": METRIC,
@@ -364,6 +406,7 @@ def main():
                             if k not in ("sliding", "sparse")},
         "c5_prefill_sparse": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c5["sparse"].items()},
         "kv_block_save_restore": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in blocks.items()},
+        "qkv_o_projections_decode": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in gemv.items()},
         "c5_prefill_sliding": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c5["sliding"].items()},
     }
     if not args.no_cpu:

@@ -519,4 +519,21 @@ int embla_ring_block_copy(void* cache, const unsigned long long* regions, int n_
     return launch_block_copy(a, stream);
 }
 
+// ---------------------------------------------------------------- 4-bit projections
+int embla_gemv_q4(const void* W, const void* X, void* Y, const EmblaSeg* segs, int nseg, int K, int epi,
+                  hipStream_t stream) {
+    if (!W || !X || !Y || !segs || nseg <= 0 || nseg > kMaxGemvSegs) return EMBLA_ERR_INVALID;
+    if ((K != 2048 && K != 4096) || epi < EMBLA_EPI_BF16 || epi > EMBLA_EPI_F32) return EMBLA_ERR_INVALID;
+    GemvArgs a{};
+    a.W = W; a.X = X; a.Y = Y; a.nseg = nseg; a.K = K;
+    unsigned int prev = 0;
+    for (int i = 0; i < nseg; i++) {
+        const EmblaSeg& g = segs[i];
+        if (g.end <= prev || g.end % 4 || g.w % 16 || g.s % 2 || g.b % 2 || g.x % 8) return EMBLA_ERR_INVALID;
+        a.seg[i] = GemvSeg{g.w, g.s, g.b, g.end, g.x, g.y, 0};
+        prev = g.end;
+    }
+    return launch_gemv_q4(a, epi, stream);
+}
+
 }  // extern "C"

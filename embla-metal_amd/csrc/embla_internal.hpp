@@ -182,4 +182,19 @@ struct BlockCopyArgs {
 };
 int launch_block_copy(const BlockCopyArgs& a, hipStream_t st);
 
+/// The 4-bit projections (gemv_q4.hip): stacked segments, as gemv.metal's Seg.
+constexpr int kMaxGemvSegs = 8;
+struct GemvSeg {
+    unsigned long long w, s, b;   // byte offsets in W of the segment's words, scales, biases
+    unsigned int end, x, y, pad;  // end row (exclusive, a multiple of 4); input, output element offsets
+};
+struct GemvArgs {
+    const void* W;
+    const void* X;   // bf16
+    void* Y;
+    GemvSeg seg[kMaxGemvSegs];
+    int nseg, K;
+};
+int launch_gemv_q4(const GemvArgs& a, int epi, hipStream_t st);
+
 }  // namespace embla

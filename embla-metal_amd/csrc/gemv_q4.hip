@@ -1,0 +1,126 @@
+// The 4-bit projections either side of attention at decode: y = W x for one token over stacked
+// segments (q, k and v in one launch; or the o-projection accumulating into the residual).
+//
+// Follows gemv.metal:1-92 (MIX = 0) and GemvRows (common.metal:104-152): W in MLX's affine 4-bit
+// layout (words [O][K/8], nibble q of word c the weight of column 8c + q; bf16 scales and biases
+// [O][K/64], w = s * nibble + b), segments as the reference's Seg records (rows stacked, each with
+// its own input and output offset), epilogues EPI 0-4 (gemv.metal:77-88).
+//
+// MI355X design. A wave takes 4 rows; lane l holds 4 words (16 bytes, columns 32 l .. 32 l + 31)
+// of each 2048-column span, so a row is one coalesced 1 KB load a span, and all 4 rows' words,
+// scales and biases are requested before x is read. Two columns go through one v_dot2_f32_bf16:
+// the nibbles of columns 8j + k and 8j + k + 4 of word j sit 16 bits apart, so
+// (word >> 4k) & 0x000F000F | 0x43004300 is the bf16 pair (128 + q, 128 + q') exactly (bf16 holds
+// integers to 256), and x is paired the same way once a wave (v_perm_b32). The 128 folds into the
+// group's bias term: sum (s q + b) x = s sum (128 + q) x + (b - 128 s) sum x. The sums are fp32.
+#include "common.hpp"
+#include "embla_internal.hpp"
+
+namespace embla {
+
+typedef __bf16 bf2v_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2v_t, a), __builtin_bit_cast(bf2v_t, b), c, false);
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256) void gemv_q4_kernel(GemvArgs a) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int row0 = (blockIdx.x * 4 + w) * 4;   // the wave's first stacked row
+    int si = 0, start = 0;
+    while (si < a.nseg && row0 >= (int)a.seg[si].end) { start = (int)a.seg[si].end; si++; }
+    if (si >= a.nseg) return;
+    const GemvSeg sg = a.seg[si];
+    const int r0 = row0 - start;   // the segment's row; a segment's rows come in whole waves
+    const int spans = a.K / 2048, wpr = a.K / 8, gpr = a.K / 64;   // words, groups a row
+    const char* W = (const char*)a.W;
+
+    constexpr int MAXS = 2;   // spans a lane keeps in registers (K <= 4096)
+    u4_t wd[4][MAXS];
+    float sc[4][MAXS], bi[4][MAXS];
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+#pragma unroll
+        for (int sp = 0; sp < MAXS; sp++)
+            if (sp < spans) {
+                const size_t r = (size_t)(r0 + u);
+                wd[u][sp] = ld16(W + sg.w + (r * wpr + 256 * sp + 4 * lane) * 4);
+                sc[u][sp] = bf2f(*(const uint16_t*)(W + sg.s + (r * gpr + 32 * sp + lane / 2) * 2));
+                bi[u][sp] = bf2f(*(const uint16_t*)(W + sg.b + (r * gpr + 32 * sp + lane / 2) * 2));
+            }
+    // x: the lane's 32 columns of each span as bf16 pairs (8j + k, 8j + k + 4), and their sum
+    uint32_t xp[MAXS][16];
+    float xs[MAXS];
+    const uint16_t* X = (const uint16_t*)a.X + sg.x;
+#pragma unroll
+    for (int sp = 0; sp < MAXS; sp++) {
+        if (sp < spans) {
+            u4_t v[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) v[j] = ld16(X + 2048 * sp + 32 * lane + 8 * j);
+            float s = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) s += bf2f((uint16_t)(v[j][i] & 0xFFFF)) + bf2f((uint16_t)(v[j][i] >> 16));
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    // columns 8j + k (dword k / 2 of v[j]) and 8j + k + 4 (dword k / 2 + 2), half k % 2
+                    const uint32_t lo = v[j][k >> 1], hi = v[j][(k >> 1) + 2];
+                    xp[sp][4 * j + k] = __builtin_amdgcn_perm(hi, lo, (k & 1) ? 0x07060302u : 0x05040100u);
+                }
+            }
+            xs[sp] = s;
+        }
+    }
+    float acc[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        float r = 0.0f;
+#pragma unroll
+        for (int sp = 0; sp < MAXS; sp++) {
+            if (sp < spans) {
+                float d = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+#pragma unroll
+                    for (int k = 0; k < 4; k++)
+                        d = dot2_bf16(((wd[u][sp][j] >> (4 * k)) & 0x000F000Fu) | 0x43004300u, xp[sp][4 * j + k], d);
+                r += sc[u][sp] * d + (bi[u][sp] - 128.0f * sc[u][sp]) * xs[sp];
+            }
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) r += shfl_xor(r, o);
+        acc[u] = r;
+    }
+    if (lane < 4) {   // lane u writes row u
+        float v = acc[0];
+#pragma unroll
+        for (int u = 1; u < 4; u++) v = lane == u ? acc[u] : v;
+        const size_t at = sg.y + (size_t)(r0 + lane);
+        if constexpr (EPI == 0) ((uint16_t*)a.Y)[at] = f2bf(v);
+        else if constexpr (EPI == 1) {
+            const float t = fmaxf(bf2f(f2bf(v)), 0.0f);
+            ((uint16_t*)a.Y)[at] = f2bf(t * t);
+        } else if constexpr (EPI == 2) ((float*)a.Y)[at] += bf2f(f2bf(v));
+        else if constexpr (EPI == 3) ((float*)a.Y)[at] = bf2f(f2bf(v));
+        else ((float*)a.Y)[at] = v;
+    }
+}
+
+int launch_gemv_q4(const GemvArgs& a, int epi, hipStream_t st) {
+    const int rows = (int)a.seg[a.nseg - 1].end;
+    const dim3 grid((rows + 15) / 16), block(256);
+    switch (epi) {
+        case 0: hipLaunchKernelGGL(gemv_q4_kernel<0>, grid, block, 0, st, a); break;
+        case 1: hipLaunchKernelGGL(gemv_q4_kernel<1>, grid, block, 0, st, a); break;
+        case 2: hipLaunchKernelGGL(gemv_q4_kernel<2>, grid, block, 0, st, a); break;
+        case 3: hipLaunchKernelGGL(gemv_q4_kernel<3>, grid, block, 0, st, a); break;
+        case 4: hipLaunchKernelGGL(gemv_q4_kernel<4>, grid, block, 0, st, a); break;
+        default: return EMBLA_ERR_INVALID;
+    }
+    return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
+}
+
+}  // namespace embla

@@ -264,3 +264,20 @@ def ring_block_copy(cache, regions, p0, ring, n_kv, stored, save, stream=None):
     arr = (C.c_ulonglong * len(flat))(*flat)
     call("embla_ring_block_copy", _p(cache), C.cast(arr, C.c_void_p), len(regions), p0, ring, n_kv, _p(stored),
          1 if save else 0, stream_handle(stream))
+
+
+class EmblaSeg(C.Structure):
+    """A stacked segment of embla_gemv_q4 (gemv.metal's Seg)."""
+    _fields_ = [("w", C.c_ulonglong), ("s", C.c_ulonglong), ("b", C.c_ulonglong), ("end", C.c_uint),
+                ("x", C.c_uint), ("y", C.c_uint), ("pad", C.c_uint)]
+
+
+EPI_BF16, EPI_RELU2, EPI_ADD, EPI_F32_BF, EPI_F32 = range(5)
+
+
+def gemv_q4(W, X, Y, segs, K, epi, stream=None):
+    """y = W x over stacked 4-bit segments: W a uint8 buffer, X bf16, Y bf16 (epi 0, 1) or fp32;
+    segs: (w, s, b, end, x, y) tuples of byte offsets in W, end row, element offsets in X and Y."""
+    arr = (EmblaSeg * len(segs))(*[EmblaSeg(*g, 0) for g in segs])
+    call("embla_gemv_q4", _p(W), _p(X), _p(Y), C.cast(arr, C.c_void_p), len(segs), K, epi, stream_handle(stream))
+    return Y

@@ -113,3 +113,13 @@ def sparse_prefill_case(seed: int, p0: int, T: int, n_q: int = 16, n_kv: int = 4
     c["w"] = g.uniform(T * n_ih).astype(np.float32).reshape(T, n_ih)
     c["ki"] = f16_bits(g.normal((p0 + T) * 64)).reshape(p0 + T, 64)
     return c
+
+
+def q4_weights(g: "SplitMix64", O: int, K: int) -> tuple:
+    """A 4-bit matrix in MLX's affine layout: words uint32 [O][K/8] of uniform nibbles, bf16
+    scales U[0.005, 0.015] and biases -7.5 scale (weights centred on 0) [O][K/64], as bits."""
+    words = (g.uniform(O * K // 8) * 2 ** 32).astype(np.uint64).astype(np.uint32).reshape(O, K // 8)
+    sc = 0.005 + 0.01 * g.uniform(O * K // 64)
+    s = bf16_bits(sc.astype(np.float32)).reshape(O, K // 64)
+    b = bf16_bits((-7.5 * bf16_val(s).reshape(-1)).astype(np.float32)).reshape(O, K // 64)
+    return words, s, b

@@ -274,6 +274,28 @@ size_t embla_ring_block_bytes(int n_layers, int n_kv);
 int embla_ring_block_copy(void* cache, const unsigned long long* regions, int n_layers, int p0, int ring, int n_kv,
                           void* stored, int save, hipStream_t stream);
 
+/* ---------------------------------------------------------------- 4-bit projections
+ * The q/k/v producer and o-projection consumer of the attention sub-layer (gemv.metal:1-92,
+ * gemm.metal:1-134): W in MLX's affine 4-bit layout, words [O][K/8] (nibble q of word c is the
+ * weight of column 8c + q), bf16 scales and biases [O][K/64] (w = s * nibble + b); x bf16. */
+
+/* Epilogues (gemv.metal:77-88): y = bf16(acc); y = bf16(relu(bf16(acc))^2); y (fp32) += bf16(acc);
+ * y (fp32) = bf16(acc); y (fp32) = acc. */
+enum { EMBLA_EPI_BF16 = 0, EMBLA_EPI_RELU2 = 1, EMBLA_EPI_ADD = 2, EMBLA_EPI_F32_BF = 3, EMBLA_EPI_F32 = 4 };
+
+/* A segment of stacked rows (gemv.metal's Seg, 29-35): byte offsets in W of its words, scales and
+ * biases; its end row in the stack (exclusive, a multiple of 4); the element offsets of its input
+ * in X (a multiple of 8) and of its first output in Y. */
+typedef struct {
+    unsigned long long w, s, b;
+    unsigned int end, x, y, pad;
+} EmblaSeg;
+
+/* y = W x for one token over nseg (<= 8) stacked segments, K columns (2048 or 4096), one launch
+ * (gemv.metal with MIX = 0: q, k and v of a layer, or the o-projection with EMBLA_EPI_ADD). */
+int embla_gemv_q4(const void* W, const void* X, void* Y, const EmblaSeg* segs, int nseg, int K, int epi,
+                  hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -9,6 +9,8 @@
  *     370-441 / 448-584 (attn_sparse, attn_sparse8: softmax, SEL), 655-744 (select_keys)
  *   Sources/EmblaMetal/Kernels/prefill.metal:127-180, 428-548 (sliding prefill),
  *     214-282 (attn_full_b); attn_nax.metal:61-364 (causal ReLU² prefill)
+ *   Sources/EmblaMetal/Kernels/gemv.metal:1-92, gemm.metal:1-134, common.metal:104-152 (the
+ *     4-bit projections either side of attention: y = W x with MLX's affine 4-bit layout)
  * and the BASELINE configs' variants of them (softmax full layers, fp16 scales, 4 kv heads,
  * window 1024, the ReLU² index scorer  score_j = Σ_h w_h relu(q_h·k_j)²).
  *
@@ -329,6 +331,35 @@ void orc_prefill_int8(const float* q, const int8_t* K, const float* ks, const in
             }
             const float den = weights == 1 ? sqrtf((float)HD) + l : l;
             for (int d = 0; d < HD; d++) out[((size_t)i * n_q + h) * HD + d] = acc[d] / den;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ 4-bit projections */
+/* y = W x of one token (gemv.metal:36-92 with MIX = 0; gemm.metal:1-134 row by row for T tokens),
+ * W in MLX's affine 4-bit layout (gemm.metal:1-3; common.metal:105-152): words [O][K/8], nibble q
+ * of word c (bits 4q .. 4q+3) the weight of column 8c + q; scales and biases bf16 [O][K/64]
+ * (group g = columns 64g .. 64g+63); w = s * nibble + b. The dot product accumulates in double
+ * (the GPU's fp32 sums in its own order are compared within tolerance), then the epilogue
+ * (gemv.metal:77-88): 0 y = bf16(acc), 1 y = bf16(relu(bf16(acc))^2), 2 y += bf16(acc) (y fp32),
+ * 3 y = bf16(acc) (fp32), 4 y = acc. Outputs are written as floats (bf16 values exactly). */
+void orc_q4_matvec(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint16_t* x, int O, int K,
+                   int epi, float* y) {
+    for (int r = 0; r < O; r++) {
+        double acc = 0.0;
+        for (int c = 0; c < K; c++) {
+            const uint32_t q = (w[(size_t)r * (K / 8) + c / 8] >> (4 * (c % 8))) & 0xFu;
+            const double wt = (double)orc_bf16_to_f32(s[(size_t)r * (K / 64) + c / 64]) * q +
+                              (double)orc_bf16_to_f32(b[(size_t)r * (K / 64) + c / 64]);
+            acc += wt * (double)orc_bf16_to_f32(x[c]);
+        }
+        const float a = (float)acc;
+        switch (epi) {
+            case 0: y[r] = bf(a); break;
+            case 1: { const float v = fmaxf(bf(a), 0.0f); y[r] = bf(v * v); break; }
+            case 2: y[r] += bf(a); break;
+            case 3: y[r] = bf(a); break;
+            default: y[r] = a; break;
         }
     }
 }

@@ -48,6 +48,7 @@ def lib() -> C.CDLL:
         L.orc_index_scores.argtypes = [u16, f32, u16, C.c_int, C.c_int, f32]
         L.orc_prefill_int8.argtypes = [f32, i8, f32, i8, f32, C.c_int, C.c_int, C.c_int, C.c_int,
                                        C.c_int, C.c_int, C.c_int, opt, C.c_int, f32]
+        L.orc_q4_matvec.argtypes = [u32, u16, u16, u16, C.c_int, C.c_int, C.c_int, f32]
         L.orc_f16_to_f32.argtypes = [C.c_uint16]
         L.orc_f16_to_f32.restype = C.c_float
         L.orc_f32_to_f16.argtypes = [C.c_float]
@@ -154,4 +155,15 @@ def prefill_int8(q, K, ks, V, vs, p0, weights=0, window=0, rows_sel=None):
     nsel = 0 if rs is None else rs.shape[1]
     out = np.empty((T, n_q, 128), np.float32)
     lib().orc_prefill_int8(q, K, ks, V, vs, T, p0, S_cache, n_q, n_kv, weights, window, _ptr(rs), nsel, out)
+    return out
+
+
+def q4_matvec(w, s, b, x, epi=4, y=None):
+    """y = W x for W in MLX's 4-bit affine layout: w uint32 [O][K/8], s, b bf16 bits [O][K/64],
+    x bf16 bits [K]; epilogue epi (2 accumulates into y)."""
+    w = _c(w, np.uint32)
+    O, K = w.shape[0], w.shape[1] * 8
+    out = np.zeros(O, np.float32) if y is None else np.ascontiguousarray(y, np.float32).copy()
+    lib().orc_q4_matvec(w.reshape(-1), _c(s, np.uint16).reshape(-1), _c(b, np.uint16).reshape(-1),
+                        _c(x, np.uint16).reshape(-1), O, K, epi, out)
     return out

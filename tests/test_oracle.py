@@ -303,3 +303,87 @@ def test_head_norm_vs_fp64(orc):
         np.testing.assert_array_equal(orc.head_norm(x, g1, g2, ng, round_bf=True), synth.bf16_val(synth.bf16_bits(got)))
     # a zero row stays zero (eps keeps the factor finite)
     assert not orc.head_norm(np.zeros(128), None, None, 0).any()
+
+
+# ---------------------------------------------------------------- 4-bit projections (gemv/gemm)
+def _bf(v):
+    return synth.bf16_bits(np.asarray(v, np.float32))
+
+
+def test_q4_matvec_nibble_order_known_answers(orc):
+    """gemm.metal's dequant: nibble q of word c (bits 4q..) is column 8c + q; group g of 64
+    columns has one scale and bias. Hand-built words with known nibbles, closed-form sums."""
+    O, K = 3, 2048
+    w = np.zeros((O, K // 8), np.uint32)
+    w[0, 0] = 0x76543210            # columns 0..7 hold 0..7
+    w[1, 9] = 0xF0000000            # column 8 * 9 + 7 = 79 holds 15
+    w[2, :] = 0xFFFFFFFF            # every column 15
+    s = np.full((O, K // 64), _bf(1.0)[()], np.uint16)
+    b = np.zeros((O, K // 64), np.uint16)
+    s[1, 1] = _bf(0.5)              # column 79 is in group 1
+    s[2, :] = _bf(2.0)
+    b[2, :] = _bf(-3.0)             # w = 2 * 15 - 3 = 27
+    # x = 1 on columns 0..7 and 79, 0 elsewhere
+    x = np.zeros(K, np.float32)
+    x[:8] = 1.0
+    x[79] = 1.0
+    y = orc.q4_matvec(w, s, b, _bf(x), epi=4)
+    assert y[0] == 28.0                  # 0 + 1 + ... + 7
+    assert y[1] == 7.5                   # 15 * 0.5 at column 79
+    assert y[2] == 27.0 * 9              # nine columns of 27
+    # one-hot columns read back each column's weight
+    g = synth.SplitMix64(5)
+    wr = (g.uniform(O * K // 8) * 2 ** 32).astype(np.uint64).astype(np.uint32).reshape(O, K // 8)
+    sr = _bf(g.uniform(O * K // 64) + 0.5).reshape(O, K // 64)
+    br = _bf(g.uniform(O * K // 64) - 0.5).reshape(O, K // 64)
+    for c in [0, 1, 7, 8, 63, 64, 65, 1000, 2047]:
+        e = np.zeros(K, np.float32)
+        e[c] = 1.0
+        y = orc.q4_matvec(wr, sr, br, _bf(e), epi=4)
+        q = np.array([(int(wr[r, c // 8]) >> (4 * (c % 8))) & 15 for r in range(O)], np.float64)
+        want = synth.bf16_val(sr[:, c // 64]).astype(np.float64) * q + synth.bf16_val(br[:, c // 64])
+        np.testing.assert_array_equal(y, want.astype(np.float32))
+
+
+def test_q4_matvec_epilogues(orc):
+    """gemv.metal:77-88. Column 0's weight is 1 * 1 + 2^-9 (scale 1, bias 2^-9: both exact in
+    bf16), every other weight 0, so acc = (1 + 2^-9) x0 and each epilogue's rounding shows."""
+    K = 2048
+    w = np.zeros((1, K // 8), np.uint32)
+    w[0, 0] = 1
+    s = np.full((1, K // 64), _bf(1.0)[()], np.uint16)
+    b = np.zeros((1, K // 64), np.uint16)
+    b[0, 0] = _bf(2.0 ** -9)
+    for x0, epi, y0, want in [(1.0, 0, None, 1.0),                          # bf16(1 + 2^-9) = 1
+                              (-2.0, 1, None, 0.0),                         # relu of a negative
+                              (3.0, 1, None, 9.0),                          # bf16(3.006) = 3, squared
+                              (1.0, 2, 10.0, 11.0),                         # y += bf16(acc)
+                              (1.0, 3, None, 1.0),
+                              (1.0, 4, None, 1.0 + 2.0 ** -9)]:             # unrounded
+        x = np.zeros(K, np.float32)
+        x[0] = x0
+        y = orc.q4_matvec(w, s, b, _bf(x), epi=epi, y=None if y0 is None else np.float32([y0]))
+        assert y[0] == np.float32(want), (x0, epi, y[0])
+
+
+def test_q4_matvec_mlx_quantised_round_trip(orc):
+    """An independent affine quantiser (MLX's published one: per group of 64, scale = (max -
+    min) / 15, bias = min, q = round((w - bias) / scale)) packed into words: the oracle's product
+    matches the dense product of the dequantised matrix, and the original within the bound."""
+    O, K = 8, 2048
+    g = synth.SplitMix64(11)
+    Wd = g.normal(O * K).astype(np.float32).reshape(O, K)
+    x = synth.bf16_val(_bf(g.normal(K)))
+    G = Wd.reshape(O, K // 64, 64)
+    lo, hi = G.min(-1), G.max(-1)
+    sc = synth.bf16_val(_bf((hi - lo) / 15))
+    bi = synth.bf16_val(_bf(lo))
+    q = np.clip(np.rint((G - bi[..., None]) / sc[..., None]), 0, 15).astype(np.uint32).reshape(O, K)
+    words = np.zeros((O, K // 8), np.uint32)
+    for j in range(8):
+        words |= q[:, j::8] << np.uint32(4 * j)
+    y = orc.q4_matvec(words, _bf(sc), _bf(bi), _bf(x), epi=4)
+    deq = (sc[..., None] * q.reshape(O, K // 64, 64) + bi[..., None]).reshape(O, K).astype(np.float64)
+    np.testing.assert_allclose(y, deq @ x.astype(np.float64), rtol=1e-6, atol=1e-4)
+    bound = (np.repeat(sc, 64, axis=1) * 0.51 + 0.02) @ np.abs(x)
+    assert np.all(np.abs(y - Wd.astype(np.float64) @ x) <= bound)
