@@ -27,6 +27,7 @@ sys.path.insert(0, str(ROOT / "embla-metal_amd"))
 
 METRIC = "attention µs/layer + HBM GB/s at 32k decode; prefill attn TFLOP/s @2048"
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0   # dense bf16/fp16 MFMA, MI355X
 
 
 def layer_bytes(L: int) -> int:
@@ -211,6 +212,33 @@ def bench_gemv(torch, reps=20):
                 frac_hbm=lw / (us * 1e-6) / 1e9 / HBM_PEAK_GBS)
 
 
+def bench_gemm(torch, reps=10):
+    """The prefill projections either side of attention (§8 next row 1): C5's 2048-token chunk
+    through q/k/v (3072 rows) and the o-projection (2048 rows, accumulating into an fp32
+    residual), K = 2048, 4-bit weights in MLX's layout; one graph. FLOPs 2 T O K."""
+    from embla_attn import ops
+    T, K = 2048, 2048
+    mats = []
+    for O in (3072, 2048):
+        wb, sb = O * K // 2, O * K // 64 * 2
+        W = torch.randint(0, 256, (wb + 2 * sb,), dtype=torch.uint8, device="cuda")
+        W[wb:wb + sb].view(torch.bfloat16).fill_(0.01)
+        W[wb + sb:].view(torch.bfloat16).fill_(-0.075)
+        mats.append((W, (0, wb, wb + sb), O))
+    x = torch.randn(T, K, device="cuda").bfloat16()
+    a = torch.randn(T, 2048, device="cuda").bfloat16()
+    qkv = torch.empty(T, 3072, dtype=torch.bfloat16, device="cuda")
+    resid = torch.zeros(T, 2048, dtype=torch.float32, device="cuda")
+
+    def run():
+        ops.gemm_q4(mats[0][0], mats[0][1], x, qkv, T, 3072, K, ops.EPI_BF16)
+        ops.gemm_q4(mats[1][0], mats[1][1], a, resid, T, 2048, K, ops.EPI_ADD)
+    wall, ms = time_graph(torch, run, reps, 2)
+    flops = 2.0 * T * K * (3072 + 2048)
+    return dict(gflop=flops / 1e9, ms=ms, tflops=flops / (ms * 1e-3) / 1e12,
+                mfma_util=flops / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS)
+
+
 def prefill_flops(p0: int, T: int, n_q: int = 16, window: int = 0) -> float:
     """Algorithmic FLOPs of causal prefill attention: 4·128 a (query row, key) pair (QK and PV)."""
     pairs = 0
@@ -370,6 +398,7 @@ def main():
     c5 = bench_c5(torch)
     blocks = bench_blocks(torch)
     gemv = bench_gemv(torch)
+    gemm = bench_gemm(torch)
     head = res[L]
     line = {
         "metric": METRIC,
@@ -407,6 +436,7 @@ def main():
         "c5_prefill_sparse": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c5["sparse"].items()},
         "kv_block_save_restore": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in blocks.items()},
         "qkv_o_projections_decode": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in gemv.items()},
+        "qkv_o_projections_prefill": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in gemm.items()},
         "c5_prefill_sliding": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c5["sliding"].items()},
     }
     if not args.no_cpu:

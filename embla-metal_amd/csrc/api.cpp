@@ -536,4 +536,13 @@ int embla_gemv_q4(const void* W, const void* X, void* Y, const EmblaSeg* segs, i
     return launch_gemv_q4(a, epi, stream);
 }
 
+int embla_gemm_q4(const void* W, const unsigned long long* wo, const void* X, void* Y, int T, int O, int K,
+                  int ldx, int ldy, int epi, hipStream_t stream) {
+    if (!W || !wo || !X || !Y || T <= 0 || O <= 0 || K <= 0 || K % 64) return EMBLA_ERR_INVALID;
+    if (ldx < K || ldx % 8 || ldy < O || epi < EMBLA_EPI_BF16 || epi > EMBLA_EPI_F32) return EMBLA_ERR_INVALID;
+    if (wo[0] % 16 || wo[1] % 2 || wo[2] % 2) return EMBLA_ERR_INVALID;
+    GemmArgs a{W, wo[0], wo[1], wo[2], (const uint16_t*)X, Y, T, O, K, ldx, ldy};
+    return launch_gemm_q4(a, epi, stream);
+}
+
 }  // extern "C"

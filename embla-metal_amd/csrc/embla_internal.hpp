@@ -197,4 +197,14 @@ struct GemvArgs {
 };
 int launch_gemv_q4(const GemvArgs& a, int epi, hipStream_t st);
 
+/// The prefill projections (gemm_q4.hip): Y [T][ldy] = X [T][ldx] W^T, W 4-bit at byte offsets.
+struct GemmArgs {
+    const void* W;
+    unsigned long long wo, so, bo;   // byte offsets in W of the words, scales, biases
+    const uint16_t* X;               // bf16
+    void* Y;
+    int T, O, K, ldx, ldy;
+};
+int launch_gemm_q4(const GemmArgs& a, int epi, hipStream_t st);
+
 }  // namespace embla

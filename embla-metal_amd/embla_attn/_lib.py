@@ -65,6 +65,7 @@ SIGNATURES = {
     "embla_ring_append": (i32, [vp, vp, i32, i32, i32, i32, i32, vp, vp, i32, vp, vp]),
     "embla_kv_block_bytes": (sz, [i32, i32, i32]),
     "embla_gemv_q4": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
+    "embla_gemm_q4": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp]),
     "embla_kv_block_copy": (i32, [vp, vp, i32, i32, i32, i32, i32, vp, i32, vp]),
     "embla_ring_block_bytes": (sz, [i32, i32]),
     "embla_ring_block_copy": (i32, [vp, vp, i32, i32, i32, i32, vp, i32, vp]),

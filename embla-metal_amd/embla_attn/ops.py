@@ -281,3 +281,12 @@ def gemv_q4(W, X, Y, segs, K, epi, stream=None):
     arr = (EmblaSeg * len(segs))(*[EmblaSeg(*g, 0) for g in segs])
     call("embla_gemv_q4", _p(W), _p(X), _p(Y), C.cast(arr, C.c_void_p), len(segs), K, epi, stream_handle(stream))
     return Y
+
+
+def gemm_q4(W, wo, X, Y, T, O, K, epi, ldx=None, ldy=None, stream=None):
+    """Y = X W^T for T tokens: W a uint8 buffer with the words, scales and biases at byte offsets
+    wo = (w, s, b); X bf16 [T][ldx]; Y [T][ldy] bf16 (epi 0, 1) or fp32."""
+    arr = (C.c_ulonglong * 3)(*[int(v) for v in wo])
+    call("embla_gemm_q4", _p(W), C.cast(arr, C.c_void_p), _p(X), _p(Y), T, O, K, ldx or K, ldy or O, epi,
+         stream_handle(stream))
+    return Y

@@ -296,6 +296,12 @@ typedef struct {
 int embla_gemv_q4(const void* W, const void* X, void* Y, const EmblaSeg* segs, int nseg, int K, int epi,
                   hipStream_t stream);
 
+/* Y = X W^T for T tokens (gemm.metal with EXPERTS = GATHER = 0): X [T][ldx] bf16 (ldx a multiple of
+ * 8), W's words, scales and biases at byte offsets wo[0], wo[1], wo[2] (16, 2, 2-byte aligned),
+ * O rows, K inputs (a multiple of 64), Y [T][ldy] in the epilogue's type. */
+int embla_gemm_q4(const void* W, const unsigned long long* wo, const void* X, void* Y, int T, int O, int K,
+                  int ldx, int ldy, int epi, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
