@@ -239,6 +239,53 @@ def bench_gemm(torch, reps=10):
                 mfma_util=flops / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS)
 
 
+def bench_step(torch, regions, L=32768, reps=20):
+    """The whole attention sub-layer decode step of one token (§8 next row 3) over C3's 16-layer
+    stack at context L, captured as one graph: per layer the 4-bit q/k/v projection, the int8 append
+    of the new k and v at position L - 1, the q preparation, the split-K decode over L positions
+    (bf16 out) and the 4-bit o-projection into the fp32 residual. Algorithmic bytes a layer: the
+    cache as in C3 plus the weights."""
+    from embla_attn import ops
+    n_layers, D, n_q, n_kv, max_s = len(regions), 2048, 16, 4, 32768
+
+    def mat_bytes(O):
+        return O * D // 2, O * D // 64 * 2
+
+    lw = sum(mat_bytes(O)[0] + 2 * mat_bytes(O)[1] for O in (3072, D))
+    W = torch.randint(0, 256, (n_layers * lw,), dtype=torch.uint8, device="cuda")
+    segs, at = [], 0
+    for l in range(n_layers):
+        lay = []
+        for O in (3072, D):
+            wb, sb = mat_bytes(O)
+            W[at + wb:at + wb + sb].view(torch.bfloat16).fill_(0.002)
+            W[at + wb + sb:at + wb + 2 * sb].view(torch.bfloat16).fill_(-0.015)
+            lay.append((at, at + wb, at + wb + sb, O, 0, 0))
+            at += wb + 2 * sb
+        segs.append(lay)
+    x = torch.randn(D, device="cuda").bfloat16()
+    qkv = torch.empty(3072, dtype=torch.bfloat16, device="cuda")
+    qf = torch.empty(1, n_q, 128, dtype=torch.float16, device="cuda")
+    o = torch.empty(n_q, 128, dtype=torch.bfloat16, device="cuda")
+    resid = torch.empty(D, dtype=torch.float32, device="cuda")
+    ws = ops.Workspace(max_s, n_q)
+
+    def run():
+        resid.zero_()
+        for l in range(n_layers):
+            kc, vc = regions[l]
+            ops.gemv_q4(W, x, qkv, [segs[l][0]], D, ops.EPI_BF16)
+            ops.kv_quant_append(qkv[2048:2560], qkv[2560:3072], 1, L - 1, n_kv, kc, vc, max_s)
+            ops.q_prep(qkv[:2048], None, None, 0, 1, n_q, out=qf)
+            ops.decode_int8(qf[0], kc, vc, L, max_s, n_kv, out_dtype=ops.BF16, ws=ws, out=o)
+            ops.gemv_q4(W, o, resid, [segs[l][1]], D, ops.EPI_ADD)
+    wall, ms = time_graph(torch, run, reps, 3)
+    us = ms * 1000 / n_layers
+    nbytes = layer_bytes(L) + lw
+    return dict(context=L, layers=n_layers, kernels_per_layer=6, bytes_layer=nbytes, us_per_layer=us,
+                gbs=nbytes / (us * 1e-6) / 1e9, frac_hbm=nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS)
+
+
 def prefill_flops(p0: int, T: int, n_q: int = 16, window: int = 0) -> float:
     """Algorithmic FLOPs of causal prefill attention: 4·128 a (query row, key) pair (QK and PV)."""
     pairs = 0
@@ -392,7 +439,8 @@ def main():
         print(json.dumps({"metric": METRIC, "value": round(h["gbs"], 1), "unit": "GB/s",
                           "us_per_layer": round(h["us_per_layer"], 3), "steps": args.steps}))
         return
-    res, case, out0, _ = bench_c3(torch, args.steps, args.warmup)
+    res, case, out0, regions = bench_c3(torch, args.steps, args.warmup)
+    step = bench_step(torch, regions)
     c2 = bench_c2(torch)
     c4 = bench_c4(torch)
     c5 = bench_c5(torch)
@@ -436,6 +484,7 @@ def main():
         "c5_prefill_sparse": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c5["sparse"].items()},
         "kv_block_save_restore": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in blocks.items()},
         "qkv_o_projections_decode": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in gemv.items()},
+        "decode_sublayer_step_graph": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in step.items()},
         "qkv_o_projections_prefill": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in gemm.items()},
         "c5_prefill_sliding": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c5["sliding"].items()},
     }

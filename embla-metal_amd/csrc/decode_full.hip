@@ -380,6 +380,7 @@ int launch_full_decode(const FullDecodeArgs& a, hipStream_t st) {
     const int gq = a.n_q / a.n_kv;
     if (gq == 4 && !a.relu2 && !a.scale32 && !a.out_bf16 && !a.scores) EMBLA_FD(4, false, false, false, false);
     else if (gq == 4 && !a.relu2 && a.scale32 && a.out_bf16 && !a.scores) EMBLA_FD(4, false, true, true, false);
+    else if (gq == 4 && !a.relu2 && !a.scale32 && a.out_bf16 && !a.scores) EMBLA_FD(4, false, false, true, false);
     else if (gq == 8 && a.relu2 && a.scale32 && a.out_bf16 && !a.scores) EMBLA_FD(8, true, true, true, false);
     else if (gq == 8 && a.relu2 && a.scale32 && a.out_bf16 && a.scores) EMBLA_FD(8, true, true, true, true);
     else if (gq == 8 && !a.relu2 && a.scale32 && a.out_bf16 && !a.scores) EMBLA_FD(8, false, true, true, false);

@@ -57,9 +57,10 @@ def kv_quant_append(k, v, T, p0, n_kv, kc, vc, max_s, in_dtype=BF16, scale_dtype
          scale_dtype, int(norm_k), stream_handle(stream))
 
 
-def q_prep(qraw, g1, g2, ng, T, n_q, out_dtype=F16, stride=None, stream=None):
+def q_prep(qraw, g1, g2, ng, T, n_q, out_dtype=F16, stride=None, out=None, stream=None):
     stride = stride if stride is not None else n_q * 128
-    out = torch.empty((T, n_q, 128), dtype=_DT[out_dtype], device=qraw.device)
+    if out is None:
+        out = torch.empty((T, n_q, 128), dtype=_DT[out_dtype], device=qraw.device)
     call("embla_q_prep", _p(qraw), _p(g1), _p(g2), ng, stride, T, n_q, _p(out), out_dtype,
          stream_handle(stream))
     return out

@@ -51,6 +51,19 @@ def test_decode_independent_of_split(torch_gpu, orc, chunk):
     assert_close(got, ref, what=f"chunk={chunk}")
 
 
+@pytest.mark.parametrize("S", [40, 5000])
+def test_decode_f16_scales_bf16_out(torch_gpu, orc, S):
+    """The sub-layer step's decode: fp16 scales, bf16 output for the o-projection's input."""
+    from embla_attn import ops
+    say(f"decode f16 scales bf16 out S={S}")
+    c = synth.decode_int8_case(seed=11, S=S)
+    kc, vc = upload_int8_case(c, 8192)
+    o = ops.decode_int8(dev(c["q"], torch_gpu.float16), kc, vc, S, 8192, c["n_kv"], out_dtype=ops.BF16,
+                        ws=ops.Workspace(8192, c["n_q"]))
+    torch_gpu.cuda.synchronize()
+    assert_close(bf16_host(o), oracle_cfg(orc, c), what=f"S={S}")
+
+
 def test_decode_repeated_calls_leave_counters_zero(torch_gpu, orc):
     from embla_attn import ops
     say("decode repeated calls, one workspace")
