@@ -286,6 +286,34 @@ def bench_step(torch, regions, L=32768, reps=20):
                 gbs=nbytes / (us * 1e-6) / 1e9, frac_hbm=nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS)
 
 
+def bench_sampling(torch, reps=10):
+    """The sampling tail (§8 next row 4) on a 65536-token row: the greedy token, a top-p draw over
+    few candidates (a peaked row: 316 tokens within 1/16384 of the top) and a draw that bisects
+    over every token (a flat row); 32 positions a graph. Latency-bound: µs a call."""
+    from embla_attn import ops
+    V, n = 65536, 32
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    flat = torch.randn(V, device="cuda", generator=g)
+    peaked = torch.randn(V, device="cuda", generator=g) - 6
+    hot = torch.randperm(V, device="cuda", generator=g)[:300]
+    peaked[hot] = torch.rand(300, device="cuda", generator=g) * 6 + 2
+    st = ops.SampleState(V, n + 2)
+    res = {}
+    for name, fn in [
+        ("greedy_us", lambda p: ops.argmax(flat, st, p)),
+        ("draw_candidates_us", lambda p: ops.sample(peaked, st, p, 1.0, 0.9, 7)),
+        ("draw_all_tokens_us", lambda p: ops.sample(flat, st, p, 1.0, 0.9, 7)),
+    ]:
+        def run(fn=fn):
+            for p in range(n):
+                fn(p)
+        _, ms = time_graph(torch, run, reps, 2)
+        res[name] = ms * 1000 / n
+    res["vocab"] = V
+    return res
+
+
 def prefill_flops(p0: int, T: int, n_q: int = 16, window: int = 0) -> float:
     """Algorithmic FLOPs of causal prefill attention: 4·128 a (query row, key) pair (QK and PV)."""
     pairs = 0
@@ -441,6 +469,7 @@ def main():
         return
     res, case, out0, regions = bench_c3(torch, args.steps, args.warmup)
     step = bench_step(torch, regions)
+    sampling = bench_sampling(torch)
     c2 = bench_c2(torch)
     c4 = bench_c4(torch)
     c5 = bench_c5(torch)
@@ -485,6 +514,7 @@ def main():
         "kv_block_save_restore": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in blocks.items()},
         "qkv_o_projections_decode": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in gemv.items()},
         "decode_sublayer_step_graph": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in step.items()},
+        "sampling_tail": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in sampling.items()},
         "qkv_o_projections_prefill": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in gemm.items()},
         "c5_prefill_sliding": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c5["sliding"].items()},
     }

@@ -545,4 +545,21 @@ int embla_gemm_q4(const void* W, const unsigned long long* wo, const void* X, vo
     return launch_gemm_q4(a, epi, stream);
 }
 
+size_t embla_sample_workspace_bytes(int V) { return V > 0 && V <= 65536 ? sample_ws_bytes(V) : 0; }
+
+int embla_argmax(const float* logits, uint32_t* token, int V, uint32_t* greedy, int pos, int prompt_len, void* ws,
+                 size_t ws_bytes, hipStream_t stream) {
+    if (!logits || !token || !greedy || V <= 0 || V > 65536 || pos < 0 || (uintptr_t)logits % 16) return EMBLA_ERR_INVALID;
+    if (!ws || ws_bytes < sample_ws_bytes(V)) return EMBLA_ERR_WORKSPACE;
+    return launch_argmax(logits, V, token, greedy, pos, prompt_len, (char*)ws, stream);
+}
+
+int embla_sample(const float* logits, uint32_t* token, int V, uint32_t* greedy, int pos, int prompt_len, float inv_t,
+                 float top_p, uint32_t seed, void* ws, size_t ws_bytes, hipStream_t stream) {
+    if (!logits || !token || !greedy || V <= 0 || V > 65536 || pos < 0 || (uintptr_t)logits % 16) return EMBLA_ERR_INVALID;
+    if (!(inv_t > 0.0f) || !(inv_t < __builtin_huge_valf()) || !(top_p > 0.0f) || !(top_p <= 1.0f)) return EMBLA_ERR_INVALID;
+    if (!ws || ws_bytes < sample_ws_bytes(V)) return EMBLA_ERR_WORKSPACE;
+    return launch_sample(logits, V, token, greedy, pos, prompt_len, inv_t, top_p, seed, (char*)ws, stream);
+}
+
 }  // extern "C"

@@ -207,4 +207,14 @@ struct GemmArgs {
 };
 int launch_gemm_q4(const GemmArgs& a, int epi, hipStream_t st);
 
+/// The sampling tail (sample.hip). Workspace: the capped row as bf16, then the block maxima and
+/// their indices (64 each) and 64 block records of 32 bytes, then a 1024-word candidate list a block.
+inline size_t sample_ws_off_blk(int V) { return ((size_t)V * 2 + 255) / 256 * 256; }
+inline size_t sample_ws_off_cand(int V) { return sample_ws_off_blk(V) + 2560; }
+inline size_t sample_ws_bytes(int V) { return sample_ws_off_cand(V) + (size_t)((V + 1023) / 1024) * 4096; }
+int launch_argmax(const float* logits, int V, uint32_t* token, uint32_t* greedy, int pos, int prompt, char* ws,
+                  hipStream_t st);
+int launch_sample(const float* logits, int V, uint32_t* token, uint32_t* greedy, int pos, int prompt, float inv_t,
+                  float top_p, uint32_t seed, char* ws, hipStream_t st);
+
 }  // namespace embla

@@ -66,6 +66,9 @@ SIGNATURES = {
     "embla_kv_block_bytes": (sz, [i32, i32, i32]),
     "embla_gemv_q4": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
     "embla_gemm_q4": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp]),
+    "embla_sample_workspace_bytes": (sz, [i32]),
+    "embla_argmax": (i32, [vp, vp, i32, vp, i32, i32, vp, sz, vp]),
+    "embla_sample": (i32, [vp, vp, i32, vp, i32, i32, C.c_float, C.c_float, C.c_uint32, vp, sz, vp]),
     "embla_kv_block_copy": (i32, [vp, vp, i32, i32, i32, i32, i32, vp, i32, vp]),
     "embla_ring_block_bytes": (sz, [i32, i32]),
     "embla_ring_block_copy": (i32, [vp, vp, i32, i32, i32, i32, vp, i32, vp]),

@@ -291,3 +291,37 @@ def gemm_q4(W, wo, X, Y, T, O, K, epi, ldx=None, ldy=None, stream=None):
     call("embla_gemm_q4", _p(W), C.cast(arr, C.c_void_p), _p(X), _p(Y), T, O, K, ldx or K, ldy or O, epi,
          stream_handle(stream))
     return Y
+
+
+class SampleState:
+    """The sampling tail's buffers for vocabularies up to V tokens (Engine.swift:261-267): the token
+    ids by position, the greedy words (word 0 the polled word, then one a position) and the
+    workspace."""
+
+    def __init__(self, V: int, max_pos: int, device="cuda"):
+        self.V = V
+        self.ws_bytes = int(lib().embla_sample_workspace_bytes(V))
+        if self.ws_bytes == 0:
+            raise ValueError("vocabulary outside 1 .. 65536")
+        self.ws = torch.empty(self.ws_bytes, dtype=torch.uint8, device=device)
+        self.tokens = torch.zeros(max_pos + 2, dtype=torch.int32, device=device)
+        self.greedy = torch.zeros(max_pos + 3, dtype=torch.int32, device=device)
+
+    def _args(self, pos, prompt_len):
+        if not 0 <= pos <= self.tokens.numel() - 2:
+            raise ValueError("position outside the buffers")
+        return _p(self.tokens), self.V, self.greedy.data_ptr() + 4, pos, prompt_len
+
+
+def argmax(logits, st: SampleState, pos: int, prompt_len: int = 0, stream=None):
+    """The greedy token of fp32 logits [V] at position pos (misc.metal:86-128)."""
+    tok, V, g, pos, pl = st._args(pos, prompt_len)
+    call("embla_argmax", _p(logits), tok, V, g, pos, pl, _p(st.ws), st.ws_bytes, stream_handle(stream))
+
+
+def sample(logits, st: SampleState, pos: int, inv_t: float, top_p: float, seed: int, prompt_len: int = 0,
+           stream=None):
+    """The top-p Gumbel draw at position pos (misc.metal:196-298)."""
+    tok, V, g, pos, pl = st._args(pos, prompt_len)
+    call("embla_sample", _p(logits), tok, V, g, pos, pl, inv_t, top_p, seed & 0xFFFFFFFF, _p(st.ws), st.ws_bytes,
+         stream_handle(stream))

@@ -302,6 +302,28 @@ int embla_gemv_q4(const void* W, const void* X, void* Y, const EmblaSeg* segs, i
 int embla_gemm_q4(const void* W, const unsigned long long* wo, const void* X, void* Y, int T, int O, int K,
                   int ldx, int ldy, int epi, hipStream_t stream);
 
+/* ---------------------------------------------------------------- sampling tail
+ * The token of a step from V (<= 65536) fp32 logits, each softcapped in bf16 as
+ * bf(bf(tanh(bf(bf(l) / 15))) * 15). Outputs as the reference's: greedy[pos] = the token; past the
+ * prompt (pos + 1 >= prompt_len) token[pos + 1] = the token; last, greedy[-1] =
+ * (pos + 1) << 16 | token, written at system scope after the others for a host that polls it.
+ * `greedy` points one word into its buffer (the reference binds it at byte offset 4). logits
+ * 16-byte aligned. Workspace: embla_sample_workspace_bytes(V) bytes, no zeroing needed. */
+size_t embla_sample_workspace_bytes(int V);
+
+/* The greedy token: the first index of the largest softcapped logit (misc.metal:86-128, the
+ * `argmax` dispatch of Engine.swift:972-987). */
+int embla_argmax(const float* logits, uint32_t* token, int V, uint32_t* greedy, int pos, int prompt_len, void* ws,
+                 size_t ws_bytes, hipStream_t stream);
+
+/* A draw from softmax(c / T) cut to its top-p nucleus by the Gumbel-max trick (misc.metal:196-298,
+ * the `sample` dispatch of Engine.swift:972-987, SampleParams {1/T, top-p, seed}): inv_t = 1/T > 0,
+ * 0 < top_p <= 1; the noise of token i is a hash of (seed, pos, i), so a draw is a function of its
+ * inputs. Callers wanting greedy decoding (T <= 0 or top-p <= 0, Sampling.isGreedy) call
+ * embla_argmax. */
+int embla_sample(const float* logits, uint32_t* token, int V, uint32_t* greedy, int pos, int prompt_len, float inv_t,
+                 float top_p, uint32_t seed, void* ws, size_t ws_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -11,6 +11,8 @@
  *     214-282 (attn_full_b); attn_nax.metal:61-364 (causal ReLU² prefill)
  *   Sources/EmblaMetal/Kernels/gemv.metal:1-92, gemm.metal:1-134, common.metal:104-152 (the
  *     4-bit projections either side of attention: y = W x with MLX's affine 4-bit layout)
+ *   Sources/EmblaMetal/Kernels/misc.metal:83-128 (argmax), 164-298 (sample: the top-p nucleus by
+ *     bisection and the Gumbel-max draw)
  * and the BASELINE configs' variants of them (softmax full layers, fp16 scales, 4 kv heads,
  * window 1024, the ReLU² index scorer  score_j = Σ_h w_h relu(q_h·k_j)²).
  *
@@ -362,4 +364,147 @@ void orc_q4_matvec(const uint32_t* w, const uint16_t* s, const uint16_t* b, cons
             default: y[r] = a; break;
         }
     }
+}
+
+/* ------------------------------------------------------------------ sampling tail
+ * misc.metal:83-128 (argmax) and 164-298 (sample). */
+
+/* The softcap of one logit as the reference computes it: bf(bf(tanh(bf(bf(l) / 15))) * 15)
+ * (misc.metal:101, 216). tanh in fp64 rounded once to fp32: the correctly rounded fp32 tanh that
+ * precise::tanh approximates. */
+float orc_softcap(float l) {
+    const float y = bf(bf(l) / 15.0f);
+    const float t = (float)tanh((double)y);
+    return bf(bf(t) * 15.0f);
+}
+
+/* The first index of the largest softcapped logit (misc.metal:99-121). */
+uint32_t orc_argmax(const float* logits, int V) {
+    float best = -INFINITY;
+    uint32_t idx = 0;
+    for (int i = 0; i < V; i++) {
+        const float c = orc_softcap(logits[i]);
+        if (c > best) { best = c; idx = (uint32_t)i; }
+    }
+    return idx;
+}
+
+/* The 32-bit integer mix of misc.metal:186-191 (the "lowbias32" finaliser: xorshift-multiply
+ * rounds with the constants 0x7feb352d and 0x846ca68b). */
+uint32_t orc_mix32(uint32_t x) {
+    x ^= x >> 16; x *= 0x7feb352du;
+    x ^= x >> 15; x *= 0x846ca68bu;
+    x ^= x >> 16;
+    return x;
+}
+
+/* Gumbel noise of token i for a step key: -log(-log(u)), u in (0, 1) from the hash's top 24 bits
+ * (misc.metal:278-281). */
+static float gumbel_g(uint32_t key, uint32_t i) {
+    const float u = ((float)(orc_mix32(key ^ i) >> 8) + 0.5f) * (1.0f / 16777216.0f);
+    return logf(-logf(u));
+}
+
+static double rel(double a, double b) { return fabs(a - b) / (fabs(b) > 1e-30 ? fabs(b) : 1e-30); }
+/* a within 2 fp32 ulps of b: an exp or log that differs by an ulp may order them otherwise */
+static int near2(float a, float b) { return fabs((double)a - b) <= 2.0 * ((double)nextafterf(fabsf(b), INFINITY) - fabsf(b)); }
+
+/* The token misc.metal:196-298 draws at position pos: softmax(softcap(l) / T) cut to its top-p
+ * nucleus by bisection on exp(x) (over the tokens with exp(x) >= 1/16384 when they are at most 2048
+ * and hold top-p of the mass, else over all), then the argmax of x + Gumbel noise over the nucleus.
+ * Sums are in fp64 (the reference's are fp32 in an unspecified order). *fragile is set when a
+ * decision of the draw lies within floating-point error of its boundary (a sum within 2e-5 of
+ * top-p's mass, relative: above the error of an fp32 sum of 65536 terms by blocks and trees; an
+ * exp(x) within 2 ulps of a threshold it is compared with; an x within 2 ulps of the nucleus
+ * floor; the two best Gumbel scores unequal and within 1e-5): an implementation
+ * that sums in another order or whose exp/log differ by an ulp may then draw another token. Equal
+ * best scores are no hazard: they come from one x and one hash value, equal everywhere, and the
+ * lower index wins. */
+static float sample_threshold(const float* logits, int V, float inv_t, float top_p, float* x, int* fragile) {
+    const float CMIN = 1.0f / 16384.0f;
+    float* e = (float*)malloc(sizeof(float) * (size_t)V);
+    float mx = -INFINITY;
+    for (int i = 0; i < V; i++) {
+        x[i] = orc_softcap(logits[i]) * inv_t;
+        mx = fmaxf(mx, x[i]);
+    }
+    double z = 0.0;
+    for (int i = 0; i < V; i++) {
+        x[i] = x[i] - mx;
+        e[i] = expf(x[i]);
+        z += e[i];
+    }
+    int frag = 0;
+    float lo = 0.0f;
+    if (top_p < 1.0f) {
+        const float want = top_p * (float)z;
+        int nc = 0;
+        double cm = 0.0;
+        for (int i = 0; i < V; i++) {
+            if (near2(e[i], CMIN)) frag = 1;
+            if (e[i] >= CMIN) { nc++; cm += e[i]; }
+        }
+        float hi = 1.0f;
+        const int cand = nc <= 2048 && cm >= want;
+        if (nc <= 2048 && rel(cm, want) < 2e-5) frag = 1;
+        lo = cand ? CMIN : 0.0f;
+        for (int it = 0; it < 20; it++) {
+            const float mid = 0.5f * (lo + hi);
+            double kept = 0.0;
+            for (int i = 0; i < V; i++) {
+                if (cand && e[i] < CMIN) continue;
+                if (near2(e[i], mid)) frag = 1;
+                kept += e[i] >= mid ? e[i] : 0.0f;
+            }
+            if (rel(kept, want) < 2e-5) frag = 1;
+            if (kept >= want) lo = mid; else hi = mid;
+        }
+    }
+    free(e);
+    *fragile = frag;
+    return lo;
+}
+
+/* The draw at pos given x and the threshold lo (misc.metal:274-298). */
+static uint32_t sample_draw(const float* x, int V, float lo, int pos, uint32_t seed, int* fragile) {
+    int frag = 0;
+    const float floor_x = lo > 0.0f ? logf(lo) : -INFINITY;
+    const uint32_t key = orc_mix32(seed ^ orc_mix32((uint32_t)pos * 0x9e3779b9u));
+    float best = -INFINITY, second = -INFINITY;
+    uint32_t idx = 0;
+    for (int i = 0; i < V; i++) {
+        if (lo > 0.0f && near2(x[i], floor_x)) frag = 1;
+        if (x[i] < floor_x) continue;
+        const float sc = x[i] - gumbel_g(key, (uint32_t)i);
+        if (sc > best) { second = best; best = sc; idx = (uint32_t)i; }
+        else if (sc > second) second = sc;
+    }
+    if (best > second && best - second < 1e-5 * fmax(1.0, fabs(best))) frag = 1;
+    *fragile = frag;
+    return idx;
+}
+
+uint32_t orc_sample(const float* logits, int V, int pos, float inv_t, float top_p, uint32_t seed, int* fragile) {
+    float* x = (float*)malloc(sizeof(float) * (size_t)V);
+    int f1 = 0, f2 = 0;
+    const float lo = sample_threshold(logits, V, inv_t, top_p, x, &f1);
+    const uint32_t tok = sample_draw(x, V, lo, pos, seed, &f2);
+    free(x);
+    if (fragile) *fragile = f1 | f2;
+    return tok;
+}
+
+/* Draws at positions pos0 .. pos0 + n - 1 of one row of logits (the threshold does not depend on
+ * the position). */
+void orc_sample_many(const float* logits, int V, int pos0, int n, float inv_t, float top_p, uint32_t seed,
+                     uint32_t* tokens, int32_t* fragile) {
+    float* x = (float*)malloc(sizeof(float) * (size_t)V);
+    int f1 = 0;
+    const float lo = sample_threshold(logits, V, inv_t, top_p, x, &f1);
+    for (int k = 0; k < n; k++) {
+        int f2 = 0;
+        tokens[k] = sample_draw(x, V, lo, pos0 + k, seed, &f2);
+        fragile[k] = f1 | f2;
+    }
+    free(x);
 }

@@ -49,6 +49,15 @@ def lib() -> C.CDLL:
         L.orc_prefill_int8.argtypes = [f32, i8, f32, i8, f32, C.c_int, C.c_int, C.c_int, C.c_int,
                                        C.c_int, C.c_int, C.c_int, opt, C.c_int, f32]
         L.orc_q4_matvec.argtypes = [u32, u16, u16, u16, C.c_int, C.c_int, C.c_int, f32]
+        L.orc_softcap.argtypes = [C.c_float]
+        L.orc_softcap.restype = C.c_float
+        L.orc_argmax.argtypes = [f32, C.c_int]
+        L.orc_argmax.restype = C.c_uint32
+        L.orc_mix32.argtypes = [C.c_uint32]
+        L.orc_mix32.restype = C.c_uint32
+        L.orc_sample.argtypes = [f32, C.c_int, C.c_int, C.c_float, C.c_float, C.c_uint32, P(np.int32)]
+        L.orc_sample.restype = C.c_uint32
+        L.orc_sample_many.argtypes = [f32, C.c_int, C.c_int, C.c_int, C.c_float, C.c_float, C.c_uint32, u32, i32]
         L.orc_f16_to_f32.argtypes = [C.c_uint16]
         L.orc_f16_to_f32.restype = C.c_float
         L.orc_f32_to_f16.argtypes = [C.c_float]
@@ -167,3 +176,32 @@ def q4_matvec(w, s, b, x, epi=4, y=None):
     lib().orc_q4_matvec(w.reshape(-1), _c(s, np.uint16).reshape(-1), _c(b, np.uint16).reshape(-1),
                         _c(x, np.uint16).reshape(-1), O, K, epi, out)
     return out
+
+
+def softcap(logits):
+    """bf(bf(tanh(bf(bf(l) / 15))) * 15) of each logit (misc.metal:101)."""
+    f = lib().orc_softcap
+    return np.array([f(float(v)) for v in np.asarray(logits, np.float32).reshape(-1)], np.float32)
+
+
+def argmax(logits) -> int:
+    """The greedy token: first index of the largest softcapped logit (misc.metal:86-128)."""
+    lg = _c(logits, np.float32).reshape(-1)
+    return int(lib().orc_argmax(lg, lg.size))
+
+
+def sample(logits, pos, inv_t, top_p, seed):
+    """The top-p Gumbel draw of misc.metal:196-298 -> (token, fragile)."""
+    lg = _c(logits, np.float32).reshape(-1)
+    fr = np.zeros(1, np.int32)
+    tok = lib().orc_sample(lg, lg.size, pos, inv_t, top_p, seed & 0xFFFFFFFF, fr)
+    return int(tok), bool(fr[0])
+
+
+def sample_many(logits, pos0, n, inv_t, top_p, seed):
+    """Draws at positions pos0 .. pos0 + n - 1 -> (tokens, fragile flags)."""
+    lg = _c(logits, np.float32).reshape(-1)
+    tok = np.zeros(n, np.uint32)
+    fr = np.zeros(n, np.int32)
+    lib().orc_sample_many(lg, lg.size, pos0, n, inv_t, top_p, seed & 0xFFFFFFFF, tok, fr)
+    return tok, fr.astype(bool)

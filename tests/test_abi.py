@@ -72,3 +72,23 @@ def test_block_copy_rejects_bad_arguments():
     assert L.embla_kv_block_copy(d, regs, 65, 128, 1024, 4, 0, d, 1, None) < 0
     assert L.embla_ring_block_copy(d, regs, 2, 128, 1000, 4, d, 0, None) < 0
     assert L.embla_ring_block_bytes(2, 4) == 2 * 2 * 4 * 128 * 256
+
+
+def test_sampling_rejects_bad_arguments():
+    """The sampling tail: vocabulary outside 1 .. 65536, unaligned logits, T or top-p out of range,
+    a short workspace (no GPU: validation precedes any HIP call)."""
+    L = _lib.lib()
+    d = C.c_void_p(256)
+    g = C.c_void_p(260)
+    assert L.embla_sample_workspace_bytes(0) == 0 and L.embla_sample_workspace_bytes(65537) == 0
+    ws = L.embla_sample_workspace_bytes(65536)
+    assert ws == 65536 * 2 + 2560 + 64 * 4096
+    assert L.embla_argmax(d, d, 65537, g, 0, 0, d, ws, None) < 0
+    assert L.embla_argmax(C.c_void_p(260), d, 1000, g, 0, 0, d, ws, None) < 0
+    assert L.embla_argmax(d, d, 65536, g, 0, 0, d, ws - 1, None) < 0
+    assert L.embla_sample(d, d, 65536, g, 0, 0, 0.0, 0.9, 1, d, ws, None) < 0
+    assert L.embla_sample(d, d, 65536, g, 0, 0, float("inf"), 0.9, 1, d, ws, None) < 0
+    assert L.embla_sample(d, d, 65536, g, 0, 0, 1.0, 0.0, 1, d, ws, None) < 0
+    assert L.embla_sample(d, d, 65536, g, 0, 0, 1.0, 1.5, 1, d, ws, None) < 0
+    assert L.embla_sample(d, d, 65536, g, -1, 0, 1.0, 0.9, 1, d, ws, None) < 0
+    assert L.embla_sample(d, d, 65536, g, 0, 0, 1.0, 0.9, 1, None, ws, None) < 0
