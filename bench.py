@@ -148,7 +148,7 @@ def bench_c4(torch, reps=20):
 
 
 def bench_blocks(torch, reps=20):
-    """Prefix-cache block save + restore (§8 next row 2): 16 blocks (positions 16384 + 128 i ..,
+    """Prefix-cache block save + restore: 16 blocks (positions 16384 + 128 i ..,
     i < 16) of 16 full layers at C3's shape (4 kv heads, 32768 positions, int8 + fp16 scales), each
     saved then restored, in one graph (a graph of a single pair would time the graph launch);
     bytes = each copy's reads and writes."""
@@ -172,7 +172,7 @@ def bench_blocks(torch, reps=20):
 
 
 def bench_gemv(torch, reps=20):
-    """The decode projections either side of attention (§8 next row 1): per layer q/k/v (3072 rows)
+    """The decode projections either side of attention: per layer q/k/v (3072 rows)
     and the o-projection (2048 rows, accumulating into an fp32 residual) of one token, K = 2048,
     4-bit weights in MLX's layout; 48 distinct layers (283 MB of weights, beyond the 256 MB MALL)
     in one graph. Algorithmic bytes: the weights' words, scales and biases."""
@@ -213,7 +213,7 @@ def bench_gemv(torch, reps=20):
 
 
 def bench_gemm(torch, reps=10):
-    """The prefill projections either side of attention (§8 next row 1): C5's 2048-token chunk
+    """The prefill projections either side of attention: C5's 2048-token chunk
     through q/k/v (3072 rows) and the o-projection (2048 rows, accumulating into an fp32
     residual), K = 2048, 4-bit weights in MLX's layout; one graph. FLOPs 2 T O K."""
     from embla_attn import ops
@@ -240,10 +240,10 @@ def bench_gemm(torch, reps=10):
 
 
 def bench_step(torch, regions, L=32768, reps=20):
-    """The whole attention sub-layer decode step of one token (§8 next row 3) over C3's 16-layer
+    """The whole attention sub-layer decode step of one token over C3's 16-layer
     stack at context L, captured as one graph: per layer the 4-bit q/k/v projection, the int8 append
-    of the new k and v at position L - 1, the q preparation, the split-K decode over L positions
-    (bf16 out) and the 4-bit o-projection into the fp32 residual. Algorithmic bytes a layer: the
+    of the new k and v at position L - 1, the split-K decode over L positions with the q head norm
+    inside its kernel (bf16 out) and the 4-bit o-projection into the fp32 residual. Algorithmic bytes a layer: the
     cache as in C3 plus the weights."""
     from embla_attn import ops
     n_layers, D, n_q, n_kv, max_s = len(regions), 2048, 16, 4, 32768
@@ -265,7 +265,6 @@ def bench_step(torch, regions, L=32768, reps=20):
         segs.append(lay)
     x = torch.randn(D, device="cuda").bfloat16()
     qkv = torch.empty(3072, dtype=torch.bfloat16, device="cuda")
-    qf = torch.empty(1, n_q, 128, dtype=torch.float16, device="cuda")
     o = torch.empty(n_q, 128, dtype=torch.bfloat16, device="cuda")
     resid = torch.empty(D, dtype=torch.float32, device="cuda")
     ws = ops.Workspace(max_s, n_q)
@@ -276,18 +275,17 @@ def bench_step(torch, regions, L=32768, reps=20):
             kc, vc = regions[l]
             ops.gemv_q4(W, x, qkv, [segs[l][0]], D, ops.EPI_BF16)
             ops.kv_quant_append(qkv[2048:2560], qkv[2560:3072], 1, L - 1, n_kv, kc, vc, max_s)
-            ops.q_prep(qkv[:2048], None, None, 0, 1, n_q, out=qf)
-            ops.decode_int8(qf[0], kc, vc, L, max_s, n_kv, out_dtype=ops.BF16, ws=ws, out=o)
+            ops.decode_int8_qraw(qkv[:2048], kc, vc, L, max_s, n_kv, ws=ws, out=o)
             ops.gemv_q4(W, o, resid, [segs[l][1]], D, ops.EPI_ADD)
     wall, ms = time_graph(torch, run, reps, 3)
     us = ms * 1000 / n_layers
     nbytes = layer_bytes(L) + lw
-    return dict(context=L, layers=n_layers, kernels_per_layer=6, bytes_layer=nbytes, us_per_layer=us,
+    return dict(context=L, layers=n_layers, kernels_per_layer=5, bytes_layer=nbytes, us_per_layer=us,
                 gbs=nbytes / (us * 1e-6) / 1e9, frac_hbm=nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS)
 
 
 def bench_sampling(torch, reps=10):
-    """The sampling tail (§8 next row 4) on a 65536-token row: the greedy token, a top-p draw over
+    """The sampling tail on a 65536-token row: the greedy token, a top-p draw over
     few candidates (a peaked row: 316 tokens within 1/16384 of the top) and a draw that bisects
     over every token (a flat row); 32 positions a graph. Latency-bound: µs a call."""
     from embla_attn import ops

@@ -124,6 +124,39 @@ int embla_decode_int8(const void* q, const void* kc, const void* vc, void* o, fl
     return launch_full_decode(a, stream);
 }
 
+int embla_decode_int8_qraw(const void* qraw, const void* g1, const void* g2, int ng, const void* kc, const void* vc,
+                           void* o, int S, int max_s, int n_q, int n_kv, int scale_dtype, int out_dtype, int chunk,
+                           void* ws, size_t ws_bytes, hipStream_t stream) {
+    if (!qraw || !kc || !vc || !o || ng < 0 || ng > 2 || (ng >= 1 && !g1) || (ng >= 2 && !g2)) return EMBLA_ERR_INVALID;
+    if (S <= 0 || max_s <= 0 || max_s % 32 || S > max_s) return EMBLA_ERR_INVALID;
+    if (n_kv <= 0 || n_q % n_kv || n_kv > kMaxKV) return EMBLA_ERR_INVALID;
+    if (!valid_scale(scale_dtype) || !valid_act(out_dtype)) return EMBLA_ERR_INVALID;
+    if (chunk < 0 || chunk % 32) return EMBLA_ERR_INVALID;
+    const int ch = chunk ? chunk : decode_chunk(S, n_kv);
+    const int C = (S + ch - 1) / ch;
+    if (C > kMaxChunks) return EMBLA_ERR_INVALID;
+    if (C > 1) {
+        if (!ws || ws_bytes < embla_workspace_bytes(max_s, n_q)) return EMBLA_ERR_WORKSPACE;
+        if ((size_t)C * n_q * kPartStride * 4 > part_bytes(max_s, n_q)) return EMBLA_ERR_WORKSPACE;
+    }
+    Workspace w = ws ? carve(ws, max_s, n_q) : Workspace{nullptr, nullptr, nullptr};
+    FullDecodeArgs a;
+    a.q = (const uint16_t*)qraw;
+    a.g1 = (const uint16_t*)g1;
+    a.g2 = (const uint16_t*)g2;
+    a.ng = ng;
+    a.kc = (const int8_t*)kc;
+    a.vc = (const int8_t*)vc;
+    a.part = w.part;
+    a.scores = nullptr;
+    a.o = (uint16_t*)o;
+    a.S = S; a.CH = ch; a.C = C; a.max_s = max_s; a.n_q = n_q; a.n_kv = n_kv;
+    a.relu2 = false;
+    a.scale32 = scale_dtype == EMBLA_F32;
+    a.out_bf16 = out_dtype == EMBLA_BF16;
+    return launch_full_decode(a, stream);
+}
+
 int embla_q_prep(const void* qraw, const void* g1, const void* g2, int ng, int stride, int T,
                  int n_q, void* out, int out_dtype, hipStream_t stream) {
     if (!qraw || !out || T <= 0 || n_q <= 0 || ng < 0 || ng > 2 || stride < n_q * 128) return EMBLA_ERR_INVALID;
@@ -138,15 +171,17 @@ int embla_attn_full8(const void* qraw, const void* g1, const void* g2, const voi
                      hipStream_t stream) {
     if (!p || !part || !counter) return EMBLA_ERR_INVALID;
     if (p->S <= 0 || p->maxS <= 0 || p->maxS % 32 || p->S > p->maxS) return EMBLA_ERR_INVALID;
-    // the reference's part buffer doubles as this call's workspace: q, then the partials
-    const size_t need = embla_workspace_bytes(p->maxS, 16);
+    if (!qraw || p->ng < 0 || p->ng > 2 || (p->ng >= 1 && !g1) || (p->ng >= 2 && !g2)) return EMBLA_ERR_INVALID;
+    // the reference's part buffer doubles as this call's workspace (the partials); the head norm
+    // of q runs inside the decode kernel, as in the reference's kernel
     Workspace w = carve(part, p->maxS, 16);
-    int rc = embla_q_prep(qraw, g1, g2, p->ng, 16 * 128, 1, 16, w.qprep, EMBLA_F16, stream);
-    if (rc) return rc;
     const int ch = p->CH > 0 ? p->CH : decode_chunk(p->S, 2);
     if (ch % 32 || (p->S + ch - 1) / ch > kMaxChunks) return EMBLA_ERR_INVALID;
     FullDecodeArgs a;
-    a.q = w.qprep;
+    a.q = (const uint16_t*)qraw;
+    a.g1 = (const uint16_t*)g1;
+    a.g2 = (const uint16_t*)g2;
+    a.ng = p->ng;
     a.kc = (const int8_t*)kc;
     a.vc = (const int8_t*)vc;
     a.part = w.part;
@@ -155,7 +190,6 @@ int embla_attn_full8(const void* qraw, const void* g1, const void* g2, const voi
     a.o = (uint16_t*)o;
     a.S = p->S; a.CH = ch; a.C = (p->S + ch - 1) / ch; a.max_s = p->maxS; a.n_q = 16; a.n_kv = 2;
     a.relu2 = true; a.scale32 = true; a.out_bf16 = true;
-    (void)need;
     return launch_full_decode(a, stream);
 }
 
@@ -165,14 +199,17 @@ int embla_attn_sparse8(const void* qraw, const void* g1, const void* g2, const v
     if (!p || !part || !counter) return EMBLA_ERR_INVALID;
     if (p->S <= 0 || p->maxS <= 0 || p->maxS % 32 || p->S > p->maxS) return EMBLA_ERR_INVALID;
     Workspace w = carve(part, p->maxS, 16);
-    int rc = embla_q_prep(qraw, g1, g2, p->ng, 16 * 128, 1, 16, w.qprep, EMBLA_F16, stream);
-    if (rc) return rc;
     (void)counter;   // no counters: the partials are merged by a second kernel
-    if (!idx) {      // SEL = 0: every key 0 .. S-1, softmax (attention.metal:448-584)
+    if (!idx) {      // SEL = 0: every key 0 .. S-1, softmax (attention.metal:448-584); the head
+                     // norm of q inside the decode kernel
+        if (!qraw || p->ng < 0 || p->ng > 2 || (p->ng >= 1 && !g1) || (p->ng >= 2 && !g2)) return EMBLA_ERR_INVALID;
         const int ch = p->CH > 0 ? p->CH : decode_chunk(p->S, 2);
         if (ch % 32 || (p->S + ch - 1) / ch > kMaxChunks) return EMBLA_ERR_INVALID;
         FullDecodeArgs a;
-        a.q = w.qprep;
+        a.q = (const uint16_t*)qraw;
+        a.g1 = (const uint16_t*)g1;
+        a.g2 = (const uint16_t*)g2;
+        a.ng = p->ng;
         a.kc = (const int8_t*)kc;
         a.vc = (const int8_t*)vc;
         a.part = w.part;
@@ -183,6 +220,8 @@ int embla_attn_sparse8(const void* qraw, const void* g1, const void* g2, const v
         return launch_full_decode(a, stream);
     }
     // SEL: the rows idx[kv head][0 .. S) of the tile cache, gathered
+    int rc = embla_q_prep(qraw, g1, g2, p->ng, 16 * 128, 1, 16, w.qprep, EMBLA_F16, stream);
+    if (rc) return rc;
     const int ch = p->CH > 0 ? p->CH : kSparseRefCH;
     if (ch % 32 || ch > kTopK + kRecent) return EMBLA_ERR_INVALID;
     const int C = (p->S + ch - 1) / ch;

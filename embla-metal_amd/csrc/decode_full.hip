@@ -59,12 +59,13 @@ __device__ __forceinline__ void scales8(const u4_t* r, float* out) {
 
 constexpr int DW = 8;            // waves a workgroup: one 32-key tile each a round
 
-template <int GQ, bool RELU2, bool SCALE32, bool OBF, bool SCORES>
+template <int GQ, bool RELU2, bool SCALE32, bool OBF, bool SCORES, bool QR>
 __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
-    const uint16_t* __restrict__ q,   // [n_kv * GQ][128] fp16, prepared
+    const uint16_t* __restrict__ q,   // [n_kv * GQ][128]: fp16 prepared, or (QR) raw bf16
     const int8_t* __restrict__ kc, const int8_t* __restrict__ vc,
     float* __restrict__ part, float* __restrict__ scores, uint16_t* __restrict__ o, int S, int CH,
-    int C, int max_s, int n_kv, float qk_scale, float sink) {
+    int C, int max_s, int n_kv, float qk_scale, float sink, const uint16_t* __restrict__ g1,
+    const uint16_t* __restrict__ g2, int ng) {
     static_assert(GQ == 4 || GQ == 8, "4 or 8 query heads a kv head");
     const int c = blockIdx.x, kvh = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -97,8 +98,32 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
             const u4_t r = ld16(qr + 8 * u);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                qf[8 * u + 2 * i] = h2f((uint16_t)(r[i] & 0xFFFF));
-                qf[8 * u + 2 * i + 1] = h2f((uint16_t)(r[i] >> 16));
+                qf[8 * u + 2 * i] = QR ? bf2f((uint16_t)(r[i] & 0xFFFF)) : h2f((uint16_t)(r[i] & 0xFFFF));
+                qf[8 * u + 2 * i + 1] = QR ? bf2f((uint16_t)(r[i] >> 16)) : h2f((uint16_t)(r[i] >> 16));
+            }
+        }
+        if constexpr (QR) {
+            // the head norm of common.metal:13-26 (q_prep's): x * rms * (1 + g1) * (1 + g2),
+            // rounded to bf16; the lane groups g = 0..3 hold dims 32 g .. 32 g + 31
+            float ss = 0.0f;
+#pragma unroll
+            for (int d = 0; d < 32; d++) ss += qf[d] * qf[d];
+            ss += shfl_xor(ss, 16);
+            ss += shfl_xor(ss, 32);
+            const float rf = 1.0f / sqrtf(ss / 128.0f + 1.1920929e-07f);
+            u4_t ga[4], gb[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                ga[u] = ng >= 1 ? ld16(g1 + 32 * g + 8 * u) : (u4_t){0, 0, 0, 0};
+                gb[u] = ng >= 2 ? ld16(g2 + 32 * g + 8 * u) : (u4_t){0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int d = 0; d < 32; d++) {
+                const uint32_t wa = ga[d / 8][(d % 8) / 2], wb = gb[d / 8][(d % 8) / 2];
+                float gf = rf;
+                if (ng >= 1) gf = gf * (1.0f + bf2f((uint16_t)(d & 1 ? wa >> 16 : wa & 0xFFFF)));
+                if (ng >= 2) gf = gf * (1.0f + bf2f((uint16_t)(d & 1 ? wb >> 16 : wb & 0xFFFF)));
+                qf[d] = bf2f(f2bf(qf[d] * gf));
             }
         }
 #pragma unroll
@@ -375,10 +400,19 @@ int launch_full_decode(const FullDecodeArgs& a, hipStream_t st) {
     const float qs = 0.08838834764831845f;   // 1/sqrt(128)
     const float sink = 11.313708498984761f;   // sqrt(128)
 #define EMBLA_FD(GQ, R, S32, OBF, SC)                                                              \
-    hipLaunchKernelGGL((full_decode_kernel<GQ, R, S32, OBF, SC>), grid, block, 0, st, a.q, a.kc, a.vc, \
-                       a.part, a.scores, a.o, a.S, a.CH, a.C, a.max_s, a.n_kv, qs, sink)
+    hipLaunchKernelGGL((full_decode_kernel<GQ, R, S32, OBF, SC, false>), grid, block, 0, st, a.q, a.kc, a.vc, \
+                       a.part, a.scores, a.o, a.S, a.CH, a.C, a.max_s, a.n_kv, qs, sink, nullptr, nullptr, 0)
+#define EMBLA_FDR(GQ, R, S32, OBF, SC)                                                             \
+    hipLaunchKernelGGL((full_decode_kernel<GQ, R, S32, OBF, SC, true>), grid, block, 0, st, a.q, a.kc, a.vc, \
+                       a.part, a.scores, a.o, a.S, a.CH, a.C, a.max_s, a.n_kv, qs, sink, a.g1, a.g2, a.ng)
     const int gq = a.n_q / a.n_kv;
-    if (gq == 4 && !a.relu2 && !a.scale32 && !a.out_bf16 && !a.scores) EMBLA_FD(4, false, false, false, false);
+    if (a.ng >= 0) {   // raw queries: the reference's full and sparse layers, and the decode step
+        if (gq == 8 && a.relu2 && a.scale32 && a.out_bf16 && !a.scores) EMBLA_FDR(8, true, true, true, false);
+        else if (gq == 8 && a.relu2 && a.scale32 && a.out_bf16 && a.scores) EMBLA_FDR(8, true, true, true, true);
+        else if (gq == 8 && !a.relu2 && a.scale32 && a.out_bf16 && !a.scores) EMBLA_FDR(8, false, true, true, false);
+        else if (gq == 4 && !a.relu2 && !a.scale32 && a.out_bf16 && !a.scores) EMBLA_FDR(4, false, false, true, false);
+        else return EMBLA_ERR_UNSUPPORTED;
+    } else if (gq == 4 && !a.relu2 && !a.scale32 && !a.out_bf16 && !a.scores) EMBLA_FD(4, false, false, false, false);
     else if (gq == 4 && !a.relu2 && a.scale32 && a.out_bf16 && !a.scores) EMBLA_FD(4, false, true, true, false);
     else if (gq == 4 && !a.relu2 && !a.scale32 && a.out_bf16 && !a.scores) EMBLA_FD(4, false, false, true, false);
     else if (gq == 8 && a.relu2 && a.scale32 && a.out_bf16 && !a.scores) EMBLA_FD(8, true, true, true, false);
@@ -387,6 +421,7 @@ int launch_full_decode(const FullDecodeArgs& a, hipStream_t st) {
     else if (gq == 8 && !a.relu2 && !a.scale32 && !a.out_bf16 && !a.scores) EMBLA_FD(8, false, false, false, false);
     else return EMBLA_ERR_UNSUPPORTED;
 #undef EMBLA_FD
+#undef EMBLA_FDR
     if (a.C > 1) return launch_decode_merge(a.part, a.o, a.C, a.n_q, a.relu2, a.out_bf16, WSCALE, st);
     return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
 }

@@ -16,6 +16,11 @@ struct FullDecodeArgs {
     uint16_t* o;
     int S, CH, C, max_s, n_q, n_kv;
     bool relu2, scale32, out_bf16;
+    // raw queries (ng >= 0): q holds bf16 rows [n_q][128] straight from the q/k/v projection; the
+    // kernel applies the head norm with ng (0-2) gains g1, g2 and the bf16 rounding itself
+    const uint16_t* g1 = nullptr;
+    const uint16_t* g2 = nullptr;
+    int ng = -1;
 };
 int launch_full_decode(const FullDecodeArgs& a, hipStream_t st);
 /// Merges C chunk partials [C][n_q][132] into o [n_q][128]; the partials' sums carry a factor oscale.

@@ -50,6 +50,17 @@ def decode_int8(q, kc, vc, S, max_s, n_kv, weights=SOFTMAX, scale_dtype=F16, out
     return out
 
 
+def decode_int8_qraw(qraw, kc, vc, S, max_s, n_kv, g1=None, g2=None, ng=0, scale_dtype=F16, out_dtype=BF16,
+                     chunk=0, ws: Workspace | None = None, out=None, stream=None):
+    """Split-K decode (softmax) of raw bf16 q [n_q][128], head-normed inside the kernel."""
+    n_q = qraw.numel() // 128
+    if out is None:
+        out = torch.empty((n_q, 128), dtype=_DT[out_dtype], device=qraw.device)
+    call("embla_decode_int8_qraw", _p(qraw), _p(g1), _p(g2), ng, _p(kc), _p(vc), _p(out), S, max_s, n_q, n_kv,
+         scale_dtype, out_dtype, chunk, ws.ptr if ws else None, ws.nbytes if ws else 0, stream_handle(stream))
+    return out
+
+
 def kv_quant_append(k, v, T, p0, n_kv, kc, vc, max_s, in_dtype=BF16, scale_dtype=F16, norm_k=False,
                     stride=None, stream=None):
     stride = stride if stride is not None else n_kv * 128

@@ -245,6 +245,15 @@ int embla_attn_sparse8(const void* qraw, const void* g1, const void* g2, const v
 int embla_kv_append(const void* qkv, void* cache, const EmblaKVJob* jobs, int njobs, int pm_pos,
                     int maxS, int T, hipStream_t stream);
 
+/* embla_decode_int8 with the q preparation folded in (softmax weights): q is the raw bf16 q of
+ * the q/k/v projection [n_q][128], head-normed with ng (0-2) bf16 gains and rounded to bf16 inside
+ * the decode kernel, as the reference's attention kernels do (common.metal:13-26 called from
+ * attention.metal:235-363), instead of a separate embla_q_prep launch. Combinations: n_q / n_kv = 4,
+ * fp16 scales, bf16 output; n_q / n_kv = 8, fp32 scales, bf16 output. */
+int embla_decode_int8_qraw(const void* qraw, const void* g1, const void* g2, int ng, const void* kc, const void* vc,
+                           void* o, int S, int max_s, int n_q, int n_kv, int scale_dtype, int out_dtype, int chunk,
+                           void* ws, size_t ws_bytes, hipStream_t stream);
+
 /* Query preparation (head_norm with ng gains + bf16 rounding; attention.metal:167-169,
  * prefill.metal:406-426): qraw bf16 rows of `stride` elements, n_q heads, T tokens ->
  * out [T][n_q][128] in out_dtype. */

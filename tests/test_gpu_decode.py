@@ -64,6 +64,28 @@ def test_decode_f16_scales_bf16_out(torch_gpu, orc, S):
     assert_close(bf16_host(o), oracle_cfg(orc, c), what=f"S={S}")
 
 
+@pytest.mark.parametrize("ng,S", [(0, 3000), (2, 32768), (1, 77)])
+def test_decode_qraw_matches_oracle(torch_gpu, orc, ng, S):
+    """embla_decode_int8_qraw: raw bf16 q, head-normed (with ng gains) inside the decode kernel."""
+    from embla_attn import ops
+    torch = torch_gpu
+    say(f"decode raw q ng={ng} S={S}")
+    c = synth.decode_int8_case(seed=13 + ng, S=S)
+    g = synth.SplitMix64(50 + ng)
+    qraw = synth.bf16_bits(g.normal(16 * 128) * 3)
+    g1 = synth.bf16_bits(g.normal(128) * 0.2)
+    g2 = synth.bf16_bits(g.normal(128) * 0.2)
+    ms = (S + 31) // 32 * 32
+    kc, vc = upload_int8_case(c, ms)
+    o = ops.decode_int8_qraw(dev(qraw, torch.bfloat16), kc, vc, S, ms, 4, g1=dev(g1, torch.bfloat16),
+                             g2=dev(g2, torch.bfloat16), ng=ng, ws=ops.Workspace(ms, 16))
+    torch.cuda.synchronize()
+    qn = np.stack([orc.head_norm(synth.bf16_val(qraw.reshape(16, 128)[h]), synth.bf16_val(g1), synth.bf16_val(g2), ng)
+                   for h in range(16)])
+    ref = orc.decode_int8(qn, c["K"], synth.f16_val(c["ks"]), c["V"], synth.f16_val(c["vs"]))
+    assert_close(bf16_host(o), ref, what=f"ng={ng} S={S}")
+
+
 def test_decode_repeated_calls_leave_counters_zero(torch_gpu, orc):
     from embla_attn import ops
     say("decode repeated calls, one workspace")

@@ -1,6 +1,7 @@
-"""A whole attention sub-layer decode step captured as one HIP graph (§8 next row 3: the event-
-chained step of Engine.swift:71-88 as a graph): per layer the q/k/v projection, the int8 append of
-the new k, v, the q preparation, the split-K decode and the o-projection into an fp32 residual.
+"""A whole attention sub-layer decode step captured as one HIP graph (the event-chained step of
+Engine.swift:71-88 as a graph): per layer the q/k/v projection, the int8 append of the new k, v,
+the q preparation and split-K decode (layer 0 as two calls, layer 1 as the decode with the head
+norm inside) and the o-projection into an fp32 residual.
 The graph is replayed several times with eager work between the replays, and every replay's
 outputs (the decode outputs, the residual, the appended cache bytes) equal the eager step's bit
 for bit: every kernel here reduces in a fixed order."""
@@ -54,7 +55,7 @@ def test_graph_decode_step_replays(torch_gpu, orc):
         vc = dev(layout.pack_region(hist["V"], hist["vs"], max_s, "v"))
         layers.append(dict(W=W, segs=segs, osegs=osegs, kc=kc, vc=vc, ws=ops.Workspace(max_s, n_q),
                            o=torch.empty(n_q, 128, dtype=torch.bfloat16, device="cuda"),
-                           qf=torch.empty(1, n_q, 128, dtype=torch.float16, device="cuda")))
+                           qf=torch.empty(1, n_q, 128, dtype=torch.float16, device="cuda"), raw=l % 2 == 1))
     x = dev(synth.bf16_bits(g.normal(D).astype(np.float32)), torch.bfloat16)
     qkv = torch.empty(3072, dtype=torch.bfloat16, device="cuda")
     resid = torch.empty(D, dtype=torch.float32, device="cuda")
@@ -64,9 +65,12 @@ def test_graph_decode_step_replays(torch_gpu, orc):
         for L in layers:
             ops.gemv_q4(L["W"], x, qkv, L["segs"], D, ops.EPI_BF16)
             ops.kv_quant_append(qkv[2048:2560], qkv[2560:3072], 1, pos, n_kv, L["kc"], L["vc"], max_s)
-            ops.q_prep(qkv[:2048], None, None, 0, 1, n_q, out=L["qf"])
-            ops.decode_int8(L["qf"][0], L["kc"], L["vc"], pos + 1, max_s, n_kv, out_dtype=ops.BF16, ws=L["ws"],
-                            out=L["o"])
+            if L["raw"]:   # the head norm inside the decode kernel
+                ops.decode_int8_qraw(qkv[:2048], L["kc"], L["vc"], pos + 1, max_s, n_kv, ws=L["ws"], out=L["o"])
+            else:
+                ops.q_prep(qkv[:2048], None, None, 0, 1, n_q, out=L["qf"])
+                ops.decode_int8(L["qf"][0], L["kc"], L["vc"], pos + 1, max_s, n_kv, out_dtype=ops.BF16,
+                                ws=L["ws"], out=L["o"])
             ops.gemv_q4(L["W"], L["o"], resid, L["osegs"], D, ops.EPI_ADD)
 
     def snapshot():
@@ -88,7 +92,12 @@ def test_graph_decode_step_replays(torch_gpu, orc):
         K, ks = layout.unpack_region(cache[:rb], n_kv, max_s, "k", np.uint16)
         V, vs = layout.unpack_region(cache[rb:], n_kv, max_s, "v", np.uint16)
         n = pos + 1
-        q = L["qf"].float().cpu().numpy()[0]
+        if L["raw"]:   # the last layer: the step's final q/k/v are its own
+            assert l == n_layers - 1
+            qb = qkv[:2048].view(torch.int16).cpu().numpy().view(np.uint16).reshape(n_q, 128)
+            q = np.stack([orc.head_norm(synth.bf16_val(qb[h])) for h in range(n_q)])
+        else:
+            q = L["qf"].float().cpu().numpy()[0]
         ref = orc.decode_int8(q, K[:, :n], synth.f16_val(ks[:, :n]), V[:, :n], synth.f16_val(vs[:, :n]))
         assert_close(want[l], ref, what=f"layer {l} decode")
     graph = torch.cuda.CUDAGraph()
