@@ -21,7 +21,9 @@
 //    capped value packed in a word, compacted in the block's own list) and the block's Gumbel
 //    winner over all its tokens (the draw when the threshold stays 0); sample_final_kernel (one
 //    workgroup) sums the block records and runs the bisection over the <= 2048 candidates in LDS;
-//    when the reference would bisect over all tokens it holds the row in registers instead.
+//    when the reference would bisect over all tokens it holds the row's e in registers instead
+//    (64 a thread), and draws again only the blocks whose winner over all tokens lies outside the
+//    nucleus.
 // Every value a later kernel needs is recomputed from the capped bf16 with the same rounded
 // operations (__fmul_rn, __fsub_rn: no contraction), so x and e agree bit for bit between kernels.
 #include "common.hpp"
@@ -139,7 +141,7 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restric
 }
 
 // ------------------------------------------------------------------ the draw
-struct BlockRec { float z, cm; uint32_t nc; float s; uint32_t si; uint32_t pad[3]; };
+struct BlockRec { float z, cm; uint32_t nc; float s; uint32_t si; float x; uint32_t pad[2]; };   // x: the winner's
 
 /// the global max of x's scale: the largest block maximum (every wave computes it)
 __device__ __forceinline__ float global_max(const float* bmax, int G) {
@@ -204,7 +206,8 @@ __global__ __launch_bounds__(256) void sample_weights_kernel(const uint16_t* __r
             r.nc += sn[ww];
             best_of(r.s, r.si, ss[ww], ssi[ww]);
         }
-        r.pad[0] = r.pad[1] = r.pad[2] = 0;
+        r.x = r.si < (uint32_t)V ? __fsub_rn(__fmul_rn(bf2f(cb[r.si]), inv_t), M) : NEG_INF;
+        r.pad[0] = r.pad[1] = 0;
         rec[b] = r;
     }
 }
@@ -239,9 +242,8 @@ __global__ __launch_bounds__(FT) void sample_final_kernel(const uint16_t* __rest
                                                           const float* __restrict__ bmax, int G, uint32_t key,
                                                           const BlockRec* __restrict__ rec, const uint32_t* __restrict__ cand,
                                                           uint32_t* token, uint32_t* greedy, int pos, int prompt) {
-    // the candidates' e and words, or on the all-token path the e of tokens q >= FPT / 8 (the
-    // rest stay in registers): 128 KB
-    __shared__ float lds[FPT / 2 * FT];
+    // the candidates' e and words
+    __shared__ float lds[2 * NCAND];
     float* ce = lds;
     uint32_t* cw = (uint32_t*)(lds + NCAND);
     __shared__ uint32_t off[65];
@@ -249,6 +251,8 @@ __global__ __launch_bounds__(FT) void sample_final_kernel(const uint16_t* __rest
     __shared__ float bv[FW];
     __shared__ uint32_t bix[FW];
     __shared__ float tot[3];
+    __shared__ float ws_[64], wx_[64];   // the blocks' all-token Gumbel winners: score, x
+    __shared__ uint32_t wi_[64];
     const int t = threadIdx.x, lane = t & 63;
     const float M = global_max(bmax, G);
     // the block records: wave 0 sums them and scans the candidate counts
@@ -265,6 +269,9 @@ __global__ __launch_bounds__(FT) void sample_final_kernel(const uint16_t* __rest
         if (lane == 0) off[0] = 0;
         float s = lane < G ? r.s : NEG_INF;
         uint32_t si = lane < G ? r.si : 0xFFFFFFFFu;
+        ws_[lane] = s;
+        wi_[lane] = si;
+        wx_[lane] = lane < G ? r.x : NEG_INF;
         wave_best(s, si);
         const float z = wave_sum(lane < G ? r.z : 0.0f), cm = wave_sum(lane < G ? r.cm : 0.0f);
         if (lane == 0) { tot[0] = z; tot[1] = cm; tot[2] = s; bix[0] = si; }
@@ -337,8 +344,7 @@ __global__ __launch_bounds__(FT) void sample_final_kernel(const uint16_t* __rest
             if (t == 0) write_token(bi, token, greedy, pos, prompt);
             return;
         }
-        // every token: the row in registers (capped values as packed pairs), token 4 t + 4096 q + k
-        // the capped pairs of a quad (re-read for the draw: the first read left them in this L2)
+        // every token: the row's e in registers (64 a thread), token 4 t + 4096 q + k
         auto quad = [&](int q) {
             const int i0 = 4 * t + 4 * FT * q;
             if (i0 + 3 < V) return ld8(cb + i0);
@@ -347,7 +353,7 @@ __global__ __launch_bounds__(FT) void sample_final_kernel(const uint16_t* __rest
             for (int k = 0; k < 4; k++) h[k] = i0 + k < V ? cb[i0 + k] : 0;
             return (u2_t){h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
         };
-        float e[FPT / 2];
+        float e[FPT];
 #pragma unroll
         for (int q = 0; q < FPT / 4; q++) {
             const u2_t c2 = quad(q);
@@ -356,34 +362,45 @@ __global__ __launch_bounds__(FT) void sample_final_kernel(const uint16_t* __rest
                 const int i = 4 * t + 4 * FT * q + k;
                 const uint16_t c = (uint16_t)(c2[k >> 1] >> (16 * (k & 1)));
                 const float v = i < V ? expf(__fsub_rn(__fmul_rn(bf2f(c), inv_t), M)) : 0.0f;
-                if (q < FPT / 8) e[4 * q + k] = v;
-                else lds[(4 * q + k - FPT / 2) * FT + t] = v;
+                e[4 * q + k] = v;
             }
         }
         for (int it = 0; it < 20; it++) {
             const float mid = __fmul_rn(0.5f, __fadd_rn(lo, hi));
             float kept = 0.0f;
 #pragma unroll
-            for (int k = 0; k < FPT / 2; k++) kept += e[k] >= mid ? e[k] : 0.0f;
-#pragma unroll 8
-            for (int k = 0; k < FPT / 2; k++) {
-                const float v = lds[k * FT + t];
-                kept += v >= mid ? v : 0.0f;
-            }
+            for (int k = 0; k < FPT; k++) kept += e[k] >= mid ? e[k] : 0.0f;
             if (block_sum(kept, red[it & 1]) >= want) lo = mid; else hi = mid;
         }
         if (lo > 0.0f) {
+            // a block's winner over all its tokens is its winner over its nucleus tokens when it
+            // is in the nucleus itself; the other blocks are drawn again, a wave a block
             const float floor_x = logf(lo);
+            const int w = t >> 6;
             float best = NEG_INF;
             uint32_t bi = 0xFFFFFFFFu;
-            for (int q = 0; q < FPT / 4; q++) {
-                const u2_t c2 = quad(q);
+            for (int b = w; b < G; b += FW) {
+                if (wx_[b] >= floor_x) {
+                    best_of(best, bi, ws_[b], wi_[b]);
+                    continue;
+                }
 #pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const int i = 4 * t + 4 * FT * q + k;
-                    const uint16_t c = (uint16_t)(c2[k >> 1] >> (16 * (k & 1)));
-                    const float x = __fsub_rn(__fmul_rn(bf2f(c), inv_t), M);
-                    if (i < V && x >= floor_x) best_of(best, bi, gumbel_score(x, key, (uint32_t)i), (uint32_t)i);
+                for (int q = 0; q < SB / 256; q++) {
+                    const int i0 = b * SB + 256 * q + 4 * lane;
+                    u2_t c2;
+                    if (i0 + 3 < V) c2 = ld8(cb + i0);
+                    else {
+                        uint32_t h[4];
+#pragma unroll
+                        for (int k = 0; k < 4; k++) h[k] = i0 + k < V ? cb[i0 + k] : 0;
+                        c2 = (u2_t){h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+                    }
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        const int i = i0 + k;
+                        const float x = __fsub_rn(__fmul_rn(bf2f((uint16_t)(c2[k >> 1] >> (16 * (k & 1)))), inv_t), M);
+                        if (i < V && x >= floor_x) best_of(best, bi, gumbel_score(x, key, (uint32_t)i), (uint32_t)i);
+                    }
                 }
             }
             block_best(best, bi, bv, bix);
