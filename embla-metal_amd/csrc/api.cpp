@@ -92,10 +92,14 @@ int embla_workspace_init(void* ws, size_t ws_bytes, hipStream_t stream) {
     return hipMemsetAsync(ws, 0, kCounterBytes, stream) == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
 }
 
-int embla_decode_int8(const void* q, const void* kc, const void* vc, void* o, float* scores, int S,
-                      int max_s, int n_q, int n_kv, int weights, int scale_dtype, int out_dtype,
-                      int chunk, void* ws, size_t ws_bytes, hipStream_t stream) {
-    if (!q || !kc || !vc || !o) return EMBLA_ERR_INVALID;
+}  // extern "C"
+
+namespace {
+
+/// The split-K decode's arguments from embla_decode_int8's (validated); rc != 0 on a bad argument.
+int full_decode_args(const void* q, const void* kc, const void* vc, void* o, float* scores, int S, int max_s, int n_q,
+                     int n_kv, int weights, int scale_dtype, int out_dtype, int chunk, void* ws, size_t ws_bytes,
+                     FullDecodeArgs& a) {
     if (S <= 0 || max_s <= 0 || max_s % 32 || S > max_s) return EMBLA_ERR_INVALID;
     if (n_kv <= 0 || n_q % n_kv || n_kv > kMaxKV) return EMBLA_ERR_INVALID;
     if (weights != EMBLA_SOFTMAX && weights != EMBLA_RELU2_SINK) return EMBLA_ERR_INVALID;
@@ -110,7 +114,6 @@ int embla_decode_int8(const void* q, const void* kc, const void* vc, void* o, fl
         if ((size_t)C * n_q * kPartStride * 4 > part_bytes(max_s, n_q)) return EMBLA_ERR_WORKSPACE;
     }
     Workspace w = ws ? carve(ws, max_s, n_q) : Workspace{nullptr, nullptr, nullptr};
-    FullDecodeArgs a;
     a.q = (const uint16_t*)q;
     a.kc = (const int8_t*)kc;
     a.vc = (const int8_t*)vc;
@@ -121,7 +124,45 @@ int embla_decode_int8(const void* q, const void* kc, const void* vc, void* o, fl
     a.relu2 = weights == EMBLA_RELU2_SINK;
     a.scale32 = scale_dtype == EMBLA_F32;
     a.out_bf16 = out_dtype == EMBLA_BF16;
+    return EMBLA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int embla_decode_int8(const void* q, const void* kc, const void* vc, void* o, float* scores, int S,
+                      int max_s, int n_q, int n_kv, int weights, int scale_dtype, int out_dtype,
+                      int chunk, void* ws, size_t ws_bytes, hipStream_t stream) {
+    if (!q || !kc || !vc || !o) return EMBLA_ERR_INVALID;
+    FullDecodeArgs a;
+    const int rc = full_decode_args(q, kc, vc, o, scores, S, max_s, n_q, n_kv, weights, scale_dtype, out_dtype, chunk,
+                                    ws, ws_bytes, a);
+    return rc ? rc : launch_full_decode(a, stream);
+}
+
+int embla_decode_int8_partials(const void* q, const void* kc, const void* vc, float* scores, int S, int max_s,
+                               int n_q, int n_kv, int weights, int scale_dtype, int out_dtype, int chunk, void* ws,
+                               size_t ws_bytes, hipStream_t stream) {
+    if (!q || !kc || !vc || !ws) return EMBLA_ERR_INVALID;
+    FullDecodeArgs a;
+    const int rc = full_decode_args(q, kc, vc, nullptr, scores, S, max_s, n_q, n_kv, weights, scale_dtype, out_dtype,
+                                    chunk, ws, ws_bytes, a);
+    if (rc) return rc;
+    if (a.C < 2) return EMBLA_ERR_INVALID;   // one chunk writes o itself: nothing to merge
+    a.merge = false;
     return launch_full_decode(a, stream);
+}
+
+int embla_decode_int8_merge(void* o, int S, int max_s, int n_q, int n_kv, int weights, int out_dtype, int chunk,
+                            void* ws, size_t ws_bytes, hipStream_t stream) {
+    if (!o || !ws) return EMBLA_ERR_INVALID;
+    FullDecodeArgs a;
+    const int rc = full_decode_args(o, o, o, o, nullptr, S, max_s, n_q, n_kv, weights, EMBLA_F16, out_dtype, chunk, ws,
+                                    ws_bytes, a);
+    if (rc) return rc;
+    if (a.C < 2) return EMBLA_ERR_INVALID;
+    return launch_full_decode_merge(a, stream);
 }
 
 int embla_decode_int8_qraw(const void* qraw, const void* g1, const void* g2, int ng, const void* kc, const void* vc,

@@ -8,11 +8,12 @@
 //
 // The MI355X design (not the reference's): a wave64 takes 32-key tiles. S^T = K·q^T runs on
 // v_mfma_i32_16x16x64_i8 straight on the cache's int8 K bytes: q is held as a 15-bit fixed point
-// per head (|error| <= absmax/64000) split exactly into two int8 halves, q = s·(256·hi + lo), which
-// sit in columns n and n + GQ of the B operand, so one MFMA gives both partial sums. A lane (head n,
-// lane group g) of the score tile then holds keys {16t + 4g + i}, which is exactly the A-operand
-// slice it needs for O += W·V (v_mfma_f32_16x16x32_f16, V bytes converted exactly to fp16), so the
-// weights never move between lanes. K and V tiles are stored in MFMA lane order (common.hpp), so
+// per head (|error| <= absmax/64000) split exactly into two int8 halves, q = s·(256·hi + lo), each
+// half its own B operand (column n = head n), so both partial sums land in the lane that combines
+// them (two more MFMAs a tile instead of a cross-lane exchange a score: 10.50 against 10.69 us a
+// launch at 32k). A lane (head n, lane group g) of the score tile then holds keys {16t + 4g + i},
+// which is exactly the A-operand slice it needs for O += W·V (v_mfma_f32_16x16x32_f16, V bytes
+// converted exactly to fp16), so the weights never move between lanes. K and V tiles are stored in MFMA lane order (common.hpp), so
 // each of a wave's 8 loads a tile reads 1 KB contiguous. Scores and weights stay in fp32;
 // W = p·scale_v is rounded to fp16 (with a power-of-two prescale) only as the MFMA operand.
 // Chunk partials are merged by a second, wide kernel (a workgroup a (query head, 32 dims), one
@@ -83,13 +84,14 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
 #pragma unroll
     for (int u = 0; u < 8; u++) O[u] = (f4_t){0, 0, 0, 0};
 
-    i4_t qb[2];
+    i4_t qb[2], ql[2];
     float qsc = 0.0f;   // the fixed point's step, per head
-    // q as a 15-bit fixed point split into int8 halves: column n < GQ holds hi of head n, column
-    // GQ + n holds lo; lane (n, g), MFMA b: dims 32g + 16b .. + 15 (the K slice's dims).
+    // q as a 15-bit fixed point split into int8 halves, hi in qb and lo in ql: column n < GQ holds
+    // head n (other columns 0); lane (n, g), MFMA b: dims 32g + 16b .. + 15 (the K slice's dims).
+    // Separate operands put both halves' products in the lane that uses them (no cross-lane step).
     auto setup_q = [&]() {
         const int hn = n % GQ;
-        const bool live = n < 2 * GQ, is_lo = n >= GQ;
+        const bool live = n < GQ;
         const uint16_t* qr = q + ((size_t)kvh * GQ + hn) * HD + 32 * g;
         float qf[32];
         float am = 0.0f;
@@ -136,15 +138,16 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
         for (int b = 0; b < 2; b++) {
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                uint32_t word = 0;
+                uint32_t wh = 0, wl = 0;
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const int qi = (int)rintf(qf[16 * b + 4 * k + e] * inv);
                     const int hi = (qi + 128) >> 8, lo = qi - hi * 256;
-                    const int byte = live ? (is_lo ? lo : hi) : 0;
-                    word |= (uint32_t)(byte & 0xFF) << (8 * e);
+                    wh |= (uint32_t)((live ? hi : 0) & 0xFF) << (8 * e);
+                    wl |= (uint32_t)((live ? lo : 0) & 0xFF) << (8 * e);
                 }
-                qb[b][k] = (int)word;
+                qb[b][k] = (int)wh;
+                ql[b][k] = (int)wl;
             }
         }
     };
@@ -175,14 +178,13 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
         float x[8];
 #pragma unroll
         for (int t = 0; t < 2; t++) {
-            i4_t st = {0, 0, 0, 0};
+            i4_t st = {0, 0, 0, 0}, sl = {0, 0, 0, 0};
             st = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i4_t, T.k[2 * t]), qb[0], st, 0, 0, 0);
             st = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i4_t, T.k[2 * t + 1]), qb[1], st, 0, 0, 0);
+            sl = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i4_t, T.k[2 * t]), ql[0], sl, 0, 0, 0);
+            sl = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i4_t, T.k[2 * t + 1]), ql[1], sl, 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int lo = __shfl_xor(st[i], GQ, 64);
-                x[4 * t + i] = (float)(st[i] * 256 + lo) * qsc * ks[4 * t + i];
-            }
+            for (int i = 0; i < 4; i++) x[4 * t + i] = (float)(st[i] * 256 + sl[i]) * qsc * ks[4 * t + i];
         }
         bool valid[8];
 #pragma unroll
@@ -422,8 +424,12 @@ int launch_full_decode(const FullDecodeArgs& a, hipStream_t st) {
     else return EMBLA_ERR_UNSUPPORTED;
 #undef EMBLA_FD
 #undef EMBLA_FDR
-    if (a.C > 1) return launch_decode_merge(a.part, a.o, a.C, a.n_q, a.relu2, a.out_bf16, WSCALE, st);
+    if (a.C > 1 && a.merge) return launch_decode_merge(a.part, a.o, a.C, a.n_q, a.relu2, a.out_bf16, WSCALE, st);
     return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
+}
+
+int launch_full_decode_merge(const FullDecodeArgs& a, hipStream_t st) {
+    return launch_decode_merge(a.part, a.o, a.C, a.n_q, a.relu2, a.out_bf16, WSCALE, st);
 }
 
 int launch_decode_merge(const float* part, uint16_t* o, int C, int n_q, bool relu2, bool out_bf16, float oscale,

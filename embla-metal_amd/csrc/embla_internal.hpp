@@ -21,8 +21,11 @@ struct FullDecodeArgs {
     const uint16_t* g1 = nullptr;
     const uint16_t* g2 = nullptr;
     int ng = -1;
+    bool merge = true;   // false: leave the chunk partials (C > 1) for a later merge
 };
 int launch_full_decode(const FullDecodeArgs& a, hipStream_t st);
+/// The merge launch_full_decode ends with, on its own (a.C > 1, partials in a.part).
+int launch_full_decode_merge(const FullDecodeArgs& a, hipStream_t st);
 /// Merges C chunk partials [C][n_q][132] into o [n_q][128]; the partials' sums carry a factor oscale.
 int launch_decode_merge(const float* part, uint16_t* o, int C, int n_q, bool relu2, bool out_bf16, float oscale,
                         hipStream_t st);

@@ -50,6 +50,20 @@ def decode_int8(q, kc, vc, S, max_s, n_kv, weights=SOFTMAX, scale_dtype=F16, out
     return out
 
 
+def decode_int8_partials(q, kc, vc, S, max_s, n_kv, ws: Workspace, weights=SOFTMAX, scale_dtype=F16, out_dtype=F16,
+                         chunk=0, scores=None, stream=None):
+    """The split-K kernel of decode_int8 alone: chunk partials left in ws."""
+    call("embla_decode_int8_partials", _p(q), _p(kc), _p(vc), _p(scores), S, max_s, q.shape[0], n_kv, weights,
+         scale_dtype, out_dtype, chunk, ws.ptr, ws.nbytes, stream_handle(stream))
+
+
+def decode_int8_merge(out, S, max_s, n_kv, ws: Workspace, weights=SOFTMAX, out_dtype=F16, chunk=0, stream=None):
+    """The merge of decode_int8_partials' chunk partials into out [n_q][128]."""
+    call("embla_decode_int8_merge", _p(out), S, max_s, out.shape[0], n_kv, weights, out_dtype, chunk, ws.ptr,
+         ws.nbytes, stream_handle(stream))
+    return out
+
+
 def decode_int8_qraw(qraw, kc, vc, S, max_s, n_kv, g1=None, g2=None, ng=0, scale_dtype=F16, out_dtype=BF16,
                      chunk=0, ws: Workspace | None = None, out=None, stream=None):
     """Split-K decode (softmax) of raw bf16 q [n_q][128], head-normed inside the kernel."""

@@ -79,6 +79,18 @@ int embla_decode_int8(const void* q, const void* kc, const void* vc, void* o, fl
                       int S, int max_s, int n_q, int n_kv, int weights, int scale_dtype,
                       int out_dtype, int chunk, void* ws, size_t ws_bytes, hipStream_t stream);
 
+/* embla_decode_int8 as its two launches, for a caller that merges later or times the split-K
+ * kernel alone: _partials runs the chunks (at least two) and leaves their partials in ws;
+ * _merge reads them and writes o. Same arguments as embla_decode_int8 (the merge's S, max_s,
+ * n_q, n_kv, weights, out_dtype and chunk as the partials call's); nothing may touch ws between
+ * the two. No counterpart in the reference, whose arrive_last step merges inside the kernel
+ * (common.metal:86-99). */
+int embla_decode_int8_partials(const void* q, const void* kc, const void* vc, float* scores, int S, int max_s,
+                               int n_q, int n_kv, int weights, int scale_dtype, int out_dtype, int chunk, void* ws,
+                               size_t ws_bytes, hipStream_t stream);
+int embla_decode_int8_merge(void* o, int S, int max_s, int n_q, int n_kv, int weights, int out_dtype, int chunk,
+                            void* ws, size_t ws_bytes, hipStream_t stream);
+
 /* Reference-signature full layer (attn_full8, attention.metal:235-363; bound at Engine.swift:
  * 800-818): raw bf16 q [16][128] normed with p->ng gains g1, g2 (common.metal:13-26) and rounded
  * to bf16, ReLU² with sink over the int8 cache of 2 kv heads with fp32 scales; o bf16 [16][128].

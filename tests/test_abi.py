@@ -92,3 +92,13 @@ def test_sampling_rejects_bad_arguments():
     assert L.embla_sample(d, d, 65536, g, 0, 0, 1.0, 1.5, 1, d, ws, None) < 0
     assert L.embla_sample(d, d, 65536, g, -1, 0, 1.0, 0.9, 1, d, ws, None) < 0
     assert L.embla_sample(d, d, 65536, g, 0, 0, 1.0, 0.9, 1, None, ws, None) < 0
+
+
+def test_decode_split_rejects_single_chunk():
+    """The partials/merge pair needs at least two chunks: one chunk writes o itself."""
+    L = _lib.lib()
+    d = C.c_void_p(256)
+    ws = L.embla_workspace_bytes(1024, 16)
+    assert L.embla_decode_int8_partials(d, d, d, None, 100, 1024, 16, 4, 0, 0, 0, 0, d, ws, None) < 0
+    assert L.embla_decode_int8_merge(d, 100, 1024, 16, 4, 0, 0, 0, d, ws, None) < 0
+    assert L.embla_decode_int8_partials(d, d, d, None, 1024, 1024, 16, 4, 0, 0, 0, 256, None, 0, None) < 0

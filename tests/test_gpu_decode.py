@@ -86,6 +86,24 @@ def test_decode_qraw_matches_oracle(torch_gpu, orc, ng, S):
     assert_close(bf16_host(o), ref, what=f"ng={ng} S={S}")
 
 
+@pytest.mark.parametrize("S", [32768, 3000])
+def test_decode_partials_then_merge_equals_one_call(torch_gpu, S):
+    """embla_decode_int8_partials + embla_decode_int8_merge run the one-call decode's two kernels."""
+    from embla_attn import ops
+    torch = torch_gpu
+    say(f"decode partials + merge S={S}")
+    c = synth.decode_int8_case(seed=21, S=S)
+    ms = (S + 31) // 32 * 32
+    kc, vc = upload_int8_case(c, ms)
+    q = dev(c["q"], torch.float16)
+    ws = ops.Workspace(ms, 16)
+    one = ops.decode_int8(q, kc, vc, S, ms, 4, ws=ws)
+    ops.decode_int8_partials(q, kc, vc, S, ms, 4, ws)
+    two = ops.decode_int8_merge(torch.empty_like(one), S, ms, 4, ws)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(two.cpu().numpy(), one.cpu().numpy())
+
+
 def test_decode_repeated_calls_leave_counters_zero(torch_gpu, orc):
     from embla_attn import ops
     say("decode repeated calls, one workspace")
