@@ -6,9 +6,9 @@
 // [O][K/64], w = s * nibble + b), segments as the reference's Seg records (rows stacked, each with
 // its own input and output offset), epilogues EPI 0-4 (gemv.metal:77-88).
 //
-// MI355X design. A wave takes 4 rows; lane l holds 4 words (16 bytes, columns 32 l .. 32 l + 31)
-// of each 2048-column span, so a row is one coalesced 1 KB load a span, and all 4 rows' words,
-// scales and biases are requested before x is read. Two columns go through one v_dot2_f32_bf16:
+// MI355X design. A wave takes RW rows (one, at launch); lane l holds 4 words (16 bytes, columns
+// 32 l .. 32 l + 31) of each 2048-column span, so a row is one coalesced 1 KB load a span, and the
+// rows' words, scales and biases are requested before x is read. Two columns go through one v_dot2_f32_bf16:
 // the nibbles of columns 8j + k and 8j + k + 4 of word j sit 16 bits apart, so
 // (word >> 4k) & 0x000F000F | 0x43004300 is the bf16 pair (128 + q, 128 + q') exactly (bf16 holds
 // integers to 256), and x is paired the same way once a wave (v_perm_b32). The 128 folds into the
@@ -24,10 +24,10 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2v_t, a), __builtin_bit_cast(bf2v_t, b), c, false);
 }
 
-template <int EPI>
+template <int EPI, int RW>
 __global__ __launch_bounds__(256) void gemv_q4_kernel(GemvArgs a) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int row0 = (blockIdx.x * 4 + w) * 4;   // the wave's first stacked row
+    const int row0 = (blockIdx.x * 4 + w) * RW;   // the wave's first stacked row
     int si = 0, start = 0;
     while (si < a.nseg && row0 >= (int)a.seg[si].end) { start = (int)a.seg[si].end; si++; }
     if (si >= a.nseg) return;
@@ -37,10 +37,10 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(GemvArgs a) {
     const char* W = (const char*)a.W;
 
     constexpr int MAXS = 2;   // spans a lane keeps in registers (K <= 4096)
-    u4_t wd[4][MAXS];
-    float sc[4][MAXS], bi[4][MAXS];
+    u4_t wd[RW][MAXS];
+    float sc[RW][MAXS], bi[RW][MAXS];
 #pragma unroll
-    for (int u = 0; u < 4; u++)
+    for (int u = 0; u < RW; u++)
 #pragma unroll
         for (int sp = 0; sp < MAXS; sp++)
             if (sp < spans) {
@@ -52,13 +52,20 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(GemvArgs a) {
     // x: the lane's 32 columns of each span as bf16 pairs (8j + k, 8j + k + 4), and their sum
     uint32_t xp[MAXS][16];
     float xs[MAXS];
+    // x is read once a workgroup into LDS (its 4 waves' rows share one segment: segment ends are
+    // multiples of 4 rows), after the weights are requested
     const uint16_t* X = (const uint16_t*)a.X + sg.x;
+    __shared__ u4_t xl[MAXS * 256];
+#pragma unroll
+    for (int sp = 0; sp < MAXS; sp++)
+        if (sp < spans) xl[256 * sp + threadIdx.x] = ld16(X + 2048 * sp + 8 * threadIdx.x);
+    __syncthreads();
 #pragma unroll
     for (int sp = 0; sp < MAXS; sp++) {
         if (sp < spans) {
             u4_t v[4];
 #pragma unroll
-            for (int j = 0; j < 4; j++) v[j] = ld16(X + 2048 * sp + 32 * lane + 8 * j);
+            for (int j = 0; j < 4; j++) v[j] = xl[256 * sp + 4 * lane + j];
             float s = 0.0f;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
@@ -74,9 +81,9 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(GemvArgs a) {
             xs[sp] = s;
         }
     }
-    float acc[4];
+    float acc[RW];
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
+    for (int u = 0; u < RW; u++) {
         float r = 0.0f;
 #pragma unroll
         for (int sp = 0; sp < MAXS; sp++) {
@@ -94,10 +101,10 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(GemvArgs a) {
         for (int o = 32; o >= 1; o >>= 1) r += shfl_xor(r, o);
         acc[u] = r;
     }
-    if (lane < 4) {   // lane u writes row u
+    if (lane < RW) {   // lane u writes row u
         float v = acc[0];
 #pragma unroll
-        for (int u = 1; u < 4; u++) v = lane == u ? acc[u] : v;
+        for (int u = 1; u < RW; u++) v = lane == u ? acc[u] : v;
         const size_t at = sg.y + (size_t)(r0 + lane);
         if constexpr (EPI == 0) ((uint16_t*)a.Y)[at] = f2bf(v);
         else if constexpr (EPI == 1) {
@@ -109,18 +116,23 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(GemvArgs a) {
     }
 }
 
-int launch_gemv_q4(const GemvArgs& a, int epi, hipStream_t st) {
+template <int RW>
+int launch_gemv_q4_rw(const GemvArgs& a, int epi, hipStream_t st) {
     const int rows = (int)a.seg[a.nseg - 1].end;
-    const dim3 grid((rows + 15) / 16), block(256);
+    const dim3 grid((rows + 4 * RW - 1) / (4 * RW)), block(256);
     switch (epi) {
-        case 0: hipLaunchKernelGGL(gemv_q4_kernel<0>, grid, block, 0, st, a); break;
-        case 1: hipLaunchKernelGGL(gemv_q4_kernel<1>, grid, block, 0, st, a); break;
-        case 2: hipLaunchKernelGGL(gemv_q4_kernel<2>, grid, block, 0, st, a); break;
-        case 3: hipLaunchKernelGGL(gemv_q4_kernel<3>, grid, block, 0, st, a); break;
-        case 4: hipLaunchKernelGGL(gemv_q4_kernel<4>, grid, block, 0, st, a); break;
+        case 0: hipLaunchKernelGGL((gemv_q4_kernel<0, RW>), grid, block, 0, st, a); break;
+        case 1: hipLaunchKernelGGL((gemv_q4_kernel<1, RW>), grid, block, 0, st, a); break;
+        case 2: hipLaunchKernelGGL((gemv_q4_kernel<2, RW>), grid, block, 0, st, a); break;
+        case 3: hipLaunchKernelGGL((gemv_q4_kernel<3, RW>), grid, block, 0, st, a); break;
+        case 4: hipLaunchKernelGGL((gemv_q4_kernel<4, RW>), grid, block, 0, st, a); break;
         default: return EMBLA_ERR_INVALID;
     }
     return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
 }
+
+// One row a wave: 3072 q/k/v rows are 768 workgroups, enough requests in flight to cover every
+// CU (48-layer q/k/v + o: 4 rows a wave 11.1 us a layer, 2 rows 9.1 us, 1 row 8.4 us).
+int launch_gemv_q4(const GemvArgs& a, int epi, hipStream_t st) { return launch_gemv_q4_rw<1>(a, epi, st); }
 
 }  // namespace embla
