@@ -65,6 +65,9 @@ def make_caches(torch, n_layers: int, max_s: int, n_kv: int = 4, seed_layer0: in
     return regions, case
 
 
+LAST_MEDIAN_MS = [0.0]   # the median replay of the last time_graph call
+
+
 def time_graph(torch, fn, steps: int, warmup: int):
     """Captures fn() once as a graph, replays `warmup` untimed then `steps` timed replays between
     synchronisations; returns (seconds, ms a replay by events)."""
@@ -78,15 +81,17 @@ def time_graph(torch, fn, steps: int, warmup: int):
     for _ in range(warmup):
         g.replay()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     t0 = time.perf_counter()
-    e0.record()
-    for _ in range(steps):
+    ev[0].record()
+    for i in range(steps):
         g.replay()
-    e1.record()
+        ev[i + 1].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    return wall, e0.elapsed_time(e1) / steps
+    per = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+    LAST_MEDIAN_MS[0] = per[steps // 2]
+    return wall, ev[0].elapsed_time(ev[steps]) / steps
 
 
 def bench_c3(torch, steps, warmup, n_layers=16, contexts=(4096, 16384, 32768)):
@@ -103,6 +108,7 @@ def bench_c3(torch, steps, warmup, n_layers=16, contexts=(4096, 16384, 32768)):
                 ops.decode_int8(q, regions[i][0], regions[i][1], L, max_s, 4, ws=ws, out=outs[i])
         wall, ms = time_graph(torch, step, steps if L == max_s else max(10, steps // 2), warmup)
         res[L] = dict(ms_per_step=ms, us_per_layer=ms * 1000 / n_layers, wall_s=wall,
+                      us_per_layer_median=LAST_MEDIAN_MS[0] * 1000 / n_layers,
                       gbs=layer_bytes(L) * n_layers / (ms * 1e-3) / 1e9)
     # the split-K kernel alone (no merge), the dominant kernel of the roofline: 16 launches a graph
     L = max_s
@@ -527,6 +533,7 @@ def main():
         },
         "c3_sweep_us_per_layer": {str(k): round(v["us_per_layer"], 3) for k, v in res.items()},
         "c3_sweep_gbs": {str(k): round(v["gbs"], 1) for k, v in res.items()},
+        "c3_sweep_us_per_layer_median": {str(k): round(v["us_per_layer_median"], 3) for k, v in res.items()},
         "c2_sliding": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in c2.items()},
         "c4_sparse": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in c4.items()},
         "c5_prefill_full": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c5.items()
