@@ -94,6 +94,15 @@ def time_graph(torch, fn, steps: int, warmup: int):
     return wall, ev[0].elapsed_time(ev[steps]) / steps
 
 
+def time_calls(torch, fn, n: int, reps: int, warmup: int) -> float:
+    """ms a call of fn, n calls captured in one graph (a graph of a short call would time its own
+    launch)."""
+    def run():
+        for _ in range(n):
+            fn()
+    return time_graph(torch, run, reps, warmup)[1] / n
+
+
 def bench_c3(torch, steps, warmup, n_layers=16, contexts=(4096, 16384, 32768)):
     from embla_attn import ops
     max_s = max(contexts)
@@ -239,7 +248,7 @@ def bench_gemv(torch, reps=20):
 def bench_gemm(torch, reps=10):
     """The prefill projections either side of attention: C5's 2048-token chunk
     through q/k/v (3072 rows) and the o-projection (2048 rows, accumulating into an fp32
-    residual), K = 2048, 4-bit weights in MLX's layout; one graph. FLOPs 2 T O K."""
+    residual), K = 2048, 4-bit weights in MLX's layout; 4 pairs a graph. FLOPs 2 T O K."""
     from embla_attn import ops
     T, K = 2048, 2048
     mats = []
@@ -257,7 +266,7 @@ def bench_gemm(torch, reps=10):
     def run():
         ops.gemm_q4(mats[0][0], mats[0][1], x, qkv, T, 3072, K, ops.EPI_BF16)
         ops.gemm_q4(mats[1][0], mats[1][1], a, resid, T, 2048, K, ops.EPI_ADD)
-    wall, ms = time_graph(torch, run, reps, 2)
+    ms = time_calls(torch, run, 4, reps, 2)
     flops = 2.0 * T * K * (3072 + 2048)
     return dict(gflop=flops / 1e9, ms=ms, tflops=flops / (ms * 1e-3) / 1e12,
                 mfma_util=flops / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS)
@@ -374,8 +383,9 @@ def bench_c5(torch, reps=10):
     kring = torch.randn(n_kv * R * 128, generator=g, device="cuda").bfloat16()
     vring = torch.randn(n_kv * R * 128, generator=g, device="cuda").bfloat16()
     sflops = 4.0 * 128 * 16 * sum(min(W, p0 + t + 1) for t in range(T))
-    _, ms_sl = time_graph(torch, lambda: ops.prefill_sliding(q, kn, vn, kring, vring, T, p0, R, W, n_kv, out=out, ws=ws), reps, 2)
-    _, ms_sla = time_graph(torch, lambda: ops.prefill_ring(q, kring, vring, T, p0, R, W, n_kv, out=out, ws=ws), reps, 2)
+    ms_sl = time_calls(torch, lambda: ops.prefill_sliding(q, kn, vn, kring, vring, T, p0, R, W, n_kv, out=out, ws=ws),
+                       8, reps, 2)
+    ms_sla = time_calls(torch, lambda: ops.prefill_ring(q, kring, vring, T, p0, R, W, n_kv, out=out, ws=ws), 8, reps, 2)
     sliding = dict(window=W, ring=R, gflop=sflops / 1e9, ms_attention=ms_sla,
                    tflops_attention=sflops / (ms_sla * 1e-3) / 1e12, ms_fused=ms_sl,
                    tokens_per_s=T / (ms_sl * 1e-3))
@@ -390,8 +400,8 @@ def bench_c5(torch, reps=10):
     wi = torch.rand(T, 4, generator=g, device="cuda")
     ki = torch.randn(p0 + T, 64, generator=g, device="cuda").half()
     sws = ops.SparsePrefillWorkspace(T, p0)
-    _, ms_sp = time_graph(torch, lambda: ops.prefill_sparse(q, kn, vn, qi, wi, ki, kr, vr, T, p0, max_s, n_kv, sws,
-                                                            out=out), reps, 2)
+    ms_sp = time_calls(torch, lambda: ops.prefill_sparse(q, kn, vn, qi, wi, ki, kr, vr, T, p0, max_s, n_kv, sws,
+                                                         out=out), 2, reps, 2)
     att = 4.0 * 128 * 16 * T * 1152
     idxf = 4.0 * 128 * sum(p0 + t + 1 - 128 for t in range(T))
     sparse = dict(gflop_attention=att / 1e9, gflop_indexer=idxf / 1e9, ms_layer=ms_sp,
