@@ -34,7 +34,8 @@ def oracle_cfg(orc, c, weights=0):
 
 
 @pytest.mark.parametrize("S,max_s,seed", [(1024, 1024, 0), (1000, 1024, 5), (33, 64, 6), (1, 32, 7), (4096, 4096, 2),
-                                          (16384, 16384, 2), (32768, 32768, 2)])
+                                          (16384, 16384, 2), (32768, 32768, 2),
+                                          (131072, 131072, 9)])   # beyond the configs: a 128k context
 def test_decode_softmax_int8_matches_oracle(torch_gpu, orc, S, max_s, seed):
     say(f"decode softmax int8 S={S} max_s={max_s} seed={seed}")
     c = synth.decode_int8_case(seed=seed, S=S)
