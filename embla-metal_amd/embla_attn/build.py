@@ -14,6 +14,8 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG.parent / "csrc"
 INCLUDE = PKG.parent.parent / "include"
 LIB = PKG / "libembla_attn.so"
+HOST = PKG.parent / "host"
+HOST_LIB = PKG / "libembla_host.so"
 OBJ = PKG.parent / "_build"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -51,9 +53,23 @@ def build(verbose: bool = False) -> Path:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, LIB)
+    build_host()
     if verbose:
-        print(f"built {LIB} from {len(srcs)} sources")
+        print(f"built {LIB} from {len(srcs)} sources, and {HOST_LIB.name}")
     return LIB
+
+
+def build_host() -> Path:
+    """The C++ host side over the C ABI (host/*.cpp: the attention engine) as libembla_host.so,
+    linked to libembla_attn.so beside it."""
+    tmp = HOST_LIB.with_suffix(".so.tmp")
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", f"-I{INCLUDE}", f"-I{HOST}",
+           *map(str, sorted(HOST.glob("*.cpp"))), f"-L{PKG}", "-lembla_attn", "-Wl,-rpath,$ORIGIN", "-o", str(tmp)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"host library build failed:\n{r.stderr}")
+    os.replace(tmp, HOST_LIB)
+    return HOST_LIB
 
 
 if __name__ == "__main__":

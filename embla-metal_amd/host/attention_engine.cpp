@@ -1,0 +1,49 @@
+// Engine.encodeAttention (Sources/EmblaMetal/Engine.swift:743-832) over the C ABI; see the header.
+#include "attention_engine.hpp"
+
+namespace embla_host {
+
+namespace {
+const char* at(const void* base, size_t off) { return static_cast<const char*>(base) + off; }
+char* at(void* base, size_t off) { return static_cast<char*>(base) + off; }
+}  // namespace
+
+int AttentionEngine::encodeAttention(const Layer& L, int pos, hipStream_t st, bool kvOnly) const {
+    if (pos < 0 || pos >= maxContext_ || L.qkv.empty() || L.oproj.empty()) return EMBLA_ERR_INVALID;
+    // the q/k/v projection (Engine.swift:745-749)
+    int rc = embla_gemv_q4(b_.W, b_.hs, b_.qkv, L.qkv.data(), (int)L.qkv.size(), d, EMBLA_EPI_BF16, st);
+    if (rc) return rc;
+    // the k/v appends of the full layers (Engine.swift:754-764, 782-793)
+    const bool appends = L.kind != LayerKind::sliding && !L.kvJobs.empty();
+    if (appends) {
+        rc = embla_kv_append(b_.qkv, b_.cache, L.kvJobs.data(), (int)L.kvJobs.size(), pos, maxContext_, 1, st);
+        if (rc) return rc;
+    }
+    if (kvOnly) return EMBLA_OK;
+    const void* qg = at(b_.W, L.qGain);
+    const void* kg = at(b_.W, L.kGain);
+    if (L.kind == LayerKind::sliding) {   // Engine.swift:771-780 (writes the new k, v into its ring)
+        rc = embla_attn_sliding(b_.qkv, qg, kg, at(b_.cache, L.kOffset), at(b_.cache, L.vOffset), b_.o, pos, st);
+    } else {
+        // past topk + recent keys the selecting full layers score every key and select, and the
+        // sparse layers attend the selected rows only (Engine.swift:794-799)
+        const int keys = pos + 1;
+        const bool sel = selecting(pos), score = scoring(L, pos);
+        const int rows = sel && L.kind == LayerKind::sparse ? topk + recent : keys;
+        EmblaAttnParams ap{rows, 0, 0, maxContext_, pos, L.nGains, 0, 0};
+        if (L.kind == LayerKind::full) {
+            rc = embla_attn_full8(b_.qkv, qg, kg, at(b_.cache, L.kOffset), at(b_.cache, L.vOffset), b_.apart,
+                                  score ? b_.scores : nullptr, b_.counter, b_.o, &ap, st);
+            if (!rc && score) rc = embla_select_keys(b_.scores, b_.sel, keys, maxContext_, st);   // 819-827
+        } else {
+            rc = embla_attn_sparse8(b_.qkv, qg, kg, at(b_.cache, L.kOffset), at(b_.cache, L.vOffset), b_.apart,
+                                    sel ? b_.sel : nullptr, b_.counter, b_.o, &ap, st);
+        }
+    }
+    if (rc) return rc;
+    // the o-projection into the residual (Engine.swift:830)
+    return embla_gemv_q4(b_.W, b_.o, b_.x, L.oproj.data(), (int)L.oproj.size(), d,
+                         L.oFirst ? EMBLA_EPI_F32_BF : EMBLA_EPI_ADD, st);
+}
+
+}  // namespace embla_host

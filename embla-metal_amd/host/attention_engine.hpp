@@ -1,0 +1,85 @@
+// The attention sub-layer of a decode step, host side, over the library's C ABI.
+//
+// Mirrors Engine.encodeAttention (Sources/EmblaMetal/Engine.swift:743-832) and the attention parts
+// of Engine's state (layer kinds and cache offsets, Engine.swift:269-284, 441-485; the selection
+// constants, Engine.swift:7-27): for one layer at position pos, the 4-bit q/k/v projection, the
+// int8 append of the new k and v (full and sparse layers' KV jobs), the layer's attention (sliding
+// window; full ReLU² with the scores a selecting layer needs and the top-k selection; sparse
+// softmax over the selected rows of its block's full-layer cache), then the o-projection into the
+// fp32 residual x. Where the reference encodes Metal dispatches with barriers between them, this
+// issues stream-ordered calls on one HIP stream; the chunking is the library's.
+//
+// Ownership as the reference's: the caller owns every buffer (weights, cache, activations,
+// workspaces); the engine keeps offsets and launch choices only, allocates nothing and returns the
+// first failing call's error code (EMBLA_OK = 0).
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <set>
+#include <vector>
+
+#include "embla_attn.h"
+
+namespace embla_host {
+
+/// Layer kinds (Engine.swift's Layer.kind).
+enum class LayerKind { sliding, full, sparse };
+
+/// One attention layer's offsets (Engine.swift:441-485): gains and the cache regions as byte
+/// offsets; a sparse layer's regions are its block's full layer's (Engine.swift:461-462).
+struct Layer {
+    int index = 0;
+    LayerKind kind = LayerKind::full;
+    size_t qGain = 0, kGain = 0;        // byte offsets of the q and k gains in W (bf16 [128])
+    size_t kOffset = 0, vOffset = 0;    // byte offsets of the layer's K and V regions in the cache
+    int nGains = 2;                     // gains applied to q in the full and sparse layers
+    std::vector<EmblaKVJob> kvJobs;     // the k/v appends this layer owns (full layers)
+    std::vector<EmblaSeg> qkv, oproj;   // stacked 4-bit segments of the projections
+    bool oFirst = false;                // a block's first layer: the o-projection sets x (EPI 3)
+};
+
+/// Device buffers of a step (Engine.swift:252-267): W weights, the cache, hs the projection input
+/// (bf16 [2048]), qkv (bf16 [4096]), o (bf16 [16][128]), x the fp32 residual [2048], the split-K
+/// workspace (embla_workspace_bytes(maxContext, 16) bytes), scores fp32 [2][maxContext], sel u32
+/// [2][topk + recent] and the reference's counter words.
+struct Buffers {
+    void* W = nullptr;
+    void* cache = nullptr;
+    void* hs = nullptr;
+    void* qkv = nullptr;
+    void* o = nullptr;
+    float* x = nullptr;
+    float* apart = nullptr;
+    float* scores = nullptr;
+    uint32_t* sel = nullptr;
+    uint32_t* counter = nullptr;
+};
+
+class AttentionEngine {
+public:
+    static constexpr int d = 2048, headDim = 128, topk = 1024, recent = 128;   // Engine.swift:7-27
+
+    /// selects: the full layers that score every key for the sparse layers after them
+    /// (Embla.selects).
+    AttentionEngine(int maxContext, Buffers buffers, std::set<int> selects)
+        : maxContext_(maxContext), b_(buffers), selects_(std::move(selects)) {}
+
+    /// Engine.encodeAttention: the layer's attention sub-layer at position pos. With kvOnly, only
+    /// the q/k/v projection and the k/v append (a prompt token's last layer).
+    int encodeAttention(const Layer& L, int pos, hipStream_t stream, bool kvOnly = false) const;
+
+    /// Whether a layer at position pos selects (keys past topk + recent) and, for a full layer,
+    /// scores (Engine.swift:796-798).
+    bool selecting(int pos) const { return pos + 1 > topk + recent; }
+    bool scoring(const Layer& L, int pos) const {
+        return selecting(pos) && L.kind == LayerKind::full && selects_.count(L.index) > 0;
+    }
+
+private:
+    int maxContext_;
+    Buffers b_;
+    std::set<int> selects_;
+};
+
+}  // namespace embla_host

@@ -1,0 +1,24 @@
+"""The C++ attention engine (embla-metal_amd/host: Engine.encodeAttention's mirror over the C ABI)
+on a three-layer stack, every stage checked against the C oracle by tests/cpp's test binary."""
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from conftest import gpu_available
+from gpu_util import say
+
+pytestmark = pytest.mark.gpu
+
+BIN = Path(__file__).resolve().parent / "cpp" / "test_attention_engine"
+
+
+def test_attention_engine_stack():
+    if not gpu_available():
+        pytest.skip("no GPU")
+    assert BIN.exists(), f"{BIN} is not built: run __graft_entry__.build()"
+    say("C++ attention engine: sliding, full (scores + selection), sparse layers, positions 0 .. 1400")
+    r = subprocess.run([str(BIN)], capture_output=True, text=True, timeout=110)
+    print(r.stdout[-4000:])
+    assert r.returncode == 0, r.stdout[-4000:] + r.stderr[-2000:]
+    assert " 0 failed" in r.stdout
