@@ -207,6 +207,13 @@ int embla_q_prep(const void* qraw, const void* g1, const void* g2, int ng, int s
     return launch_q_prep(a, stream);
 }
 
+int embla_q_prep_b(const void* qkv, const void* g1, const void* g2, void* qn, int T, hipStream_t stream) {
+    if (!qkv || !g1 || !g2 || !qn || T <= 0) return EMBLA_ERR_INVALID;
+    QPrepArgs a{(const uint16_t*)qkv, (const uint16_t*)g1, (const uint16_t*)g2, 2, 4096, T, 16, (uint16_t*)qn, true};
+    a.head_major = true;
+    return launch_q_prep(a, stream);
+}
+
 int embla_attn_full8(const void* qraw, const void* g1, const void* g2, const void* kc, const void* vc,
                      float* part, float* scores, uint32_t* counter, void* o, const EmblaAttnParams* p,
                      hipStream_t stream) {

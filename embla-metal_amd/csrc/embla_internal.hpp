@@ -160,8 +160,9 @@ struct QPrepArgs {
     const uint16_t* g1;     // optional gains (bf16 [128])
     const uint16_t* g2;
     int ng, stride, T, n_q;
-    uint16_t* out;          // [T][n_q][128] fp16 or bf16
+    uint16_t* out;          // [T][n_q][128] fp16 or bf16; head-major [n_q][T][128] with head_major
     bool out_bf16;
+    bool head_major = false;
 };
 int launch_q_prep(const QPrepArgs& a, hipStream_t st);
 

@@ -98,7 +98,7 @@ __global__ __launch_bounds__(64) void q_prep_kernel(QPrepArgs a) {
     }
     x0 = bf2f(f2bf(x0 * g0));
     x1 = bf2f(f2bf(x1 * g1));
-    uint16_t* out = a.out + ((size_t)t * a.n_q + h) * HD + 2 * lane;
+    uint16_t* out = a.out + (a.head_major ? (size_t)h * a.T + t : (size_t)t * a.n_q + h) * HD + 2 * lane;
     out[0] = a.out_bf16 ? f2bf(x0) : f2h(x0);
     out[1] = a.out_bf16 ? f2bf(x1) : f2h(x1);
 }

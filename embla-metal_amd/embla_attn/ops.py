@@ -211,6 +211,14 @@ def prefill_full(q, k, v, kc, vc, T, p0, max_s, n_kv, out=None, ws=None, stream=
     return out
 
 
+def q_prep_b(qkv, g1, g2, T, out=None, stream=None):
+    """Reference-signature q_prep_b: qkv [T][4096] bf16 -> qn [16][T][128] bf16, head-major."""
+    if out is None:
+        out = torch.empty((16, T, 128), dtype=torch.bfloat16, device=qkv.device)
+    call("embla_q_prep_b", _p(qkv), _p(g1), _p(g2), _p(out), T, stream_handle(stream))
+    return out
+
+
 def relu2_prefill(qn, kc, vc, Tq, Tk, maxS, out=None, stream=None):
     """Reference-signature relu2_prefill_nax: qn [16][Tq][128] bf16 -> out [Tq][2048] bf16."""
     if out is None:

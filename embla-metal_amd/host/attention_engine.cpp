@@ -46,4 +46,40 @@ int AttentionEngine::encodeAttention(const Layer& L, int pos, hipStream_t st, bo
                          L.oFirst ? EMBLA_EPI_F32_BF : EMBLA_EPI_ADD, st);
 }
 
+int PrefillEncoder::encode(const Layer& L, int p0, int T, hipStream_t st, bool kvOnly) const {
+    constexpr int d = AttentionEngine::d;
+    if (p0 < 0 || T <= 0 || p0 + T > maxContext_ || L.qkv.empty() || L.oproj.empty()) return EMBLA_ERR_INVALID;
+    // the q/k/v GEMM, one call a segment (segmentGEMM, Prefill.swift:288)
+    unsigned start = 0;
+    for (const EmblaSeg& s : L.qkv) {
+        const unsigned long long wo[3] = {s.w, s.s, s.b};
+        const int rc = embla_gemm_q4(b_.W, wo, static_cast<const uint16_t*>(b_.hs) + s.x,
+                                     static_cast<uint16_t*>(b_.qkv) + s.y, T, (int)(s.end - start), d, d, 4096,
+                                     EMBLA_EPI_BF16, st);
+        if (rc) return rc;
+        start = s.end;
+    }
+    int rc = EMBLA_OK;
+    const void* qg = at(b_.W, L.qGain);
+    const void* kg = at(b_.W, L.kGain);
+    if (L.kind == LayerKind::sliding) {   // Prefill.swift:291-313
+        if (kvOnly) return EMBLA_OK;
+        rc = embla_attn_sliding8_b(b_.qkv, qg, kg, at(b_.cache, L.kOffset), at(b_.cache, L.vOffset), b_.o, p0, T, st);
+    } else {                              // Prefill.swift:315-340, 378-407
+        if (!L.kvJobs.empty()) {
+            rc = embla_kv_append(b_.qkv, b_.cache, L.kvJobs.data(), (int)L.kvJobs.size(), p0, maxContext_, T, st);
+            if (rc) return rc;
+        }
+        if (kvOnly) return EMBLA_OK;
+        rc = embla_q_prep_b(b_.qkv, qg, kg, b_.qn, T, st);
+        if (!rc) rc = embla_relu2_prefill(b_.qn, at(b_.cache, L.kOffset), at(b_.cache, L.vOffset), b_.o, T, p0 + T,
+                                          maxContext_, st);
+    }
+    if (rc) return rc;
+    // the o-projection GEMM into the residual (Prefill.swift:337-339)
+    const EmblaSeg& os = L.oproj[0];
+    const unsigned long long wo[3] = {os.w, os.s, os.b};
+    return embla_gemm_q4(b_.W, wo, b_.o, b_.x, T, d, d, d, d, L.oFirst ? EMBLA_EPI_F32_BF : EMBLA_EPI_ADD, st);
+}
+
 }  // namespace embla_host

@@ -82,4 +82,35 @@ private:
     std::set<int> selects_;
 };
 
+/// Device buffers of a prefill chunk of up to T tokens (Prefill.swift's own buffers): hs bf16
+/// [T][2048] the projection input, qkv bf16 [T][4096], qn bf16 [16][T][128] (the full layers'
+/// prepared queries), o bf16 [T][2048], x fp32 [T][2048]; W and cache as the decode's.
+struct PrefillBuffers {
+    void* W = nullptr;
+    void* cache = nullptr;
+    void* hs = nullptr;
+    void* qkv = nullptr;
+    void* qn = nullptr;
+    void* o = nullptr;
+    float* x = nullptr;
+};
+
+/// The attention parts of Prefill.encode (Sources/EmblaMetal/Prefill.swift:285-341, 378-407) for
+/// one layer and a chunk of T tokens at positions p0 .. p0 + T - 1: the q/k/v GEMM per segment;
+/// a sliding layer's ring append with its pre-ops and windowed attention (kv_sliding_b +
+/// attn_sliding8_b); a full or sparse layer's int8 append, q preparation and causal ReLU² attention
+/// with sink over every key (kv_append_b, q_prep_b, relu2_prefill_nax: the reference prefills its
+/// sparse layers with the full layers' kernel too); then the o-projection GEMM into x.
+class PrefillEncoder {
+public:
+    PrefillEncoder(int maxContext, PrefillBuffers buffers) : maxContext_(maxContext), b_(buffers) {}
+    /// With kvOnly, only the q/k/v GEMM and the k/v append (the prompt's last layer, Prefill.swift:287,
+    /// 323).
+    int encode(const Layer& L, int p0, int T, hipStream_t stream, bool kvOnly = false) const;
+
+private:
+    int maxContext_;
+    PrefillBuffers b_;
+};
+
 }  // namespace embla_host

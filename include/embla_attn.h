@@ -272,6 +272,11 @@ int embla_decode_int8_qraw(const void* qraw, const void* g1, const void* g2, int
 int embla_q_prep(const void* qraw, const void* g1, const void* g2, int ng, int stride, int T,
                  int n_q, void* out, int out_dtype, hipStream_t stream);
 
+/* Reference-signature q_prep_b (prefill.metal:406-426, bound at Prefill.swift:381-388): the full
+ * layer's queries of qkv bf16 [T][4096] normed with both gains and rounded to bf16, head-major
+ * qn [16][T][128], the input embla_relu2_prefill takes. */
+int embla_q_prep_b(const void* qkv, const void* g1, const void* g2, void* qn, int T, hipStream_t stream);
+
 /* ---------------------------------------------------------------- prefix-cache blocks
  * Save/restore of 128-position blocks between the layer caches and a stored block buffer, one
  * launch for every layer (Engine.fullSpans / windowSpans / copy, PrefixCache.swift:147-200). The

@@ -7,7 +7,11 @@
 // the selected 1024 + 128 rows once keys pass 1152). One token a step from position 0; at the
 // checked positions each layer's q/k/v projection, k/v append (bytes and scales, bit for bit),
 // attention output, scores and selection (bit for bit), ring row and residual are compared with
-// oracle/oracle.c. Exit status 0 when every check passes.
+// oracle/oracle.c. Then the prefill mirror (PrefillEncoder, Prefill.encode) against the decode
+// path (prefill row i equals decode at p0 + i, as the reference designs it, Prefill.swift:10-13):
+// a sliding and a full layer prefilled in two chunks (the second over the first's prefix) and
+// decoded token by token into separate caches give the same residuals and caches. Exit status 0
+// when every check passes.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -36,6 +40,7 @@ void orc_q4_matvec(const uint32_t* w, const uint16_t* s, const uint16_t* b, cons
 using embla_host::AttentionEngine;
 using embla_host::Layer;
 using embla_host::LayerKind;
+using embla_host::PrefillEncoder;
 
 namespace {
 
@@ -186,9 +191,7 @@ void read_ring(const std::vector<uint8_t>& cache, size_t off, bool is_v, std::ve
 
 }  // namespace
 
-int main() {
-    std::setvbuf(stdout, nullptr, _IOLBF, 0);   // line-buffered: a failing run still shows its last step
-    HIPCHECK(hipSetDevice(0));
+int run_decode_stack() {
     SplitMix64 g{20261201};
 
     // ---- weights: gains and 4-bit projections of three layers (Engine.swift:441-485)
@@ -406,6 +409,147 @@ int main() {
         }
     }
     HIPCHECK(hipStreamSynchronize(st));
+    return 0;
+}
+
+/// Prefill in two chunks against decode token by token: a sliding and a full layer, separate
+/// caches, the same weights and inputs.
+int run_prefill_vs_decode() {
+    SplitMix64 g{777};
+    constexpr int T1 = 160, T2 = 96, N = T1 + T2;
+    Blob W;
+    const size_t qg0 = add_gain(W, g), kg0 = add_gain(W, g), qg1 = add_gain(W, g), kg1 = add_gain(W, g);
+    const Mat q0 = add_mat(W, g, 2048), k0 = add_mat(W, g, 512), v0 = add_mat(W, g, 512), o0 = add_mat(W, g, 2048);
+    const Mat q1 = add_mat(W, g, 2048), k1 = add_mat(W, g, 256), v1 = add_mat(W, g, 256), o1 = add_mat(W, g, 2048);
+    const size_t ring_bytes = (size_t)4 * RING * HDIM * 2, region_bytes = (size_t)2 * MAXS * (HDIM + 4);
+    const size_t rk = 0, rv = ring_bytes, fk = 2 * ring_bytes, fv = fk + (region_bytes + 255) / 256 * 256;
+    const size_t cache_bytes = fv + region_bytes;
+    Layer L0, L1;
+    L0.index = 0; L0.kind = LayerKind::sliding; L0.qGain = qg0; L0.kGain = kg0; L0.kOffset = rk; L0.vOffset = rv;
+    L0.nGains = 1; L0.oFirst = true;
+    L0.qkv = {seg(q0, 2048, 0, 0), seg(k0, 2560, 0, 2048), seg(v0, 3072, 0, 2560)};
+    L0.oproj = {seg(o0, 2048, 0, 0)};
+    L1.index = 1; L1.kind = LayerKind::full; L1.qGain = qg1; L1.kGain = kg1; L1.kOffset = fk; L1.vOffset = fv;
+    L1.kvJobs = {EmblaKVJob{2048, 2560, (uint32_t)fk, (uint32_t)fv}};
+    L1.qkv = {seg(q1, 2048, 0, 0), seg(k1, 2304, 0, 2048), seg(v1, 2560, 0, 2560)};
+    L1.oproj = {seg(o1, 2048, 0, 0)};
+
+    std::vector<uint16_t> hs((size_t)N * D);
+    for (auto& v : hs) v = tobf((float)g.normal());
+    void *dW, *cacheA, *cacheB;
+    HIPCHECK(hipMalloc(&dW, W.bytes.size()));
+    HIPCHECK(hipMemcpy(dW, W.bytes.data(), W.bytes.size(), hipMemcpyHostToDevice));
+    HIPCHECK(hipMalloc(&cacheA, cache_bytes));
+    HIPCHECK(hipMalloc(&cacheB, cache_bytes));
+    HIPCHECK(hipMemset(cacheA, 0, cache_bytes));
+    HIPCHECK(hipMemset(cacheB, 0, cache_bytes));
+    hipStream_t st;
+    HIPCHECK(hipStreamCreate(&st));
+
+    // decode, token by token, into cache A
+    embla_host::Buffers B;
+    const size_t ws_bytes = embla_workspace_bytes(MAXS, 16);
+    B.W = dW; B.cache = cacheA;
+    HIPCHECK(hipMalloc(&B.hs, D * 2));
+    HIPCHECK(hipMalloc(&B.qkv, 4096 * 2));
+    HIPCHECK(hipMalloc(&B.o, D * 2));
+    HIPCHECK(hipMalloc((void**)&B.x, D * 4));
+    HIPCHECK(hipMalloc((void**)&B.apart, ws_bytes));
+    HIPCHECK(hipMemset(B.apart, 0, ws_bytes));
+    HIPCHECK(hipMalloc((void**)&B.scores, 2 * MAXS * 4));
+    HIPCHECK(hipMalloc((void**)&B.sel, 2 * NSEL * 4));
+    HIPCHECK(hipMalloc((void**)&B.counter, 64));
+    const AttentionEngine E(MAXS, B, {});
+    std::vector<float> xd((size_t)N * D);
+    for (int pos = 0; pos < N; pos++) {
+        HIPCHECK(hipMemcpy(B.hs, &hs[(size_t)pos * D], D * 2, hipMemcpyHostToDevice));
+        int rc = E.encodeAttention(L0, pos, st);
+        if (!rc) rc = E.encodeAttention(L1, pos, st);
+        if (rc) { std::printf("FAIL decode pos %d: %d\n", pos, rc); return 1; }
+        HIPCHECK(hipMemcpyAsync(&xd[(size_t)pos * D], B.x, D * 4, hipMemcpyDeviceToHost, st));
+    }
+    HIPCHECK(hipStreamSynchronize(st));
+
+    // prefill, two chunks, into cache B
+    embla_host::PrefillBuffers P;
+    P.W = dW; P.cache = cacheB;
+    HIPCHECK(hipMalloc(&P.hs, (size_t)T1 * D * 2));
+    HIPCHECK(hipMalloc(&P.qkv, (size_t)T1 * 4096 * 2));
+    HIPCHECK(hipMalloc(&P.qn, (size_t)16 * T1 * HDIM * 2));
+    HIPCHECK(hipMalloc(&P.o, (size_t)T1 * D * 2));
+    HIPCHECK(hipMalloc((void**)&P.x, (size_t)T1 * D * 4));
+    const PrefillEncoder PE(MAXS, P);
+    std::vector<float> xp((size_t)N * D);
+    const int chunks[2][2] = {{0, T1}, {T1, T2}};
+    for (const auto& c : chunks) {
+        const int p0 = c[0], T = c[1];
+        std::printf("prefill chunk p0 %d T %d\n", p0, T);
+        HIPCHECK(hipMemcpy(P.hs, &hs[(size_t)p0 * D], (size_t)T * D * 2, hipMemcpyHostToDevice));
+        int rc = PE.encode(L0, p0, T, st);
+        if (!rc) rc = PE.encode(L1, p0, T, st);
+        if (rc) { std::printf("FAIL prefill p0 %d: %d\n", p0, rc); return 1; }
+        HIPCHECK(hipMemcpyAsync(&xp[(size_t)p0 * D], P.x, (size_t)T * D * 4, hipMemcpyDeviceToHost, st));
+        HIPCHECK(hipStreamSynchronize(st));
+    }
+    // the residuals, token by token (q/k/v by GEMM or GEMV round to bf16 apart by a step at most,
+    // and an int8 key or value can move by one: a few parts in a hundred, against O(1) for a
+    // wrong position, window or row)
+    float xmax = 0.0f;
+    for (float v : xd) xmax = std::fmax(xmax, std::fabs(v));
+    int bad_tok = -1;
+    float worst = 0.0f;
+    for (int t = 0; t < N; t++) {
+        float w;
+        if (!close(&xp[(size_t)t * D], &xd[(size_t)t * D], D, 0.03f * xmax, 0.03f, &w) && bad_tok < 0) bad_tok = t;
+        worst = std::fmax(worst, w);
+    }
+    char msg[160];
+    std::snprintf(msg, sizeof msg, "prefill residuals = decode residuals (worst |err| %.3g of max %.3g, first bad token %d)",
+                  worst, xmax, bad_tok);
+    std::printf("%s\n", msg);
+    expect(bad_tok < 0, msg, N - 1, -1);
+    // the caches: the full layer's int8 rows dequantised, the sliding ring's rows
+    std::vector<uint8_t> ca(cache_bytes), cb(cache_bytes);
+    HIPCHECK(hipMemcpy(ca.data(), cacheA, cache_bytes, hipMemcpyDeviceToHost));
+    HIPCHECK(hipMemcpy(cb.data(), cacheB, cache_bytes, hipMemcpyDeviceToHost));
+    bool cache_ok = true;
+    for (int kind = 0; kind < 2; kind++) {
+        std::vector<int8_t> ra, rb;
+        std::vector<float> sa, sb;
+        read_int8_region(ca, kind ? fv : fk, kind == 1, 2, ra, sa);
+        read_int8_region(cb, kind ? fv : fk, kind == 1, 2, rb, sb);
+        for (int h = 0; h < 2; h++)
+            for (int j = 0; j < N; j++) {
+                const size_t r = (size_t)h * MAXS + j;
+                float amax = 0.0f;
+                for (int d = 0; d < HDIM; d++) amax = std::fmax(amax, std::fabs(ra[r * HDIM + d] * sa[r]));
+                for (int d = 0; d < HDIM; d++)
+                    if (std::fabs(ra[r * HDIM + d] * sa[r] - rb[r * HDIM + d] * sb[r]) > 0.03f * amax) cache_ok = false;
+            }
+    }
+    expect(cache_ok, "full layer's int8 cache rows: prefill = decode (dequantised, within 3% of the row's absmax)", N - 1, 1);
+    std::vector<float> ka, kb2;
+    std::vector<uint16_t> kab, kbb;
+    bool ring_ok = true;
+    for (int kind = 0; kind < 2; kind++) {
+        read_ring(ca, kind ? rv : rk, kind == 1, ka, kab);
+        read_ring(cb, kind ? rv : rk, kind == 1, kb2, kbb);
+        for (int h = 0; h < 4; h++)
+            for (int j = 0; j < N; j++)
+                for (int d = 0; d < HDIM; d++) {
+                    const size_t i = ((size_t)h * RING + j) * HDIM + d;
+                    if (std::fabs(ka[i] - kb2[i]) > 0.03f * (std::fabs(ka[i]) + 1.0f)) ring_ok = false;
+                }
+    }
+    expect(ring_ok, "sliding ring rows: prefill = decode", N - 1, 0);
+    return 0;
+}
+
+int main() {
+    std::setvbuf(stdout, nullptr, _IOLBF, 0);   // line-buffered: a failing run still shows its last step
+    HIPCHECK(hipSetDevice(0));
+    if (run_decode_stack()) return 1;
+    if (run_prefill_vs_decode()) return 1;
     std::printf("%d checks, %d failed\n", checks, failures);
     return failures ? 1 : 0;
 }

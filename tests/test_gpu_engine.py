@@ -1,5 +1,6 @@
-"""The C++ attention engine (embla-metal_amd/host: Engine.encodeAttention's mirror over the C ABI)
-on a three-layer stack, every stage checked against the C oracle by tests/cpp's test binary."""
+"""The C++ host side (embla-metal_amd/host: Engine.encodeAttention and Prefill.encode mirrored over
+the C ABI): a three-layer decode stack checked stage by stage against the C oracle, and prefill
+against token-by-token decode, by tests/cpp's test binary."""
 import subprocess
 from pathlib import Path
 

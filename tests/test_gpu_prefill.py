@@ -112,3 +112,23 @@ def test_relu2_prefill_reference_mode(torch_gpu, orc):
     got = bf16_host(o).reshape(Tq, 16, 128)
     ref = orc.prefill_int8(synth.bf16_val(qn).transpose(1, 0, 2), K, ks, V, vs, Tk - Tq, weights=1)
     assert_close(got, ref, what="relu2 prefill")
+
+
+def test_q_prep_b_head_major(torch_gpu, orc):
+    """q_prep_b: qkv [T][4096] bf16 -> qn [16][T][128], normed with both gains, bf16 (one bf16 step:
+    the GPU's sum of squares runs in another order)."""
+    from embla_attn import ops
+    torch = torch_gpu
+    T = 37
+    g = synth.SplitMix64(55)
+    qkv = synth.bf16_bits(g.normal(T * 4096) * 2).reshape(T, 4096)
+    g1 = synth.bf16_bits(g.normal(128) * 0.2)
+    g2 = synth.bf16_bits(g.normal(128) * 0.2)
+    qn = ops.q_prep_b(dev(qkv, torch.bfloat16), dev(g1, torch.bfloat16), dev(g2, torch.bfloat16), T)
+    torch.cuda.synchronize()
+    got = bf16_host(qn)
+    assert got.shape == (16, T, 128)
+    for t in range(T):
+        for h in range(16):
+            want = orc.head_norm(synth.bf16_val(qkv[t, h * 128:(h + 1) * 128]), synth.bf16_val(g1), synth.bf16_val(g2), 2)
+            assert (np.abs(got[h, t] - want) <= np.abs(want) * 2 ** -7 + 1e-30).all(), (t, h)
