@@ -46,6 +46,41 @@ int AttentionEngine::encodeAttention(const Layer& L, int pos, hipStream_t st, bo
                          L.oFirst ? EMBLA_EPI_F32_BF : EMBLA_EPI_ADD, st);
 }
 
+int AttentionEngine::copyFullBlock(const std::vector<const Layer*>& full, int p0, void* stored, bool save,
+                                   hipStream_t st) const {
+    std::vector<unsigned long long> regions;
+    for (const Layer* L : full) {
+        if (!L || L->kind != LayerKind::full) return EMBLA_ERR_INVALID;
+        regions.push_back(L->kOffset);
+        regions.push_back(L->vOffset);
+    }
+    if (regions.empty()) return EMBLA_ERR_INVALID;
+    return embla_kv_block_copy(b_.cache, regions.data(), (int)full.size(), p0, maxContext_, 2, EMBLA_F32, stored,
+                               save ? 1 : 0, st);
+}
+
+int AttentionEngine::copyWindowBlock(const std::vector<const Layer*>& sliding, int p0, void* stored, bool save,
+                                     hipStream_t st) const {
+    std::vector<unsigned long long> regions;
+    for (const Layer* L : sliding) {
+        if (!L || L->kind != LayerKind::sliding) return EMBLA_ERR_INVALID;
+        regions.push_back(L->kOffset);
+        regions.push_back(L->vOffset);
+    }
+    if (regions.empty()) return EMBLA_ERR_INVALID;
+    return embla_ring_block_copy(b_.cache, regions.data(), (int)sliding.size(), p0, 4096, 4, stored, save ? 1 : 0, st);
+}
+
+int AttentionEngine::encodeToken(const float* logits, int vocab, uint32_t* tokens, uint32_t* greedy, int pos,
+                                 int promptEnd, const Sampling& s, void* scratch, size_t scratchBytes,
+                                 hipStream_t st) const {
+    if (s.isGreedy())
+        return embla_argmax(logits, tokens, vocab, greedy, pos, promptEnd, scratch, scratchBytes, st);
+    const float top_p = s.topP < 1.0f ? s.topP : 1.0f;   // Sampling.init clamps it to [0, 1]
+    return embla_sample(logits, tokens, vocab, greedy, pos, promptEnd, 1.0f / s.temperature, top_p, s.seed, scratch,
+                        scratchBytes, st);
+}
+
 int PrefillEncoder::encode(const Layer& L, int p0, int T, hipStream_t st, bool kvOnly) const {
     constexpr int d = AttentionEngine::d;
     if (p0 < 0 || T <= 0 || p0 + T > maxContext_ || L.qkv.empty() || L.oproj.empty()) return EMBLA_ERR_INVALID;

@@ -69,6 +69,29 @@ public:
     /// the q/k/v projection and the k/v append (a prompt token's last layer).
     int encodeAttention(const Layer& L, int pos, hipStream_t stream, bool kvOnly = false) const;
 
+    /// The full layers' int8 keys and values of positions p0 ..< p0 + 128 (p0 % 128 == 0) to or
+    /// from a stored block (Engine.fullSpans + copy, PrefixCache.swift:153-200; one launch for every
+    /// layer): stored holds embla_kv_block_bytes(layers, 2, EMBLA_F32) bytes in fullSpans' order.
+    int copyFullBlock(const std::vector<const Layer*>& full, int p0, void* stored, bool save, hipStream_t stream) const;
+    /// The sliding layers' ring slots of positions p0 ..< p0 + 128 (Engine.windowSpans' K/V spans):
+    /// stored holds embla_ring_block_bytes(layers, 4) bytes.
+    int copyWindowBlock(const std::vector<const Layer*>& sliding, int p0, void* stored, bool save,
+                        hipStream_t stream) const;
+
+    /// How a step picks its token (Engine.swift:1306-1325): greedy when temperature <= 0 or
+    /// top-p <= 0.
+    struct Sampling {
+        float temperature = 0.0f, topP = 1.0f;
+        uint32_t seed = 0;
+        bool isGreedy() const { return temperature <= 0.0f || topP <= 0.0f; }
+    };
+    /// The step's token from the lm-head's fp32 logits (Engine.swift:972-987): the argmax or the
+    /// top-p draw, written to greedy[pos], to tokens[pos + 1] past the prompt, and last to the
+    /// polled word greedy[-1] (greedy points one word into its buffer). scratch:
+    /// embla_sample_workspace_bytes(vocab) bytes.
+    int encodeToken(const float* logits, int vocab, uint32_t* tokens, uint32_t* greedy, int pos, int promptEnd,
+                    const Sampling& sampling, void* scratch, size_t scratchBytes, hipStream_t stream) const;
+
     /// Whether a layer at position pos selects (keys past topk + recent) and, for a full layer,
     /// scores (Engine.swift:796-798).
     bool selecting(int pos) const { return pos + 1 > topk + recent; }

@@ -7,7 +7,7 @@
 // the selected 1024 + 128 rows once keys pass 1152). One token a step from position 0; at the
 // checked positions each layer's q/k/v projection, k/v append (bytes and scales, bit for bit),
 // attention output, scores and selection (bit for bit), ring row and residual are compared with
-// oracle/oracle.c. Then the prefill mirror (PrefillEncoder, Prefill.encode) against the decode
+// oracle/oracle.c; then the engine's prefix-block save/restore and token step. Then the prefill mirror (PrefillEncoder, Prefill.encode) against the decode
 // path (prefill row i equals decode at p0 + i, as the reference designs it, Prefill.swift:10-13):
 // a sliding and a full layer prefilled in two chunks (the second over the first's prefix) and
 // decoded token by token into separate caches give the same residuals and caches. Exit status 0
@@ -35,6 +35,8 @@ void orc_decode_rows(const float* q, const float* K, const float* V, int S_cache
 void orc_select_keys(const float* sc, int S, int topk, int recent, uint32_t* out);
 void orc_q4_matvec(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint16_t* x, int O, int K,
                    int epi, float* y);
+uint32_t orc_argmax(const float* logits, int V);
+uint32_t orc_sample(const float* logits, int V, int pos, float inv_t, float top_p, uint32_t seed, int* fragile);
 }
 
 using embla_host::AttentionEngine;
@@ -409,6 +411,95 @@ int run_decode_stack() {
         }
     }
     HIPCHECK(hipStreamSynchronize(st));
+
+    // ---- prefix-cache blocks through the engine (fullSpans / windowSpans + copy): positions
+    // 1280 ..< 1408 saved from this cache and restored into a zeroed one come back exactly there
+    {
+        const int p0 = 1280;
+        void *sf, *sr, *cache2;
+        const size_t fb = embla_kv_block_bytes(1, 2, EMBLA_F32), rb = embla_ring_block_bytes(1, 4);
+        HIPCHECK(hipMalloc(&sf, fb));
+        HIPCHECK(hipMalloc(&sr, rb));
+        HIPCHECK(hipMalloc(&cache2, cache_bytes));
+        HIPCHECK(hipMemset(cache2, 0, cache_bytes));
+        int rc = E.copyFullBlock({&L1}, p0, sf, true, st);
+        if (!rc) rc = E.copyWindowBlock({&L0}, p0, sr, true, st);
+        embla_host::Buffers B2 = B;
+        B2.cache = cache2;
+        const AttentionEngine E2(MAXS, B2, {1});
+        if (!rc) rc = E2.copyFullBlock({&L1}, p0, sf, false, st);
+        if (!rc) rc = E2.copyWindowBlock({&L0}, p0, sr, false, st);
+        HIPCHECK(hipStreamSynchronize(st));
+        expect(rc == EMBLA_OK, "block copies returned OK", p0, -1);
+        std::vector<uint8_t> c1(cache_bytes), c2(cache_bytes);
+        HIPCHECK(hipMemcpy(c1.data(), B.cache, cache_bytes, hipMemcpyDeviceToHost));
+        HIPCHECK(hipMemcpy(c2.data(), cache2, cache_bytes, hipMemcpyDeviceToHost));
+        bool ok = true;
+        for (int kind = 0; kind < 2; kind++) {
+            std::vector<int8_t> r1, r2;
+            std::vector<float> s1, s2;
+            read_int8_region(c1, kind ? fv : fk, kind == 1, 2, r1, s1);
+            read_int8_region(c2, kind ? fv : fk, kind == 1, 2, r2, s2);
+            for (int h = 0; h < 2; h++)
+                for (int j = 0; j < MAXS; j++) {
+                    const size_t r = (size_t)h * MAXS + j;
+                    const bool in = j >= p0 && j < p0 + 128;
+                    for (int d = 0; d < HDIM; d++) ok = ok && r2[r * HDIM + d] == (in ? r1[r * HDIM + d] : 0);
+                    ok = ok && s2[r] == (in ? s1[r] : 0.0f);
+                }
+            std::vector<float> f1, f2;
+            std::vector<uint16_t> b1, b2;
+            read_ring(c1, kind ? rv : rk, kind == 1, f1, b1);
+            read_ring(c2, kind ? rv : rk, kind == 1, f2, b2);
+            for (int h = 0; h < 4; h++)
+                for (int j = 0; j < RING; j++) {
+                    const bool in = j >= p0 % RING && j < p0 % RING + 128;
+                    for (int d = 0; d < HDIM; d++) {
+                        const size_t i = ((size_t)h * RING + j) * HDIM + d;
+                        ok = ok && b2[i] == (in ? b1[i] : 0);
+                    }
+                }
+        }
+        expect(ok, "prefix block save + restore: the block's rows, scales and ring slots, nothing else", p0, -1);
+        std::printf("prefix block save/restore checked\n");
+    }
+
+    // ---- the step's token (Engine.swift:972-987): greedy, then a top-p draw
+    {
+        const int V = 65536, pos = 10, prompt = 5;
+        std::vector<float> lg(V);
+        for (auto& v : lg) v = (float)(3.0 * g.normal());
+        float* dl;
+        uint32_t *tokens, *greedy;
+        void* scratch;
+        const size_t sb = embla_sample_workspace_bytes(V);
+        HIPCHECK(hipMalloc((void**)&dl, V * 4));
+        HIPCHECK(hipMemcpy(dl, lg.data(), V * 4, hipMemcpyHostToDevice));
+        HIPCHECK(hipMalloc((void**)&tokens, 64 * 4));
+        HIPCHECK(hipMalloc((void**)&greedy, 64 * 4));
+        HIPCHECK(hipMemset(tokens, 0xFF, 64 * 4));
+        HIPCHECK(hipMemset(greedy, 0, 64 * 4));
+        HIPCHECK(hipMalloc(&scratch, sb));
+        AttentionEngine::Sampling greedy_s;
+        int rc = E.encodeToken(dl, V, tokens, greedy + 1, pos, prompt, greedy_s, scratch, sb, st);
+        AttentionEngine::Sampling draw_s;
+        draw_s.temperature = 0.8f;
+        draw_s.topP = 0.9f;
+        draw_s.seed = 1234;
+        if (!rc) rc = E.encodeToken(dl, V, tokens, greedy + 1, pos + 1, prompt, draw_s, scratch, sb, st);
+        HIPCHECK(hipStreamSynchronize(st));
+        std::vector<uint32_t> gw(64), tw(64);
+        HIPCHECK(hipMemcpy(gw.data(), greedy, 64 * 4, hipMemcpyDeviceToHost));
+        HIPCHECK(hipMemcpy(tw.data(), tokens, 64 * 4, hipMemcpyDeviceToHost));
+        const uint32_t want_g = orc_argmax(lg.data(), V);
+        int fragile = 0;
+        const uint32_t want_d = orc_sample(lg.data(), V, pos + 1, 1.0f / 0.8f, 0.9f, 1234, &fragile);
+        expect(rc == EMBLA_OK, "encodeToken returned OK", pos, -1);
+        expect(gw[1 + pos] == want_g && tw[pos + 1] == want_g, "greedy token (greedy[pos], tokens[pos + 1])", pos, -1);
+        expect(fragile || (gw[1 + pos + 1] == want_d && tw[pos + 2] == want_d), "top-p draw against the oracle", pos + 1, -1);
+        expect(gw[0] == ((uint32_t)(pos + 2) << 16 | gw[1 + pos + 1]), "the polled word: (pos + 1) << 16 | token", pos + 1, -1);
+        std::printf("token step checked (greedy %u, draw %u%s)\n", want_g, want_d, fragile ? ", draw fragile" : "");
+    }
     return 0;
 }
 
