@@ -7,8 +7,9 @@
 // the selected 1024 + 128 rows once keys pass 1152). One token a step from position 0; at the
 // checked positions each layer's q/k/v projection, k/v append (bytes and scales, bit for bit),
 // attention output, scores and selection (bit for bit), ring row and residual are compared with
-// oracle/oracle.c; then the engine's prefix-block save/restore and token step. Then the prefill mirror (PrefillEncoder, Prefill.encode) against the decode
-// path (prefill row i equals decode at p0 + i, as the reference designs it, Prefill.swift:10-13):
+// oracle/oracle.c; then the engine's prefix-block save/restore and token step. Then the prefill
+// mirror (PrefillEncoder, Prefill.encode) against the decode path (prefill row i equals decode at
+// p0 + i, as the reference designs it, Prefill.swift:10-13):
 // a sliding and a full layer prefilled in two chunks (the second over the first's prefix) and
 // decoded token by token into separate caches give the same residuals and caches. Exit status 0
 // when every check passes.
