@@ -52,7 +52,8 @@ def upload_prefix(c, max_s):
 
 @pytest.mark.parametrize("p0,T,window,split", [(1000, 96, 0, False), (0, 64, 0, False), (517, 70, 0, False),
                                                 (300, 100, 40, False), (40, 33, 0, False), (3000, 70, 0, True),
-                                                (2100, 64, 0, True), (2500, 40, 600, True)])
+                                                (2100, 64, 0, True), (2500, 40, 600, True),
+                                                (777, 1, 0, False), (2500, 1, 0, True)])   # one token: a decode
 def test_prefill_full_small(torch_gpu, orc, p0, T, window, split):
     """Fused quantise-and-append + causal softmax prefill vs the oracle on every row."""
     from embla_attn import ops

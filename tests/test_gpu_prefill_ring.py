@@ -35,7 +35,7 @@ def check_rows(orc, got, Q, Kf, Vf, p0, W, rows, what, atol=2e-3):
 
 @pytest.mark.parametrize("R,W,p0,T,split", [(256, 96, 700, 100, False), (8192, 1024, 0, 70, False),
                                              (8192, 1024, 1500, 131, False), (512, 200, 1000, 33, False),
-                                             (8192, 4000, 5000, 64, True)])
+                                             (8192, 4000, 5000, 64, True), (8192, 1024, 2000, 1, False)])
 def test_prefill_sliding_bf16(torch_gpu, orc, R, W, p0, T, split):
     from embla_attn import ops
     torch = torch_gpu

@@ -74,7 +74,7 @@ def check_rows(orc, c, got, idx, rows, cache):
         assert_close(got[t], ref[0], what=f"row {t}")
 
 
-@pytest.mark.parametrize("p0,T", [(1500, 64), (1100, 100), (3000, 40)])
+@pytest.mark.parametrize("p0,T", [(1500, 64), (1100, 100), (3000, 40), (1300, 1), (1300, 2)])
 def test_prefill_sparse_small(torch_gpu, orc, p0, T):
     say(f"prefill sparse p0={p0} T={T}")
     c = synth.sparse_prefill_case(seed=4, p0=p0, T=T)
