@@ -272,12 +272,13 @@ def bench_gemm(torch, reps=10):
                 mfma_util=flops / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS)
 
 
-def bench_step(torch, regions, L=32768, reps=20):
+def bench_step(torch, regions, L=32768, reps=20, fused=True):
     """The whole attention sub-layer decode step of one token over C3's 16-layer
     stack at context L, captured as one graph: per layer the 4-bit q/k/v projection, the int8 append
     of the new k and v at position L - 1, the split-K decode over L positions with the q head norm
-    inside its kernel (bf16 out) and the 4-bit o-projection into the fp32 residual. Algorithmic bytes a layer: the
-    cache as in C3 plus the weights."""
+    inside its kernel (bf16 out) and the 4-bit o-projection into the fp32 residual. fused: the
+    append inside the decode launch (embla_decode_step_int8, 4 kernels a layer), else its own
+    launch (5). Algorithmic bytes a layer: the cache as in C3 plus the weights."""
     from embla_attn import ops
     n_layers, D, n_q, n_kv, max_s = len(regions), 2048, 16, 4, 32768
 
@@ -307,13 +308,16 @@ def bench_step(torch, regions, L=32768, reps=20):
         for l in range(n_layers):
             kc, vc = regions[l]
             ops.gemv_q4(W, x, qkv, [segs[l][0]], D, ops.EPI_BF16)
-            ops.kv_quant_append(qkv[2048:2560], qkv[2560:3072], 1, L - 1, n_kv, kc, vc, max_s)
-            ops.decode_int8_qraw(qkv[:2048], kc, vc, L, max_s, n_kv, ws=ws, out=o)
+            if fused:
+                ops.decode_step_int8(qkv, 0, 2048, 2560, kc, vc, L - 1, max_s, n_q, n_kv, ws, out=o)
+            else:
+                ops.kv_quant_append(qkv[2048:2560], qkv[2560:3072], 1, L - 1, n_kv, kc, vc, max_s)
+                ops.decode_int8_qraw(qkv[:2048], kc, vc, L, max_s, n_kv, ws=ws, out=o)
             ops.gemv_q4(W, o, resid, [segs[l][1]], D, ops.EPI_ADD)
     wall, ms = time_graph(torch, run, reps, 3)
     us = ms * 1000 / n_layers
     nbytes = layer_bytes(L) + lw
-    return dict(context=L, layers=n_layers, kernels_per_layer=5, bytes_layer=nbytes, us_per_layer=us,
+    return dict(context=L, layers=n_layers, kernels_per_layer=4 if fused else 5, bytes_layer=nbytes, us_per_layer=us,
                 gbs=nbytes / (us * 1e-6) / 1e9, frac_hbm=nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS)
 
 
@@ -502,6 +506,7 @@ def main():
         return
     res, case, out0, regions, main_us = bench_c3(torch, args.steps, args.warmup)
     step = bench_step(torch, regions)
+    step["us_per_layer_append_own_launch"] = bench_step(torch, regions, fused=False)["us_per_layer"]
     sampling = bench_sampling(torch)
     c2 = bench_c2(torch)
     c4 = bench_c4(torch)

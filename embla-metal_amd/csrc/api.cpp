@@ -198,6 +198,45 @@ int embla_decode_int8_qraw(const void* qraw, const void* g1, const void* g2, int
     return launch_full_decode(a, stream);
 }
 
+int embla_decode_step_int8(const void* qkv, int q_off, int k_off, int v_off, const void* g1, const void* g2, int ng,
+                           void* kc, void* vc, void* o, int pos, int max_s, int n_q, int n_kv, int scale_dtype,
+                           int norm_k, int out_dtype, int chunk, void* ws, size_t ws_bytes, hipStream_t stream) {
+    if (!qkv || !kc || !vc || !o || ng < 0 || ng > 2 || (ng >= 1 && !g1) || (ng >= 2 && !g2)) return EMBLA_ERR_INVALID;
+    if (q_off < 0 || k_off < 0 || v_off < 0 || (q_off | k_off | v_off) & 1) return EMBLA_ERR_INVALID;
+    if (pos < 0 || max_s <= 0 || max_s % 32 || pos >= max_s) return EMBLA_ERR_INVALID;
+    if (n_kv <= 0 || n_q % n_kv || n_kv > kMaxKV) return EMBLA_ERR_INVALID;
+    if (!valid_scale(scale_dtype) || !valid_act(out_dtype) || chunk < 0 || chunk % 32) return EMBLA_ERR_INVALID;
+    const int ch = pos == 0 ? 32 : chunk ? chunk : decode_chunk(pos, n_kv);
+    const int C = (pos + ch - 1) / ch;   // chunks over the cached keys 0 .. pos - 1
+    if (C + 1 > kMaxChunks) return EMBLA_ERR_INVALID;
+    if (!ws || ws_bytes < embla_workspace_bytes(max_s, n_q) || (size_t)(C + 1) * n_q * kPartStride * 4 > part_bytes(max_s, n_q))
+        return EMBLA_ERR_WORKSPACE;
+    Workspace w = carve(ws, max_s, n_q);
+    const uint16_t* base = (const uint16_t*)qkv;
+    FullDecodeArgs a;
+    a.q = base + q_off;
+    a.g1 = (const uint16_t*)g1;
+    a.g2 = (const uint16_t*)g2;
+    a.ng = ng;
+    a.kc = (const int8_t*)kc;
+    a.vc = (const int8_t*)vc;
+    a.part = w.part;
+    a.scores = nullptr;
+    a.o = (uint16_t*)o;
+    a.S = pos; a.CH = ch; a.C = C; a.max_s = max_s; a.n_q = n_q; a.n_kv = n_kv;
+    a.relu2 = false;
+    a.scale32 = scale_dtype == EMBLA_F32;
+    a.out_bf16 = out_dtype == EMBLA_BF16;
+    a.append = true;
+    a.knew = base + k_off;
+    a.vnew = base + v_off;
+    a.kcw = (int8_t*)kc;
+    a.vcw = (int8_t*)vc;
+    a.pos = pos;
+    a.norm_k = norm_k ? 1 : 0;
+    return launch_full_decode(a, stream);
+}
+
 int embla_q_prep(const void* qraw, const void* g1, const void* g2, int ng, int stride, int T,
                  int n_q, void* out, int out_dtype, hipStream_t stream) {
     if (!qraw || !out || T <= 0 || n_q <= 0 || ng < 0 || ng > 2 || stride < n_q * 128) return EMBLA_ERR_INVALID;

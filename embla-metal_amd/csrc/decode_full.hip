@@ -23,6 +23,7 @@
 // needs no counters, so the path is graph-capturable and leaves no state behind.
 #include "common.hpp"
 #include "embla_internal.hpp"
+#include "kv_row.hpp"
 
 namespace embla {
 
@@ -60,15 +61,75 @@ __device__ __forceinline__ void scales8(const u4_t* r, float* out) {
 
 constexpr int DW = 8;            // waves a workgroup: one 32-key tile each a round
 
-template <int GQ, bool RELU2, bool SCALE32, bool OBF, bool SCORES, bool QR>
+/// The decode step's own append (workgroup C of each kv head): waves 0 and 1 quantise the new
+/// token's k and v rows exactly as kv_quant_kernel does and store them at position pos; then wave
+/// h < GQ adds the new key as one more partial of query head kvh GQ + h: its score in the log2
+/// domain as the maximum, weight 1, and vs v WSCALE as the sums, the chunk partials' conventions.
+template <int GQ, bool SCALE32, bool QR>
+__device__ __forceinline__ void decode_append(const DecodeAppend& app, const uint16_t* __restrict__ q,
+                                              float* __restrict__ part, int C, int max_s, int n_kv, int kvh,
+                                              float sc, const uint16_t* __restrict__ g1,
+                                              const uint16_t* __restrict__ g2, int ng) {
+    __shared__ int8_t nk[HD], nv[HD];
+    __shared__ float nsc[2];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    if (w < 2) {
+        const bool is_v = w == 1;
+        const uint32_t raw = *(const uint32_t*)((is_v ? app.v : app.k) + (size_t)kvh * HD + 2 * lane);
+        int q0, q1;
+        const float am = quant_pair(bf2f(raw & 0xFFFF), bf2f(raw >> 16), !is_v && app.norm_k, true, q0, q1);
+        store_pair8(is_v ? app.vc : app.kc, n_kv, max_s, kvh, app.pos, is_v, false, SCALE32, q0, q1, am, lane);
+        int8_t* dst = is_v ? nv : nk;
+        dst[2 * lane] = (int8_t)q0;
+        dst[2 * lane + 1] = (int8_t)q1;
+        if (lane == 0) nsc[w] = SCALE32 ? am / 127.0f : h2f(f2h(am / 127.0f));   // the stored scale
+    }
+    __syncthreads();
+    if (w >= GQ) return;
+    const int hq = kvh * GQ + w;
+    const uint32_t qr = *(const uint32_t*)(q + (size_t)hq * HD + 2 * lane);
+    float x0, x1;
+    if constexpr (QR) {   // the head norm the chunk workgroups apply
+        x0 = bf2f(qr & 0xFFFF);
+        x1 = bf2f(qr >> 16);
+        const float rf = rms_factor(x0, x1);
+        float g0 = rf, gg1 = rf;
+        if (ng >= 1) { g0 = g0 * (1.0f + bf2f(g1[2 * lane])); gg1 = gg1 * (1.0f + bf2f(g1[2 * lane + 1])); }
+        if (ng >= 2) { g0 = g0 * (1.0f + bf2f(g2[2 * lane])); gg1 = gg1 * (1.0f + bf2f(g2[2 * lane + 1])); }
+        x0 = bf2f(f2bf(x0 * g0));
+        x1 = bf2f(f2bf(x1 * gg1));
+    } else {
+        x0 = h2f((uint16_t)(qr & 0xFFFF));
+        x1 = h2f((uint16_t)(qr >> 16));
+    }
+    const float dot = wave_sum_bfly(x0 * (float)nk[2 * lane] + x1 * (float)nk[2 * lane + 1]);
+    float* pp = part + ((size_t)C * n_kv * GQ + hq) * PS;
+    pp[2 * lane] = nsc[1] * (float)nv[2 * lane] * WSCALE;
+    pp[2 * lane + 1] = nsc[1] * (float)nv[2 * lane + 1] * WSCALE;
+    if (lane == 0) { pp[HD] = dot * nsc[0] * sc; pp[HD + 1] = 1.0f; }
+}
+
+template <int GQ, bool RELU2, bool SCALE32, bool OBF, bool SCORES, bool QR, bool APP>
 __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
     const uint16_t* __restrict__ q,   // [n_kv * GQ][128]: fp16 prepared, or (QR) raw bf16
     const int8_t* __restrict__ kc, const int8_t* __restrict__ vc,
     float* __restrict__ part, float* __restrict__ scores, uint16_t* __restrict__ o, int S, int CH,
     int C, int max_s, int n_kv, float qk_scale, float sink, const uint16_t* __restrict__ g1,
-    const uint16_t* __restrict__ g2, int ng) {
+    const uint16_t* __restrict__ g2, int ng, DecodeAppend app) {
     static_assert(GQ == 4 || GQ == 8, "4 or 8 query heads a kv head");
-    const int c = blockIdx.x, kvh = blockIdx.y;
+    static_assert(!APP || (!RELU2 && !SCORES), "the step's own append: softmax layers");
+    // APP: a 1-D grid, the C * n_kv chunk workgroups first (chunk fastest) and the n_kv append
+    // workgroups last, so that the chunks take one CU each and the short appends the spare slots
+    int c = blockIdx.x, kvh = blockIdx.y;
+    if constexpr (APP) {
+        const int id = blockIdx.x;
+        if (id >= C * n_kv) {   // uniform a workgroup
+            decode_append<GQ, SCALE32, QR>(app, q, part, C, max_s, n_kv, id - C * n_kv, qk_scale * LOG2E, g1, g2, ng);
+            return;
+        }
+        c = id % C;
+        kvh = id / C;
+    }
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
 
@@ -328,7 +389,7 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
         }
     }
     const int hq = kvh * GQ + oh;
-    if (C == 1) {
+    if (!APP && C == 1) {
         const float rr = RELU2 ? 1.0f / (WSCALE * (sink + L)) : 1.0f / (WSCALE * L);
 #pragma unroll
         for (int e = 0; e < PER; e++) o[(size_t)hq * HD + od + e] = f2a<OBF>(acc[e] * rr);
@@ -399,15 +460,23 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
 // ------------------------------------------------------------------ host launch
 int launch_full_decode(const FullDecodeArgs& a, hipStream_t st) {
     const dim3 grid(a.C, a.n_kv), block(64 * DW);
+    const DecodeAppend app{a.knew, a.vnew, a.kcw, a.vcw, a.pos, a.norm_k};
     const float qs = 0.08838834764831845f;   // 1/sqrt(128)
     const float sink = 11.313708498984761f;   // sqrt(128)
 #define EMBLA_FD(GQ, R, S32, OBF, SC)                                                              \
-    hipLaunchKernelGGL((full_decode_kernel<GQ, R, S32, OBF, SC, false>), grid, block, 0, st, a.q, a.kc, a.vc, \
-                       a.part, a.scores, a.o, a.S, a.CH, a.C, a.max_s, a.n_kv, qs, sink, nullptr, nullptr, 0)
+    hipLaunchKernelGGL((full_decode_kernel<GQ, R, S32, OBF, SC, false, false>), grid, block, 0, st, a.q, a.kc, a.vc, \
+                       a.part, a.scores, a.o, a.S, a.CH, a.C, a.max_s, a.n_kv, qs, sink, nullptr, nullptr, 0, app)
 #define EMBLA_FDR(GQ, R, S32, OBF, SC)                                                             \
-    hipLaunchKernelGGL((full_decode_kernel<GQ, R, S32, OBF, SC, true>), grid, block, 0, st, a.q, a.kc, a.vc, \
-                       a.part, a.scores, a.o, a.S, a.CH, a.C, a.max_s, a.n_kv, qs, sink, a.g1, a.g2, a.ng)
+    hipLaunchKernelGGL((full_decode_kernel<GQ, R, S32, OBF, SC, true, false>), grid, block, 0, st, a.q, a.kc, a.vc, \
+                       a.part, a.scores, a.o, a.S, a.CH, a.C, a.max_s, a.n_kv, qs, sink, a.g1, a.g2, a.ng, app)
     const int gq = a.n_q / a.n_kv;
+    if (a.append) {   // the decode step with its own append: raw queries, softmax, fp16 scales, bf16 out
+        if (!(gq == 4 && a.ng >= 0 && !a.relu2 && !a.scale32 && a.out_bf16 && !a.scores)) return EMBLA_ERR_UNSUPPORTED;
+        hipLaunchKernelGGL((full_decode_kernel<4, false, false, true, false, true, true>), dim3((a.C + 1) * a.n_kv),
+                           block, 0, st, a.q, a.kc,
+                           a.vc, a.part, a.scores, a.o, a.S, a.CH, a.C, a.max_s, a.n_kv, qs, sink, a.g1, a.g2, a.ng, app);
+        return launch_decode_merge(a.part, a.o, a.C + 1, a.n_q, false, true, WSCALE, st);
+    }
     if (a.ng >= 0) {   // raw queries: the reference's full and sparse layers, and the decode step
         if (gq == 8 && a.relu2 && a.scale32 && a.out_bf16 && !a.scores) EMBLA_FDR(8, true, true, true, false);
         else if (gq == 8 && a.relu2 && a.scale32 && a.out_bf16 && a.scores) EMBLA_FDR(8, true, true, true, true);

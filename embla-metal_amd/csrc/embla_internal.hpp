@@ -22,8 +22,25 @@ struct FullDecodeArgs {
     const uint16_t* g2 = nullptr;
     int ng = -1;
     bool merge = true;   // false: leave the chunk partials (C > 1) for a later merge
+    // the decode step's own append (append): the new token's bf16 k, v rows [n_kv][128] quantised
+    // into the writable regions kcw, vcw at position pos, and added as partial C; S = pos keys
+    bool append = false;
+    const uint16_t* knew = nullptr;
+    const uint16_t* vnew = nullptr;
+    int8_t* kcw = nullptr;
+    int8_t* vcw = nullptr;
+    int pos = 0;
+    int norm_k = 0;
 };
 int launch_full_decode(const FullDecodeArgs& a, hipStream_t st);
+/// The new token's append and partial as the kernel's extra workgroup reads them.
+struct DecodeAppend {
+    const uint16_t* k;
+    const uint16_t* v;
+    int8_t* kc;
+    int8_t* vc;
+    int pos, norm_k;
+};
 /// The merge launch_full_decode ends with, on its own (a.C > 1, partials in a.part).
 int launch_full_decode_merge(const FullDecodeArgs& a, hipStream_t st);
 /// Merges C chunk partials [C][n_q][132] into o [n_q][128]; the partials' sums carry a factor oscale.

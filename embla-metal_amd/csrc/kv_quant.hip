@@ -11,30 +11,11 @@
 // per-lane sums of two squares) that the oracle restates; no fma contraction anywhere here.
 #include "common.hpp"
 #include "embla_internal.hpp"
+#include "kv_row.hpp"
 
 #pragma clang fp contract(off)
 
 namespace embla {
-
-constexpr float EPS32 = 1.1920929e-07f;
-
-__device__ __forceinline__ float wave_sum_bfly(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = v + shfl_xor(v, m);
-    return v;
-}
-__device__ __forceinline__ float wave_max_bfly(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor(v, m));
-    return v;
-}
-
-/// RMS factor of a head held two dims a lane, in the fixed order the oracle restates.
-__device__ __forceinline__ float rms_factor(float x0, float x1) {
-    const float s0 = x0 * x0, s1 = x1 * x1;
-    const float ss = wave_sum_bfly(s0 + s1);
-    return 1.0f / sqrtf(ss / 128.0f + EPS32);
-}
 
 /// One wave a (token, kv head, K or V): two dims a lane, quantised, then stored at their places
 /// in the MFMA lane-order tiles (common.hpp; K's two bytes are adjacent, V's are not), or in plain
@@ -46,33 +27,13 @@ __global__ __launch_bounds__(64) void kv_quant_kernel(KVQuantArgs a) {
     const int pos = a.p0 + t;
     const uint16_t* src = is_v ? a.v : a.k;
     int8_t* rows = is_v ? a.vc : a.kc;
-    const size_t nrow = (size_t)a.n_kv * a.max_s * HD;
 
     const uint32_t raw = *(const uint32_t*)(src + (size_t)t * a.stride + h * HD + 2 * lane);
-    float x0 = a.in_bf16 ? bf2f(raw & 0xFFFF) : h2f(raw & 0xFFFF);
-    float x1 = a.in_bf16 ? bf2f(raw >> 16) : h2f(raw >> 16);
-    if (!is_v && a.norm_k) {
-        const float r = rms_factor(x0, x1);
-        x0 = x0 * r;
-        x1 = x1 * r;
-    }
-    if (a.in_bf16) { x0 = bf2f(f2bf(x0)); x1 = bf2f(f2bf(x1)); }
-    const float am = wave_max_bfly(fmaxf(fabsf(x0), fabsf(x1)));
-    const float inv = am > 0.0f ? 127.0f / am : 0.0f;
-    const int q0 = (int)rintf(x0 * inv), q1 = (int)rintf(x1 * inv);
-    if (lane == 0) {
-        const size_t si = (size_t)h * a.max_s + pos;
-        if (a.scale32) ((float*)(rows + nrow))[si] = am / 127.0f;
-        else ((uint16_t*)(rows + nrow))[si] = f2h(am / 127.0f);
-    }
-    if (a.row_major) {
-        *(uint16_t*)(rows + ((size_t)h * a.max_s + pos) * HD + 2 * lane) = (uint16_t)((q0 & 0xFF) | ((q1 & 0xFF) << 8));
-    } else if (!is_v) {
-        *(uint16_t*)(rows + kt_off(h, a.max_s, pos, 2 * lane, 1)) = (uint16_t)((q0 & 0xFF) | ((q1 & 0xFF) << 8));
-    } else {
-        rows[vt_off(h, a.max_s, pos, 2 * lane, 1)] = (int8_t)q0;
-        rows[vt_off(h, a.max_s, pos, 2 * lane + 1, 1)] = (int8_t)q1;
-    }
+    const float x0 = a.in_bf16 ? bf2f(raw & 0xFFFF) : h2f(raw & 0xFFFF);
+    const float x1 = a.in_bf16 ? bf2f(raw >> 16) : h2f(raw >> 16);
+    int q0, q1;
+    const float am = quant_pair(x0, x1, !is_v && a.norm_k, a.in_bf16, q0, q1);
+    store_pair8(rows, a.n_kv, a.max_s, h, pos, is_v, a.row_major, a.scale32, q0, q1, am, lane);
 }
 
 int launch_kv_quant(const KVQuantArgs& a, hipStream_t st) {

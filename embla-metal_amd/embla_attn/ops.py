@@ -64,6 +64,17 @@ def decode_int8_merge(out, S, max_s, n_kv, ws: Workspace, weights=SOFTMAX, out_d
     return out
 
 
+def decode_step_int8(qkv, q_off, k_off, v_off, kc, vc, pos, max_s, n_q, n_kv, ws: Workspace, g1=None, g2=None,
+                     ng=0, scale_dtype=F16, norm_k=False, out_dtype=BF16, chunk=0, out=None, stream=None):
+    """A full layer's decode step with its own append: the new k, v of qkv quantised into the cache
+    at pos, the softmax decode over keys 0 .. pos; q raw bf16, head-normed inside."""
+    if out is None:
+        out = torch.empty((n_q, 128), dtype=_DT[out_dtype], device=qkv.device)
+    call("embla_decode_step_int8", _p(qkv), q_off, k_off, v_off, _p(g1), _p(g2), ng, _p(kc), _p(vc), _p(out), pos,
+         max_s, n_q, n_kv, scale_dtype, int(norm_k), out_dtype, chunk, ws.ptr, ws.nbytes, stream_handle(stream))
+    return out
+
+
 def decode_int8_qraw(qraw, kc, vc, S, max_s, n_kv, g1=None, g2=None, ng=0, scale_dtype=F16, out_dtype=BF16,
                      chunk=0, ws: Workspace | None = None, out=None, stream=None):
     """Split-K decode (softmax) of raw bf16 q [n_q][128], head-normed inside the kernel."""

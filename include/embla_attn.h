@@ -266,6 +266,19 @@ int embla_decode_int8_qraw(const void* qraw, const void* g1, const void* g2, int
                            void* o, int S, int max_s, int n_q, int n_kv, int scale_dtype, int out_dtype, int chunk,
                            void* ws, size_t ws_bytes, hipStream_t stream);
 
+/* One decode step of a full layer with its own append, in one launch and a merge: the new token's
+ * k and v (bf16 [n_kv][128] at element offsets k_off, v_off of qkv) quantised into the int8 cache
+ * at position pos exactly as embla_kv_quant_append does (norm_k: K RMS-normed first; scales of
+ * scale_dtype), and the softmax decode of q (raw bf16 [n_q][128] at q_off, head-normed with ng
+ * gains as embla_decode_int8_qraw) over keys 0 .. pos, the new one included. The cached keys are
+ * read by the split-K workgroups while one more workgroup a kv head appends the new row and adds
+ * it as a partial: the append needs no launch of its own (the reference encodes kv_append and the
+ * attention as two dispatches, Engine.swift:782-818). Combinations: n_q / n_kv = 4, fp16 scales,
+ * bf16 output. ws: embla_workspace_bytes(max_s, n_q). */
+int embla_decode_step_int8(const void* qkv, int q_off, int k_off, int v_off, const void* g1, const void* g2, int ng,
+                           void* kc, void* vc, void* o, int pos, int max_s, int n_q, int n_kv, int scale_dtype,
+                           int norm_k, int out_dtype, int chunk, void* ws, size_t ws_bytes, hipStream_t stream);
+
 /* Query preparation (head_norm with ng gains + bf16 rounding; attention.metal:167-169,
  * prefill.metal:406-426): qraw bf16 rows of `stride` elements, n_q heads, T tokens ->
  * out [T][n_q][128] in out_dtype. */

@@ -102,3 +102,23 @@ def test_decode_split_rejects_single_chunk():
     assert L.embla_decode_int8_partials(d, d, d, None, 100, 1024, 16, 4, 0, 0, 0, 0, d, ws, None) < 0
     assert L.embla_decode_int8_merge(d, 100, 1024, 16, 4, 0, 0, 0, d, ws, None) < 0
     assert L.embla_decode_int8_partials(d, d, d, None, 1024, 1024, 16, 4, 0, 0, 0, 256, None, 0, None) < 0
+
+
+def test_decode_step_rejects_bad_arguments():
+    L = _lib.lib()
+    d = C.c_void_p(256)
+    ws = L.embla_workspace_bytes(1024, 16)
+
+    def step(pos=10, max_s=1024, n_q=16, n_kv=4, scale=0, out=1, chunk=0, ng=0, offs=(0, 2048, 2560), w=d, wb=ws):
+        return L.embla_decode_step_int8(d, *offs, None, None, ng, d, d, d, pos, max_s, n_q, n_kv, scale, 0, out, chunk,
+                                        w, wb, None)
+
+    assert step(pos=1024) == _lib.EMBLA_ERR_INVALID            # pos past the cache
+    assert step(pos=-1) == _lib.EMBLA_ERR_INVALID
+    assert step(offs=(0, 2049, 2560)) == _lib.EMBLA_ERR_INVALID  # k not 4-byte aligned
+    assert step(ng=1) == _lib.EMBLA_ERR_INVALID                # a gain count without its gains
+    assert step(chunk=48) == _lib.EMBLA_ERR_INVALID
+    assert step(w=None, wb=0) == _lib.EMBLA_ERR_WORKSPACE
+    assert step(pos=9000, max_s=16384, chunk=32) == _lib.EMBLA_ERR_INVALID  # 282 chunks and the append: over 256
+    assert step(scale=2) == _lib.EMBLA_ERR_UNSUPPORTED         # fp32 scales: no instance
+    assert step(n_q=32, wb=L.embla_workspace_bytes(1024, 32)) == _lib.EMBLA_ERR_UNSUPPORTED   # 8 q heads a kv head

@@ -1,7 +1,8 @@
 """A whole attention sub-layer decode step captured as one HIP graph (the event-chained step of
 Engine.swift:71-88 as a graph): per layer the q/k/v projection, the int8 append of the new k, v,
 the q preparation and split-K decode (layer 0 as two calls, layer 1 as the decode with the head
-norm inside) and the o-projection into an fp32 residual.
+norm inside, layer 2 as the decode step that appends its own token) and the o-projection into an
+fp32 residual.
 The graph is replayed several times with eager work between the replays, and every replay's
 outputs (the decode outputs, the residual, the appended cache bytes) equal the eager step's bit
 for bit: every kernel here reduces in a fixed order."""
@@ -42,7 +43,7 @@ def pack(mats):
 def test_graph_decode_step_replays(torch_gpu, orc):
     from embla_attn import ops
     torch = torch_gpu
-    n_layers, D, n_q, n_kv, max_s, pos = 2, 2048, 16, 4, 1024, 700
+    n_layers, D, n_q, n_kv, max_s, pos = 3, 2048, 16, 4, 1024, 700
     g = synth.SplitMix64(91)
     layers = []
     for l in range(n_layers):
@@ -55,7 +56,8 @@ def test_graph_decode_step_replays(torch_gpu, orc):
         vc = dev(layout.pack_region(hist["V"], hist["vs"], max_s, "v"))
         layers.append(dict(W=W, segs=segs, osegs=osegs, kc=kc, vc=vc, ws=ops.Workspace(max_s, n_q),
                            o=torch.empty(n_q, 128, dtype=torch.bfloat16, device="cuda"),
-                           qf=torch.empty(1, n_q, 128, dtype=torch.float16, device="cuda"), raw=l % 2 == 1))
+                           qf=torch.empty(1, n_q, 128, dtype=torch.float16, device="cuda"),
+                           qr=torch.empty(2048, dtype=torch.bfloat16, device="cuda"), mode=l % 3))
     x = dev(synth.bf16_bits(g.normal(D).astype(np.float32)), torch.bfloat16)
     qkv = torch.empty(3072, dtype=torch.bfloat16, device="cuda")
     resid = torch.empty(D, dtype=torch.float32, device="cuda")
@@ -64,8 +66,14 @@ def test_graph_decode_step_replays(torch_gpu, orc):
         resid.zero_()   # a fill kernel, not a memset node
         for L in layers:
             ops.gemv_q4(L["W"], x, qkv, L["segs"], D, ops.EPI_BF16)
+            if L["mode"] == 2:   # the append inside the decode launch
+                L["qr"].copy_(qkv[:2048])
+                ops.decode_step_int8(qkv, 0, 2048, 2560, L["kc"], L["vc"], pos, max_s, n_q, n_kv, L["ws"], out=L["o"])
+                ops.gemv_q4(L["W"], L["o"], resid, L["osegs"], D, ops.EPI_ADD)
+                continue
             ops.kv_quant_append(qkv[2048:2560], qkv[2560:3072], 1, pos, n_kv, L["kc"], L["vc"], max_s)
-            if L["raw"]:   # the head norm inside the decode kernel
+            if L["mode"] == 1:   # the head norm inside the decode kernel
+                L["qr"].copy_(qkv[:2048])
                 ops.decode_int8_qraw(qkv[:2048], L["kc"], L["vc"], pos + 1, max_s, n_kv, ws=L["ws"], out=L["o"])
             else:
                 ops.q_prep(qkv[:2048], None, None, 0, 1, n_q, out=L["qf"])
@@ -92,9 +100,8 @@ def test_graph_decode_step_replays(torch_gpu, orc):
         K, ks = layout.unpack_region(cache[:rb], n_kv, max_s, "k", np.uint16)
         V, vs = layout.unpack_region(cache[rb:], n_kv, max_s, "v", np.uint16)
         n = pos + 1
-        if L["raw"]:   # the last layer: the step's final q/k/v are its own
-            assert l == n_layers - 1
-            qb = qkv[:2048].view(torch.int16).cpu().numpy().view(np.uint16).reshape(n_q, 128)
+        if L["mode"]:   # the raw q the layer read
+            qb = L["qr"].view(torch.int16).cpu().numpy().view(np.uint16).reshape(n_q, 128)
             q = np.stack([orc.head_norm(synth.bf16_val(qb[h])) for h in range(n_q)])
         else:
             q = L["qf"].float().cpu().numpy()[0]
