@@ -43,13 +43,14 @@ def test_decode_softmax_int8_matches_oracle(torch_gpu, orc, S, max_s, seed):
     assert_close(got, oracle_cfg(orc, c), what=f"S={S}")
 
 
-@pytest.mark.parametrize("chunk", [128, 256, 512, 2048, 4096])
-def test_decode_independent_of_split(torch_gpu, orc, chunk):
-    say(f"decode split chunk={chunk}")
-    c = synth.decode_int8_case(seed=0, S=4000)
+@pytest.mark.parametrize("S,chunk", [(4000, 128), (4000, 256), (4000, 512), (4000, 2048), (4000, 4096),
+                                     (12000, 128), (20000, 128), (32768, 128), (8000, 96)])   # 65 .. 256 chunks
+def test_decode_independent_of_split(torch_gpu, orc, S, chunk):
+    say(f"decode split S={S} chunk={chunk}")
+    c = synth.decode_int8_case(seed=0, S=S)
     ref = oracle_cfg(orc, c)
-    got = run_cfg_decode(torch_gpu, c, 4096, chunk=chunk)
-    assert_close(got, ref, what=f"chunk={chunk}")
+    got = run_cfg_decode(torch_gpu, c, (S + 31) // 32 * 32, chunk=chunk)
+    assert_close(got, ref, what=f"S={S} chunk={chunk}")
 
 
 @pytest.mark.parametrize("S", [40, 5000])
