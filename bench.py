@@ -468,6 +468,42 @@ def measured_traffic():
     return None
 
 
+def profile_case(torch, name, calls=5):
+    """Only dispatches one workload's calls, eagerly, for rocprofv3 --pmc runs (the last dispatch
+    is read): 'c5_full' = C5's full-layer attention (embla_prefill_int8, 2048 rows after 30720
+    int8 positions); 'gemm_prefill' = the q/k/v projection GEMM of C5's chunk (T 2048, O 3072,
+    K 2048). Prints nothing."""
+    from embla_attn import ops
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4)
+    if name == "c5_full":
+        p0, T, max_s, n_kv = 30720, 2048, 32768, 4
+        nrow = n_kv * max_s * 128
+        kc = torch.empty(nrow + n_kv * max_s * 2, dtype=torch.uint8, device="cuda")
+        vc = torch.empty_like(kc)
+        for t in (kc, vc):
+            t[:nrow].random_(0, 256, generator=g)
+            t[nrow:].view(torch.float16).uniform_(0.005, 0.02, generator=g)
+        q = torch.randn(T, 16, 128, generator=g, device="cuda").bfloat16()
+        out = torch.empty(T, 16, 128, dtype=torch.bfloat16, device="cuda")
+        ws = ops.PrefillWorkspace(T, 16)
+        for _ in range(calls):
+            ops.prefill_int8(q, kc, vc, T, p0, max_s, n_kv, out=out, ws=ws)
+    elif name == "gemm_prefill":
+        T, K, O = 2048, 2048, 3072
+        wb, sb = O * K // 2, O * K // 64 * 2
+        W = torch.randint(0, 256, (wb + 2 * sb,), dtype=torch.uint8, device="cuda", generator=g)
+        W[wb:wb + sb].view(torch.bfloat16).fill_(0.01)
+        W[wb + sb:].view(torch.bfloat16).fill_(-0.075)
+        x = torch.randn(T, K, device="cuda", generator=g).bfloat16()
+        y = torch.empty(T, O, dtype=torch.bfloat16, device="cuda")
+        for _ in range(calls):
+            ops.gemm_q4(W, (0, wb, wb + sb), x, y, T, O, K, ops.EPI_BF16)
+    else:
+        raise SystemExit(f"unknown profile case {name}")
+    torch.cuda.synchronize()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -480,6 +516,8 @@ def main():
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only dispatch C3 decode layers and a 64 MB copy (each after a cache-evicting "
                          "fill) for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs; prints nothing else")
+    ap.add_argument("--profile-case", choices=["c5_full", "gemm_prefill"],
+                    help="only dispatch one workload's calls (for rocprofv3 --pmc runs); prints nothing")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the attention hot path runs on a "
@@ -494,6 +532,9 @@ def main():
     _lib.lib()   # the HIP library must load; there is no fallback path
     if args.traffic_probe:
         traffic_probe(torch)
+        return
+    if args.profile_case:
+        profile_case(torch, args.profile_case)
         return
 
     L = 32768
