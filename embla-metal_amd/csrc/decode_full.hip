@@ -317,6 +317,11 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
                 wa[e] = (_Float16)(p * vs[e] * WSCALE);
             }
         }
+        if (!full) {   // uniform: a masked key's weight is 0 whatever its scale holds (past S: maybe never written)
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                if (!valid[e]) wa[e] = (_Float16)0.0f;
+        }
         // O += W V: MFMA u covers dims 8n + u (column n), rows = heads 4g + i
 #pragma unroll
         for (int u = 0; u < 8; u++) {

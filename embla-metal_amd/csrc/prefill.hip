@@ -154,6 +154,15 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
                 const size_t vidx = (size_t)kvh * a.max_s + kt + 4 * (l >> 4);
                 scales4<SCALE32>(vsb, vidx, vsr[i]);
                 scales4<SCALE32>(vsb, vidx + 16, vsr[i] + 4);
+                // keys past the last one the workgroup needs (the last staged tile; maybe never
+                // written) are staged as zero rows: masked keys then add exactly 0 to P·V
+                const int lk = k0 + 32 * gt;   // the tile's logical first key (kt may be clamped)
+                if (lk + 31 > hi) {
+                    if (lk + 16 * (j >> 1) + (l & 15) > hi) ksr[i] = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        if (lk + 16 * (e >> 2) + 4 * (l >> 4) + (e & 3) > hi) vsr[i][e] = 0.0f;
+                }
             }
         }
     };

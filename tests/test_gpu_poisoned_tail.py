@@ -1,0 +1,88 @@
+"""Cache positions past the keys a call reads may hold anything (memory never written): NaN scales
+and arbitrary int8 rows there must not reach the output. The kernels read whole 32-key tiles (and
+128-key staged tiles in prefill), so the last tile's keys past the limit are masked; these tests
+poison them and compare with the oracle over the valid keys only."""
+import numpy as np
+import pytest
+
+from conftest import gpu_available
+from gpu_util import assert_close, bf16_host, dev, f16_host, say
+from embla_attn import layout, synth
+
+pytestmark = pytest.mark.gpu
+
+NAN16 = np.uint16(0x7E00)
+
+
+@pytest.fixture(scope="module")
+def torch_gpu():
+    if not gpu_available():
+        pytest.skip("no GPU")
+    import torch
+    return torch
+
+
+def poisoned_regions(K, ks, V, vs, S, max_s, seed):
+    """Regions whose positions S .. max_s - 1 hold random int8 rows and NaN fp16 scales."""
+    g = synth.SplitMix64(seed)
+    n_kv = K.shape[0]
+    tail = max_s - S
+    Kp = np.concatenate([K[:, :S], g.int8(n_kv * tail * 128).reshape(n_kv, tail, 128)], 1)
+    Vp = np.concatenate([V[:, :S], g.int8(n_kv * tail * 128).reshape(n_kv, tail, 128)], 1)
+    ksp = np.concatenate([ks[:, :S], np.full((n_kv, tail), NAN16, np.uint16)], 1)
+    vsp = np.concatenate([vs[:, :S], np.full((n_kv, tail), NAN16, np.uint16)], 1)
+    return dev(layout.pack_region(Kp, ksp, max_s, "k")), dev(layout.pack_region(Vp, vsp, max_s, "v"))
+
+
+@pytest.mark.parametrize("S,max_s", [(1000, 1024), (33, 64), (4001, 4096)])
+def test_decode_ignores_poisoned_tail(torch_gpu, orc, S, max_s):
+    from embla_attn import ops
+    torch = torch_gpu
+    say(f"decode poisoned tail S={S} max_s={max_s}")
+    c = synth.decode_int8_case(seed=31, S=S)
+    kc, vc = poisoned_regions(c["K"], c["ks"], c["V"], c["vs"], S, max_s, 5)
+    o = ops.decode_int8(dev(c["q"], torch.float16), kc, vc, S, max_s, 4, ws=ops.Workspace(max_s, 16))
+    ref = orc.decode_int8(synth.f16_val(c["q"]), c["K"], synth.f16_val(c["ks"]), c["V"], synth.f16_val(c["vs"]))
+    assert_close(f16_host(o), ref, what=f"S={S}")
+
+
+@pytest.mark.parametrize("pos", [1000, 40])
+def test_decode_step_ignores_poisoned_tail(torch_gpu, orc, pos):
+    """The fused step appends position pos itself; positions past it stay poisoned."""
+    from embla_attn import ops
+    torch = torch_gpu
+    say(f"decode step poisoned tail pos={pos}")
+    max_s = 1024
+    c = synth.decode_int8_case(seed=32, S=pos)
+    kc, vc = poisoned_regions(c["K"], c["ks"], c["V"], c["vs"], pos, max_s, 6)
+    g = synth.SplitMix64(33)
+    qkv = synth.bf16_bits(g.normal(24 * 128) * 2)
+    x = dev(qkv, torch.bfloat16)
+    o = ops.decode_step_int8(x, 0, 2048, 2560, kc, vc, pos, max_s, 16, 4, ops.Workspace(max_s, 16))
+    torch.cuda.synchronize()
+    K, ks = layout.unpack_region(kc.cpu().numpy(), 4, max_s, "k", np.uint16)
+    V, vs = layout.unpack_region(vc.cpu().numpy(), 4, max_s, "v", np.uint16)
+    n = pos + 1
+    qn = np.stack([orc.head_norm(synth.bf16_val(qkv[h * 128:(h + 1) * 128])) for h in range(16)])
+    ref = orc.decode_int8(qn, np.ascontiguousarray(K[:, :n]), synth.f16_val(np.ascontiguousarray(ks[:, :n])),
+                          np.ascontiguousarray(V[:, :n]), synth.f16_val(np.ascontiguousarray(vs[:, :n])))
+    assert_close(bf16_host(o), ref, what=f"pos={pos}")
+
+
+@pytest.mark.parametrize("p0,T,max_s", [(1000, 20, 1152), (100, 5, 256)])
+def test_prefill_ignores_poisoned_tail(torch_gpu, orc, p0, T, max_s):
+    from embla_attn import ops
+    torch = torch_gpu
+    say(f"prefill poisoned tail p0={p0} T={T} max_s={max_s}")
+    c = synth.prefill_case(seed=34, p0=p0, T=T)
+    kc, vc = poisoned_regions(c["K"], c["ks"], c["V"], c["vs"], p0, max_s, 7)
+    o = ops.prefill_full(dev(c["q"], torch.bfloat16), dev(c["kn"], torch.bfloat16), dev(c["vn"], torch.bfloat16),
+                         kc, vc, T, p0, max_s, 4)
+    torch.cuda.synchronize()
+    K, ks = layout.unpack_region(kc.cpu().numpy(), 4, max_s, "k", np.uint16)
+    V, vs = layout.unpack_region(vc.cpu().numpy(), 4, max_s, "v", np.uint16)
+    n = p0 + T
+    ref = orc.prefill_int8(synth.bf16_val(c["q"]), np.ascontiguousarray(K[:, :n]),
+                           synth.f16_val(np.ascontiguousarray(ks[:, :n])), np.ascontiguousarray(V[:, :n]),
+                           synth.f16_val(np.ascontiguousarray(vs[:, :n])), p0, weights=0)
+    assert_close(bf16_host(o), ref, what=f"p0={p0} T={T}")
