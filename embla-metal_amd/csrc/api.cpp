@@ -202,7 +202,9 @@ int embla_decode_step_int8(const void* qkv, int q_off, int k_off, int v_off, con
                            void* kc, void* vc, void* o, int pos, int max_s, int n_q, int n_kv, int scale_dtype,
                            int norm_k, int out_dtype, int chunk, void* ws, size_t ws_bytes, hipStream_t stream) {
     if (!qkv || !kc || !vc || !o || ng < 0 || ng > 2 || (ng >= 1 && !g1) || (ng >= 2 && !g2)) return EMBLA_ERR_INVALID;
-    if (q_off < 0 || k_off < 0 || v_off < 0 || (q_off | k_off | v_off) & 1) return EMBLA_ERR_INVALID;
+    // q is read 16 bytes at a time: 8-element offsets from a 16-byte aligned buffer
+    if (q_off < 0 || k_off < 0 || v_off < 0 || (q_off | k_off | v_off) & 7 || (uintptr_t)qkv & 15)
+        return EMBLA_ERR_INVALID;
     if (pos < 0 || max_s <= 0 || max_s % 32 || pos >= max_s) return EMBLA_ERR_INVALID;
     if (n_kv <= 0 || n_q % n_kv || n_kv > kMaxKV) return EMBLA_ERR_INVALID;
     if (!valid_scale(scale_dtype) || !valid_act(out_dtype) || chunk < 0 || chunk % 32) return EMBLA_ERR_INVALID;

@@ -267,7 +267,8 @@ int embla_decode_int8_qraw(const void* qraw, const void* g1, const void* g2, int
                            void* ws, size_t ws_bytes, hipStream_t stream);
 
 /* One decode step of a full layer with its own append, in one launch and a merge: the new token's
- * k and v (bf16 [n_kv][128] at element offsets k_off, v_off of qkv) quantised into the int8 cache
+ * k and v (bf16 [n_kv][128] at element offsets k_off, v_off of qkv; q_off, k_off, v_off multiples
+ * of 8 and qkv 16-byte aligned) quantised into the int8 cache
  * at position pos exactly as embla_kv_quant_append does (norm_k: K RMS-normed first; scales of
  * scale_dtype), and the softmax decode of q (raw bf16 [n_q][128] at q_off, head-normed with ng
  * gains as embla_decode_int8_qraw) over keys 0 .. pos, the new one included. The cached keys are

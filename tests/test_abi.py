@@ -115,7 +115,8 @@ def test_decode_step_rejects_bad_arguments():
 
     assert step(pos=1024) == _lib.EMBLA_ERR_INVALID            # pos past the cache
     assert step(pos=-1) == _lib.EMBLA_ERR_INVALID
-    assert step(offs=(0, 2049, 2560)) == _lib.EMBLA_ERR_INVALID  # k not 4-byte aligned
+    assert step(offs=(0, 2049, 2560)) == _lib.EMBLA_ERR_INVALID  # k not 16-byte aligned
+    assert step(offs=(4, 2048, 2560)) == _lib.EMBLA_ERR_INVALID  # q not 16-byte aligned
     assert step(ng=1) == _lib.EMBLA_ERR_INVALID                # a gain count without its gains
     assert step(chunk=48) == _lib.EMBLA_ERR_INVALID
     assert step(w=None, wb=0) == _lib.EMBLA_ERR_WORKSPACE
