@@ -158,6 +158,18 @@ __global__ __launch_bounds__(256) void ring_decode_kernel(RingArgs a) {
         h8_t wa;
         softmax_step(x, wa);
         const u4_t wu = __builtin_bit_cast(u4_t, wa);
+        if (!(t0 >= lo && t0 + 32 <= j1)) {
+            // uniform: a partial tile. The masked keys' V elements (the same 8 key items as the
+            // weights, two a word) are zeroed, so slots never written (NaN bits) add exactly 0.
+            u4_t mk;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int p0 = t0 + 16 * (k >> 1) + 4 * g + 2 * (k & 1);
+                mk[k] = (p0 >= lo && p0 < j1 ? 0xFFFFu : 0u) | (p0 + 1 >= lo && p0 + 1 < j1 ? 0xFFFF0000u : 0u);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) Vt[b][u] &= mk;
+        }
 #pragma unroll
         for (int u = 0; u < 8; u++) O[u] = mfma16x<BF>(wu, Vt[b][u], O[u]);
     };

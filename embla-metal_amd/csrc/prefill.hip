@@ -142,6 +142,17 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
                 const size_t off = tile_base(kvh, a.R, (k0 + 32 * gt) % a.R, 2) + (size_t)jl * 16;
                 kr[i] = ld16((const char*)a.kring + off);
                 vr[i] = ld16((const char*)a.vring + off);
+                // V piece (row jl / 64, slot l = jl % 64): keys 16 (e / 4) + 4 (l / 16) + e % 4 of
+                // the tile; those past the last key the workgroup needs (slots maybe never written)
+                // are zeroed so that their weight 0 adds exactly 0
+                const int lk = k0 + 32 * gt, l = jl & 63;
+                if (lk + 31 > hi) {
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        const int e = 2 * k, key = lk + 16 * (e >> 2) + 4 * (l >> 4) + (e & 3);
+                        vr[i][k] &= (key <= hi ? 0xFFFFu : 0u) | (key + 1 <= hi ? 0xFFFF0000u : 0u);
+                    }
+                }
             } else {
                 const int kt = tile_key(k0 + 32 * gt);
                 const size_t off = tile_base(kvh, a.max_s, kt, 1) + (size_t)jl * 16;

@@ -1,7 +1,8 @@
 """Cache positions past the keys a call reads may hold anything (memory never written): NaN scales
 and arbitrary int8 rows there must not reach the output. The kernels read whole 32-key tiles (and
 128-key staged tiles in prefill), so the last tile's keys past the limit are masked; these tests
-poison them and compare with the oracle over the valid keys only."""
+poison them and compare with the oracle over the valid keys only (int8 caches), or with the same
+call over a zero-filled ring (16-bit rings)."""
 import numpy as np
 import pytest
 
@@ -86,3 +87,61 @@ def test_prefill_ignores_poisoned_tail(torch_gpu, orc, p0, T, max_s):
                            synth.f16_val(np.ascontiguousarray(ks[:, :n])), np.ascontiguousarray(V[:, :n]),
                            synth.f16_val(np.ascontiguousarray(vs[:, :n])), p0, weights=0)
     assert_close(bf16_host(o), ref, what=f"p0={p0} T={T}")
+
+
+def ring_pair(rows_hist, upto, R, kind):
+    """A ring after positions 0 .. upto - 1, slots never written zero, and the same ring with NaN
+    bits in those slots (16-bit rows)."""
+    n_kv = rows_hist.shape[0]
+    zero = np.zeros((n_kv, R, 128), np.uint16)
+    zero[:, :upto] = rows_hist[:, :upto]
+    bad = zero.copy()
+    bad[:, upto:] = NAN16
+    return layout.pack_ring16(zero, kind), layout.pack_ring16(bad, kind)
+
+
+@pytest.mark.parametrize("pos", [3, 100, 1000])
+def test_ring_decode_ignores_unwritten_slots(torch_gpu, pos):
+    """Early in a ring's life its slots past pos were never written: NaN bits there change nothing
+    (the zero-filled ring's outputs are checked against the oracle in test_gpu_sliding)."""
+    from embla_attn import ops
+    torch = torch_gpu
+    say(f"ring decode unwritten slots pos={pos}")
+    R, W, n_kv = 8192, 1024, 4
+    g = synth.SplitMix64(40)
+    K = synth.f16_bits(g.normal(n_kv * (pos + 1) * 128)).reshape(n_kv, pos + 1, 128)
+    V = synth.f16_bits(g.normal(n_kv * (pos + 1) * 128)).reshape(n_kv, pos + 1, 128)
+    q = synth.f16_bits(g.normal(16 * 128)).reshape(16, 128)
+    outs = []
+    for i in range(2):
+        kr = dev(ring_pair(K, pos, R, "k")[i])
+        vr = dev(ring_pair(V, pos, R, "v")[i])
+        outs.append(ops.sliding_decode(dev(q, torch.float16), dev(K[:, pos].copy(), torch.float16),
+                                       dev(V[:, pos].copy(), torch.float16), kr, vr, pos, W, R, n_kv,
+                                       ws=ops.Workspace(R, 16)))
+    torch.cuda.synchronize()
+    a, b = (o.cpu().numpy() for o in outs)
+    assert np.isfinite(f16_host(outs[1])).all()
+    np.testing.assert_array_equal(b, a)
+
+
+@pytest.mark.parametrize("p0,T", [(0, 40), (100, 20)])
+def test_ring_prefill_ignores_unwritten_slots(torch_gpu, p0, T):
+    from embla_attn import ops
+    torch = torch_gpu
+    say(f"ring prefill unwritten slots p0={p0} T={T}")
+    R, W, n_kv = 8192, 1024, 4
+    g = synth.SplitMix64(41)
+    n = p0 + T
+    K = synth.f16_bits(g.normal(n_kv * n * 128)).reshape(n_kv, n, 128)
+    V = synth.f16_bits(g.normal(n_kv * n * 128)).reshape(n_kv, n, 128)
+    q = synth.f16_bits(g.normal(T * 16 * 128)).reshape(T, 16, 128)
+    outs = []
+    for i in range(2):
+        kr = dev(ring_pair(K, n, R, "k")[i])
+        vr = dev(ring_pair(V, n, R, "v")[i])
+        outs.append(ops.prefill_ring(dev(q, torch.float16), kr, vr, T, p0, R, W, n_kv, dtype=ops.F16))
+    torch.cuda.synchronize()
+    a, b = (o.cpu().numpy() for o in outs)
+    assert np.isfinite(f16_host(outs[1])).all()
+    np.testing.assert_array_equal(b, a)
