@@ -130,6 +130,31 @@ def bench_c3(torch, steps, warmup, n_layers=16, contexts=(4096, 16384, 32768)):
     return res, case, outs[0], regions, main_us
 
 
+def bench_read_floor(torch, n_layers=16, max_s=32768, n_kv=4, reps=20):
+    """The practical floor of one decode layer's split-K pass: a plain streaming read of the same
+    bytes (K and V rows + fp16 scales of 32768 keys, 34,078,720 B) in one launch, 16 distinct
+    buffers in one graph (545 MB, beyond the 256 MB MALL); the best of three grid sizes."""
+    from embla_attn import ops
+    nbytes = 2 * n_kv * max_s * (128 + 2)
+    bufs = []
+    for i in range(n_layers):
+        b = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+        b.random_(0, 256, generator=torch.Generator(device="cuda").manual_seed(500 + i))
+        bufs.append(b)
+    sink = torch.empty(4096, dtype=torch.int32, device="cuda")
+    best = None
+    for grid in (512, 1024, 2048):
+        def run(grid=grid):
+            for b in bufs:
+                ops.stream_read(b, sink, grid)
+        _, ms = time_graph(torch, run, reps, 3)
+        us = ms * 1000 / n_layers
+        if best is None or us < best[1]:
+            best = (grid, us)
+    del bufs
+    return dict(bytes=nbytes, grid=best[0], us_per_launch=best[1], gbs=nbytes / (best[1] * 1e-6) / 1e9)
+
+
 def bench_c2(torch, n_steps=512, reps=5):
     """Config C2: 512 consecutive decode steps over an fp16 ring of 8192, window 1024, each
     appending one K/V pair; one graph of the 512 steps."""
@@ -546,6 +571,7 @@ def main():
                           "steps": args.steps}))
         return
     res, case, out0, regions, main_us = bench_c3(torch, args.steps, args.warmup)
+    floor = bench_read_floor(torch)
     step = bench_step(torch, regions)
     step["us_per_layer_append_own_launch"] = bench_step(torch, regions, fused=False)["us_per_layer"]
     sampling = bench_sampling(torch)
@@ -592,6 +618,13 @@ def main():
             "frac": round(layer_bytes(L) / (head["us_per_layer"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "kernels": "full_decode_kernel + decode_merge_kernel (one layer's decode call)",
             "per_call_bytes": layer_bytes(L),
+        },
+        "hbm_read_floor": {
+            "what": "a plain streaming read of one layer's K+V bytes in one launch (embla_stream_read), "
+                    "16 distinct buffers a graph: the practical floor of the split-K pass at this size",
+            "bytes": floor["bytes"], "grid": floor["grid"], "us_per_launch": round(floor["us_per_launch"], 3),
+            "gbs": round(floor["gbs"], 1), "frac_of_peak": round(floor["gbs"] / HBM_PEAK_GBS, 4),
+            "split_k_launch_over_floor": round(main_us / floor["us_per_launch"], 3),
         },
         "c3_sweep_us_per_layer": {str(k): round(v["us_per_layer"], 3) for k, v in res.items()},
         "c3_sweep_gbs": {str(k): round(v["gbs"], 1) for k, v in res.items()},

@@ -239,6 +239,12 @@ int embla_decode_step_int8(const void* qkv, int q_off, int k_off, int v_off, con
     return launch_full_decode(a, stream);
 }
 
+int embla_stream_read(const void* p, size_t bytes, uint32_t* sink, int grid, hipStream_t stream) {
+    if (!p || !sink || bytes == 0 || bytes % 16 || ((uintptr_t)p & 15) || grid <= 0 || grid > 65536)
+        return EMBLA_ERR_INVALID;
+    return launch_stream_read(p, bytes, sink, grid, stream);
+}
+
 int embla_q_prep(const void* qraw, const void* g1, const void* g2, int ng, int stride, int T,
                  int n_q, void* out, int out_dtype, hipStream_t stream) {
     if (!qraw || !out || T <= 0 || n_q <= 0 || ng < 0 || ng > 2 || stride < n_q * 128) return EMBLA_ERR_INVALID;

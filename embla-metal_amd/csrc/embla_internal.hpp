@@ -207,6 +207,7 @@ struct BlockCopyArgs {
     int save;          // cache -> stored, else stored -> cache
 };
 int launch_block_copy(const BlockCopyArgs& a, hipStream_t st);
+int launch_stream_read(const void* p, size_t bytes, uint32_t* sink, int grid, hipStream_t st);
 
 /// The 4-bit projections (gemv_q4.hip): stacked segments, as gemv.metal's Seg.
 constexpr int kMaxGemvSegs = 8;

@@ -64,6 +64,11 @@ def decode_int8_merge(out, S, max_s, n_kv, ws: Workspace, weights=SOFTMAX, out_d
     return out
 
 
+def stream_read(buf, sink, grid=1024, stream=None):
+    """One streaming read of buf (a bandwidth probe); sink: int32 [grid]."""
+    call("embla_stream_read", _p(buf), buf.numel() * buf.element_size(), _p(sink), grid, stream_handle(stream))
+
+
 def decode_step_int8(qkv, q_off, k_off, v_off, kc, vc, pos, max_s, n_q, n_kv, ws: Workspace, g1=None, g2=None,
                      ng=0, scale_dtype=F16, norm_k=False, out_dtype=BF16, chunk=0, out=None, stream=None):
     """A full layer's decode step with its own append: the new k, v of qkv quantised into the cache
