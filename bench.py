@@ -438,27 +438,81 @@ def bench_c5(torch, reps=10):
     return dict(full, sliding=sliding, sparse=sparse)
 
 
-def cpu_baseline(case, L, budget_s=10.0):
-    """The C oracle (scalar fp32 restatement, one thread) on whole C3 layers at context L."""
+def _cpu_threads():
+    """Host threads the baseline uses: OMP_NUM_THREADS when set (the GPU box sets it to its CPU
+    share), else every core this process may run on."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        return int(env)
+    return len(os.sched_getaffinity(0))
+
+
+def _timed(fn, budget_s, min_n=2, max_n=200):
+    out, n, t0 = None, 0, time.perf_counter()
+    while n < min_n or (time.perf_counter() - t0 < budget_s and n < max_n):
+        out = fn()
+        n += 1
+    return (time.perf_counter() - t0) / n, n, out
+
+
+def cpu_baseline(case, L, budget_s=6.0):
+    """The oracle's C restatement of the reference's math (oracle/oracle.c) built at -O3
+    -march=native with OpenMP (liborc_omp.so: threads over query heads, prefill rows and index
+    keys; the same results as the checker build), timed on this host's cores: C3 whole layers at
+    context L (GB/s, the headline's unit), plus C4 (one sparse-layer step: index scores, top-k,
+    attention over the 1152 rows) and C5 full (a 64-row sample of the 2048-row chunk, scaled to
+    TFLOP/s). The reference itself has no CPU attention path (all of it is Metal)."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import numpy as np
     import orc
     from embla_attn import synth
+    orc.use_openmp(True)
+    threads = _cpu_threads()
+    os.environ["OMP_NUM_THREADS"] = str(threads)
     q = synth.f16_val(case["q"])
     K, V = case["K"][:, :L], case["V"][:, :L]
     ks, vs = synth.f16_val(case["ks"][:, :L]), synth.f16_val(case["vs"][:, :L])
-    out = None
-    n = 0
-    t0 = time.perf_counter()
-    while n < 3 or time.perf_counter() - t0 < budget_s:
-        out = orc.decode_int8(q, K, ks, V, vs)
-        n += 1
-        if n >= 200:
-            break
-    dt = (time.perf_counter() - t0) / n
-    return dict(value=layer_bytes(L) / dt / 1e9, unit="GB/s", cores=1, kind="port",
-                sample=f"{n} whole C3 layers at context {L} (16 q / 4 kv heads), "
-                       f"{dt * 1e6:.0f} us a layer, scalar fp32 oracle, 1 thread"), out
+    dt3, n3, out = _timed(lambda: orc.decode_int8(q, K, ks, V, vs), budget_s)
+    # C4: one sparse-layer decode step at context 32768
+    c4 = synth.sparse_case(seed=3, ctx=32768)
+    ctx = 32768
+
+    q4, K4, V4 = synth.f16_val(c4["q"]), synth.f16_val(c4["K"]), synth.f16_val(c4["V"])
+
+    def c4_step():
+        sc = orc.index_scores(c4["qi"], c4["w"], c4["ki"][:ctx - 128])
+        sel = orc.select_keys(np.concatenate([sc, np.zeros(128, np.float32)]), ctx)
+        return orc.decode_rows(q4, K4, V4, sel.astype(np.int32))
+    dt4, n4, _ = _timed(c4_step, budget_s / 2)
+    # C5 full: 64 consecutive rows from the middle of the chunk (row i attends p0 + i + 1 keys),
+    # threads over the rows, scaled to TFLOP/s by their exact pair count
+    p0, T, r0, nr = 30720, 2048, 992, 64
+    c5 = synth.prefill_case(seed=4, p0=p0, T=T)
+    Kc = np.concatenate([c5["K"], np.zeros((4, T, 128), np.int8)], 1)
+    Vc = np.concatenate([c5["V"], np.zeros((4, T, 128), np.int8)], 1)
+    ksc = np.concatenate([synth.f16_val(c5["ks"]), np.full((4, T), 0.01, np.float32)], 1)
+    vsc = np.concatenate([synth.f16_val(c5["vs"]), np.full((4, T), 0.01, np.float32)], 1)
+    qf = synth.bf16_val(c5["q"][r0:r0 + nr])
+    flops_rows = float(sum((p0 + r0 + i + 1) * 16 * 512 for i in range(nr)))
+
+    def c5_rows():
+        return orc.prefill_int8(qf, Kc, ksc, Vc, vsc, p0 + r0)
+    dt5, n5, _ = _timed(c5_rows, budget_s / 2, min_n=1, max_n=5)
+    orc.use_openmp(False)
+    cores = os.cpu_count()
+    base = dict(cores=threads, host_cpus=cores, kind="port", build="oracle/oracle.c, gcc -O3 -march=native -fopenmp")
+    c3 = dict(value=layer_bytes(L) / dt3 / 1e9, unit="GB/s", **base,
+              sample=f"{n3} whole C3 layers at context {L} (16 q / 4 kv heads), {dt3 * 1e6:.0f} us a layer, "
+                     f"{threads} OpenMP threads over the 16 query heads")
+    more = {
+        "c4_sparse": dict(value=dt4 * 1e6, unit="us/layer", sample=f"{n4} C4 sparse-layer steps at context 32768 "
+                          "(index scores of 32640 keys over threads, serial top-k, attention over 1152 rows)"),
+        "c5_prefill_full": dict(value=flops_rows / dt5 / 1e12, unit="TFLOP/s",
+                                sample=f"{n5} passes over rows {r0}..{r0 + nr - 1} of the C5 chunk "
+                                       f"({flops_rows / 1e9:.2f} GFLOP a pass, {dt5 * 1e3:.0f} ms), threads over rows"),
+    }
+    c3["more"] = more
+    return c3, out
 
 
 def traffic_probe(torch, reps=6):

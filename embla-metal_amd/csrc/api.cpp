@@ -100,6 +100,23 @@ namespace {
 int full_decode_args(const void* q, const void* kc, const void* vc, void* o, float* scores, int S, int max_s, int n_q,
                      int n_kv, int weights, int scale_dtype, int out_dtype, int chunk, void* ws, size_t ws_bytes,
                      FullDecodeArgs& a) {
+    const int rc = embla::full_decode_plan(q, kc, vc, o, scores, S, max_s, n_q, n_kv, weights, scale_dtype, out_dtype,
+                                           chunk, a);
+    if (rc) return rc;
+    if (a.C > 1) {
+        if (!ws || ws_bytes < embla_workspace_bytes(max_s, n_q)) return EMBLA_ERR_WORKSPACE;
+        if ((size_t)a.C * n_q * kPartStride * 4 > part_bytes(max_s, n_q)) return EMBLA_ERR_WORKSPACE;
+    }
+    a.part = ws ? carve(ws, max_s, n_q).part : nullptr;
+    return EMBLA_OK;
+}
+
+}  // namespace
+
+namespace embla {
+
+int full_decode_plan(const void* q, const void* kc, const void* vc, void* o, float* scores, int S, int max_s, int n_q,
+                     int n_kv, int weights, int scale_dtype, int out_dtype, int chunk, FullDecodeArgs& a) {
     if (S <= 0 || max_s <= 0 || max_s % 32 || S > max_s) return EMBLA_ERR_INVALID;
     if (n_kv <= 0 || n_q % n_kv || n_kv > kMaxKV) return EMBLA_ERR_INVALID;
     if (weights != EMBLA_SOFTMAX && weights != EMBLA_RELU2_SINK) return EMBLA_ERR_INVALID;
@@ -109,15 +126,10 @@ int full_decode_args(const void* q, const void* kc, const void* vc, void* o, flo
     const int ch = chunk ? chunk : decode_chunk(S, n_kv);
     const int C = (S + ch - 1) / ch;
     if (C > kMaxChunks) return EMBLA_ERR_INVALID;
-    if (C > 1) {
-        if (!ws || ws_bytes < embla_workspace_bytes(max_s, n_q)) return EMBLA_ERR_WORKSPACE;
-        if ((size_t)C * n_q * kPartStride * 4 > part_bytes(max_s, n_q)) return EMBLA_ERR_WORKSPACE;
-    }
-    Workspace w = ws ? carve(ws, max_s, n_q) : Workspace{nullptr, nullptr, nullptr};
     a.q = (const uint16_t*)q;
     a.kc = (const int8_t*)kc;
     a.vc = (const int8_t*)vc;
-    a.part = w.part;
+    a.part = nullptr;
     a.scores = scores;
     a.o = (uint16_t*)o;
     a.S = S; a.CH = ch; a.C = C; a.max_s = max_s; a.n_q = n_q; a.n_kv = n_kv;
@@ -127,7 +139,7 @@ int full_decode_args(const void* q, const void* kc, const void* vc, void* o, flo
     return EMBLA_OK;
 }
 
-}  // namespace
+}  // namespace embla
 
 extern "C" {
 
@@ -237,12 +249,6 @@ int embla_decode_step_int8(const void* qkv, int q_off, int k_off, int v_off, con
     a.pos = pos;
     a.norm_k = norm_k ? 1 : 0;
     return launch_full_decode(a, stream);
-}
-
-int embla_stream_read(const void* p, size_t bytes, uint32_t* sink, int grid, hipStream_t stream) {
-    if (!p || !sink || bytes == 0 || bytes % 16 || ((uintptr_t)p & 15) || grid <= 0 || grid > 65536)
-        return EMBLA_ERR_INVALID;
-    return launch_stream_read(p, bytes, sink, grid, stream);
 }
 
 int embla_q_prep(const void* qraw, const void* g1, const void* g2, int ng, int stride, int T,

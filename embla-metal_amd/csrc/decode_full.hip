@@ -168,12 +168,8 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
         if constexpr (QR) {
             // the head norm of common.metal:13-26 (q_prep's): x * rms * (1 + g1) * (1 + g2),
             // rounded to bf16; the lane groups g = 0..3 hold dims 32 g .. 32 g + 31
-            float ss = 0.0f;
-#pragma unroll
-            for (int d = 0; d < 32; d++) ss += qf[d] * qf[d];
-            ss += shfl_xor(ss, 16);
-            ss += shfl_xor(ss, 32);
-            const float rf = 1.0f / sqrtf(ss / 128.0f + 1.1920929e-07f);
+#pragma clang fp contract(off)
+            const float rf = 1.0f / sqrtf(sumsq_grouped32(qf) / 128.0f + EPS32);
             u4_t ga[4], gb[4];
 #pragma unroll
             for (int u = 0; u < 4; u++) {

@@ -13,6 +13,7 @@
 // decode_merge_kernel (decode_full.hip).
 #include "common.hpp"
 #include "embla_internal.hpp"
+#include "kv_row.hpp"
 
 namespace embla {
 
@@ -24,9 +25,6 @@ __device__ __forceinline__ f4_t mfma16x(u4_t a, u4_t b, f4_t c) {
     if constexpr (BF) return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8_t, a), __builtin_bit_cast(b8_t, b), c, 0, 0, 0);
     else return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, a), __builtin_bit_cast(h8_t, b), c, 0, 0, 0);
 }
-
-/// RoPE frequency f_d = 10000^(-d/32), the fp32 nearest to the exact value.
-__device__ __forceinline__ float rope_freq(int d) { return (float)exp2(-(double)d / 32.0 * 13.287712379549449); }
 
 /// Prepared row (norm with gains, RoPE, bf16 rounding when PREOPS), dims 32g .. 32g + 31 of a head
 /// held by the 4 lanes n, n+16, n+32, n+48 (lane group g), as fp32 in x[32].
@@ -42,12 +40,8 @@ __device__ __forceinline__ void prep_row(const uint16_t* src, const uint16_t* ga
         }
     }
     if constexpr (PREOPS) {
-        float ss = 0.0f;
-#pragma unroll
-        for (int d = 0; d < 32; d++) ss += x[d] * x[d];
-        ss += shfl_xor(ss, 16);
-        ss += shfl_xor(ss, 32);
-        const float r = 1.0f / sqrtf(ss / 128.0f + 1.1920929e-07f);
+#pragma clang fp contract(off)
+        const float r = 1.0f / sqrtf(sumsq_grouped32(x) / 128.0f + EPS32);
 #pragma unroll
         for (int d = 0; d < 32; d++) x[d] = x[d] * (r * (1.0f + bf2f(gain[32 * g + d])));
         // rotate dims (d, d + 32), d < 32: lane group 0 holds d, group 1 holds d + 32
@@ -55,9 +49,8 @@ __device__ __forceinline__ void prep_row(const uint16_t* src, const uint16_t* ga
         for (int d = 0; d < 32; d++) {
             const float other = shfl_xor(x[d], 16);
             if (g < 2) {
-                const float th = -(float)pos * rope_freq(d);
-                float sn, cs;
-                sincosf(th, &sn, &cs);
+                float cs, sn;
+                rope_cs(pos, d, cs, sn);
                 x[d] = g == 0 ? x[d] * cs - other * sn : other * sn + x[d] * cs;
             }
         }

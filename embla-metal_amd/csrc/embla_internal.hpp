@@ -33,6 +33,10 @@ struct FullDecodeArgs {
     int norm_k = 0;
 };
 int launch_full_decode(const FullDecodeArgs& a, hipStream_t st);
+/// Validates embla_decode_int8's arguments and fills a (chunking included) except a.part;
+/// rc != 0 on a bad argument (api.cpp).
+int full_decode_plan(const void* q, const void* kc, const void* vc, void* o, float* scores, int S, int max_s, int n_q,
+                     int n_kv, int weights, int scale_dtype, int out_dtype, int chunk, FullDecodeArgs& a);
 /// The new token's append and partial as the kernel's extra workgroup reads them.
 struct DecodeAppend {
     const uint16_t* k;
@@ -207,7 +211,6 @@ struct BlockCopyArgs {
     int save;          // cache -> stored, else stored -> cache
 };
 int launch_block_copy(const BlockCopyArgs& a, hipStream_t st);
-int launch_stream_read(const void* p, size_t bytes, uint32_t* sink, int grid, hipStream_t st);
 
 /// The 4-bit projections (gemv_q4.hip): stacked segments, as gemv.metal's Seg.
 constexpr int kMaxGemvSegs = 8;

@@ -83,8 +83,8 @@ __global__ __launch_bounds__(64) void ring_append_kernel(RingAppendArgs a) {
         if (lane < 32) {
             const int d0 = (2 * lane) & 31;
             float s0, c0, s1, c1;
-            sincosf(-(float)pos * (float)exp2(-(double)d0 / 32.0 * 13.287712379549449), &s0, &c0);
-            sincosf(-(float)pos * (float)exp2(-(double)(d0 + 1) / 32.0 * 13.287712379549449), &s1, &c1);
+            rope_cs(pos, d0, c0, s0);
+            rope_cs(pos, d0 + 1, c1, s1);
             if (lane < 16) { x0 = x0 * c0 - o0 * s0; x1 = x1 * c1 - o1 * s1; }
             else { x0 = o0 * s0 + x0 * c0; x1 = o1 * s1 + x1 * c1; }
         }

@@ -31,6 +31,42 @@ __device__ __forceinline__ float rms_factor(float x0, float x1) {
     return 1.0f / sqrtf(ss / 128.0f + EPS32);
 }
 
+/// Σx² of a head row whose lane (n, g = lane >> 4) holds dims 32g .. 32g + 31 in x[32] (every lane
+/// of a group n holds the same row): the same value, bit for bit, as rms_factor's butterfly over
+/// dim pairs (2l, 2l + 1). Pair l = 16g + i is this lane's i; the butterfly's levels xor 32 and 16
+/// cross lane groups (lane xor 32, 16), the levels 8 .. 1 stay inside the lane.
+__device__ __forceinline__ float sumsq_grouped32(const float* x) {
+#pragma clang fp contract(off)
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const float a = x[2 * i] * x[2 * i], b = x[2 * i + 1] * x[2 * i + 1];
+        v[i] = a + b;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = v[i] + shfl_xor(v[i], 32);
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = v[i] + shfl_xor(v[i], 16);
+#pragma unroll
+    for (int m = 8; m >= 1; m >>= 1)
+#pragma unroll
+        for (int i = 0; i < m; i++) v[i] = v[i] + v[i + m];
+    return v[0];
+}
+
+/// RoPE's cosine and sine for dim d (< 32) at position pos (common.metal:39-47), with the rounding
+/// the oracle fixes: f_d = 10000^(-d/32) rounded to fp32, theta = -(float)pos * f_d in fp32, then
+/// cos and sin of that theta evaluated in fp64 and rounded to fp32.
+__device__ __forceinline__ void rope_cs(int pos, int d, float& c, float& s) {
+#pragma clang fp contract(off)
+    const float f = (float)exp2(-(double)d / 32.0 * 13.287712379549449);
+    const float th = -(float)pos * f;
+    double sd, cd;
+    sincos((double)th, &sd, &cd);
+    c = (float)cd;
+    s = (float)sd;
+}
+
 /// Quantises a row held two dims a lane (x0, x1 = dims 2 lane, 2 lane + 1): the int8 pair and the
 /// row's absmax a (scale a / 127).
 __device__ __forceinline__ float quant_pair(float x0, float x1, bool norm, bool round_bf, int& q0, int& q1) {

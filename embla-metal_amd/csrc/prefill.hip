@@ -18,6 +18,7 @@
 // global loads are in flight while the current ones are multiplied.
 #include "common.hpp"
 #include "embla_internal.hpp"
+#include "kv_row.hpp"
 
 #include <type_traits>
 
@@ -221,6 +222,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
 #pragma unroll
         for (int s = 0; s < 8; s++) qb[s] = ld16(qr + 16 * s + 8 * h);
         if constexpr (PRE) {
+#pragma clang fp contract(off)
             // head_norm with the q gains, RoPE at the row's position, bf16 (attn_sliding8_b,
             // prefill.metal:450-456): the row's dims are split over lanes h = 0, 1 (xor 32); the
             // rotation pairs d and d + 32 (d < 32) sit in the same lane (k-steps s and s + 2)
@@ -232,11 +234,24 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
                     x[8 * s + 2 * i] = bf2f(qb[s][i] & 0xFFFF);
                     x[8 * s + 2 * i + 1] = bf2f(qb[s][i] >> 16);
                 }
-            float ss = 0.0f;
+            // Σx² in rms_factor's butterfly over dim pairs (2l, 2l + 1): pair l = 8s + 4h + i
+            // is this lane's (s, i); level 4 (h) crosses to lane xor 32, the others stay here
+            float v[32];
 #pragma unroll
-            for (int e = 0; e < 64; e++) ss += x[e] * x[e];
-            ss += shfl_xor(ss, 32);
-            const float rn = 1.0f / sqrtf(ss / 128.0f + 1.1920929e-07f);
+            for (int e = 0; e < 32; e++) {
+                const float p0 = x[2 * e] * x[2 * e], p1 = x[2 * e + 1] * x[2 * e + 1];
+                v[e] = p0 + p1;
+            }
+#pragma unroll
+            for (int m = 16; m >= 4; m >>= 1)   // pair levels 32, 16, 8: s ^ 4, s ^ 2, s ^ 1
+#pragma unroll
+                for (int e = 0; e < m; e++) v[e] = v[e] + v[e + m];
+#pragma unroll
+            for (int e = 0; e < 4; e++) v[e] = v[e] + shfl_xor(v[e], 32);
+            v[0] = v[0] + v[2];
+            v[1] = v[1] + v[3];
+            v[0] = v[0] + v[1];
+            const float rn = 1.0f / sqrtf(v[0] / 128.0f + EPS32);
 #pragma unroll
             for (int s = 0; s < 8; s++)
 #pragma unroll
@@ -247,7 +262,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
                 for (int e = 0; e < 8; e++) {
                     const int d = 16 * s + 8 * h + e;   // < 32, partner d + 32 at k-step s + 2
                     float sn, cs;
-                    sincosf(-(float)pos * (float)exp2(-(double)d / 32.0 * 13.287712379549449), &sn, &cs);
+                    rope_cs(pos, d, cs, sn);
                     const float x1 = x[8 * s + e], x2 = x[8 * (s + 2) + e];
                     x[8 * s + e] = x1 * cs - x2 * sn;
                     x[8 * (s + 2) + e] = x1 * sn + x2 * cs;

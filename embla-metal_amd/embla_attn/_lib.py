@@ -68,7 +68,6 @@ SIGNATURES = {
     "embla_gemm_q4": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp]),
     "embla_sample_workspace_bytes": (sz, [i32]),
     "embla_q_prep_b": (i32, [vp, vp, vp, vp, i32, vp]),
-    "embla_stream_read": (i32, [vp, sz, vp, i32, vp]),
     "embla_decode_step_int8": (i32, [vp, i32, i32, i32, vp, vp, i32, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32,
                                      vp, sz, vp]),
     "embla_decode_int8_partials": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32, vp, sz, vp]),

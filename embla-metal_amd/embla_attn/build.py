@@ -16,6 +16,8 @@ INCLUDE = PKG.parent.parent / "include"
 LIB = PKG / "libembla_attn.so"
 HOST = PKG.parent / "host"
 HOST_LIB = PKG / "libembla_host.so"
+PROBE = PKG.parent / "probe"
+PROBE_LIB = PKG / "libembla_probe.so"
 OBJ = PKG.parent / "_build"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -54,8 +56,9 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, LIB)
     build_host()
+    build_probe()
     if verbose:
-        print(f"built {LIB} from {len(srcs)} sources, and {HOST_LIB.name}")
+        print(f"built {LIB} from {len(srcs)} sources, {HOST_LIB.name} and {PROBE_LIB.name}")
     return LIB
 
 
@@ -70,6 +73,18 @@ def build_host() -> Path:
         raise RuntimeError(f"host library build failed:\n{r.stderr}")
     os.replace(tmp, HOST_LIB)
     return HOST_LIB
+
+
+def build_probe() -> Path:
+    """The bench-only bandwidth probe (probe/*.hip) as its own libembla_probe.so: bench.py's read
+    floor uses it; the attention library does not contain it."""
+    tmp = PROBE_LIB.with_suffix(".so.tmp")
+    cmd = [HIPCC, *FLAGS, "-shared", "-x", "hip", *map(str, sorted(PROBE.glob("*.hip"))), "-o", str(tmp)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"probe library build failed:\n{r.stderr}")
+    os.replace(tmp, PROBE_LIB)
+    return PROBE_LIB
 
 
 if __name__ == "__main__":

@@ -5,6 +5,7 @@ library's.
 from __future__ import annotations
 
 import ctypes as C
+from pathlib import Path
 
 import torch
 
@@ -12,6 +13,9 @@ from . import _lib
 from ._lib import BF16, F16, F32, RELU2_SINK, SOFTMAX, call, lib
 
 _DT = {F16: torch.float16, BF16: torch.bfloat16}
+
+
+_PROBE = None
 
 
 def _p(t):
@@ -64,9 +68,24 @@ def decode_int8_merge(out, S, max_s, n_kv, ws: Workspace, weights=SOFTMAX, out_d
     return out
 
 
-def stream_read(buf, sink, grid=1024, stream=None):
-    """One streaming read of buf (a bandwidth probe); sink: int32 [grid]."""
-    call("embla_stream_read", _p(buf), buf.numel() * buf.element_size(), _p(sink), grid, stream_handle(stream))
+def stream_read(buf, sink, grid=1024, depth=4, mode=0, stream=None):
+    """One streaming read of buf by the bench-only probe library (libembla_probe.so); sink: int32
+    [grid]; depth 16-byte loads in flight a thread (4, 8, 16, 32); mode 0: into registers, grid-
+    strided; 1: into LDS; 2: into registers, a contiguous slice a workgroup."""
+    global _PROBE
+    if _PROBE is None:
+        path = Path(__file__).resolve().parent / "libembla_probe.so"
+        if not path.exists():
+            raise RuntimeError(f"{path} is not built (embla_attn.build.build())")
+        _PROBE = C.CDLL(str(path))
+        _PROBE.embla_probe_stream_read.restype = C.c_int
+        _PROBE.embla_probe_stream_read.argtypes = [C.c_void_p, C.c_size_t, C.c_void_p, C.c_int, C.c_int, C.c_int,
+                                                   C.c_void_p]
+    rc = _PROBE.embla_probe_stream_read(_p(buf), buf.numel() * buf.element_size(), _p(sink), grid, depth, int(mode),
+                                        stream_handle(stream))
+    if rc != 0:
+        raise RuntimeError(f"embla_probe_stream_read failed ({rc})")
+
 
 
 def decode_step_int8(qkv, q_off, k_off, v_off, kc, vc, pos, max_s, n_q, n_kv, ws: Workspace, g1=None, g2=None,

@@ -280,11 +280,6 @@ int embla_decode_step_int8(const void* qkv, int q_off, int k_off, int v_off, con
                            void* kc, void* vc, void* o, int pos, int max_s, int n_q, int n_kv, int scale_dtype,
                            int norm_k, int out_dtype, int chunk, void* ws, size_t ws_bytes, hipStream_t stream);
 
-/* A bandwidth probe, no counterpart in the reference: reads `bytes` (a multiple of 16, p 16-byte
- * aligned) once with `grid` workgroups and writes one word a workgroup to sink[grid]. It times the
- * plain read of a decode layer's bytes in one launch, the practical floor of the split-K pass. */
-int embla_stream_read(const void* p, size_t bytes, uint32_t* sink, int grid, hipStream_t stream);
-
 /* Query preparation (head_norm with ng gains + bf16 rounding; attention.metal:167-169,
  * prefill.metal:406-426): qraw bf16 rows of `stride` elements, n_q heads, T tokens ->
  * out [T][n_q][128] in out_dtype. */

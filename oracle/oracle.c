@@ -160,6 +160,9 @@ void orc_decode_int8(const float* q, const int8_t* K, const float* ks, const int
     const float scale = 1.0f / sqrtf((float)HD);
     if (scores)
         for (int i = 0; i < n_kv * S_cache; i++) scores[i] = -INFINITY;
+    /* heads are independent (the OpenMP build splits them over threads; with scores, whose
+     * maxima several heads update, it stays serial) */
+#pragma omp parallel for schedule(static) if (!scores)
     for (int h = 0; h < n_q; h++) {
         const int kvh = h / gq;
         const float* qh = q + (size_t)h * HD;
@@ -205,6 +208,7 @@ void orc_decode_rows(const float* q, const float* K, const float* V, int S_cache
                      const int32_t* pos_list, int n, int per_head, float* out) {
     const int gq = n_q / n_kv;
     const float scale = 1.0f / sqrtf((float)HD);
+#pragma omp parallel for schedule(static)
     for (int h = 0; h < n_q; h++) {
         const int kvh = h / gq;
         const int32_t* pl = pos_list + (per_head ? (size_t)kvh * n : 0);
@@ -270,6 +274,7 @@ void orc_index_scores(const uint16_t* qi, const float* w, const uint16_t* ki, in
                       float* out) {
     float qf[16 * 64];
     for (int i = 0; i < n_ih * 64; i++) qf[i] = orc_f16_to_f32(qi[i]);
+#pragma omp parallel for schedule(static)
     for (int j = 0; j < n; j++) {
         float kf[64];
         for (int d = 0; d < 64; d++) kf[d] = orc_f16_to_f32(ki[(size_t)j * 64 + d]);
@@ -303,6 +308,7 @@ void orc_prefill_int8(const float* q, const int8_t* K, const float* ks, const in
                       const uint32_t* rows_sel, int nsel, float* out) {
     const int gq = n_q / n_kv;
     const float scale = 1.0f / sqrtf((float)HD);
+#pragma omp parallel for schedule(dynamic)
     for (int i = 0; i < T; i++) {
         const int pos = p0 + i;
         const int lo = window > 0 ? (pos - window + 1 > 0 ? pos - window + 1 : 0) : 0;

@@ -11,7 +11,9 @@ import numpy as np
 
 HERE = Path(__file__).resolve().parent
 LIB = HERE / "liborc.so"
+LIB_OMP = HERE / "liborc_omp.so"
 _lib = None
+_path = LIB
 
 P = np.ctypeslib.ndpointer
 
@@ -21,12 +23,20 @@ def build() -> Path:
     return LIB
 
 
+def use_openmp(on: bool = True) -> None:
+    """Switches this module to liborc_omp.so (the same source at -O3 -march=native with OpenMP
+    threads; the same results), the build bench.py times as the CPU baseline."""
+    global _lib, _path
+    _path = LIB_OMP if on else LIB
+    _lib = None
+
+
 def lib() -> C.CDLL:
     global _lib
     if _lib is None:
-        if not LIB.exists():
+        if not _path.exists():
             build()
-        L = C.CDLL(str(LIB))
+        L = C.CDLL(str(_path))
         f32 = P(np.float32, flags="C")
         i8 = P(np.int8, flags="C")
         u16 = P(np.uint16, flags="C")

@@ -83,14 +83,34 @@ def c2_window(orc, synth):
     return dict(out=out.astype(np.float32), digest=digest(K, V, q))
 
 
+def c5_sparse_selection(orc, synth, rows=None):
+    """C5 sparse at full size (seed 4, p0 = 30720, T = 2048): for every row t, the SHA-256 of the
+    1152 selected positions (u32, select_keys' order) over the index scores of its keys
+    [0, p0 + t + 1 - 128). rows: only those rows (the others' digests stay empty), for a quick
+    re-derivation."""
+    p0, T = 30720, 2048
+    c = synth.sparse_prefill_case(seed=4, p0=p0, T=T)
+    out = np.zeros((T, 32), np.uint8)
+    for t in range(T) if rows is None else rows:
+        S = p0 + t + 1
+        sc = orc.index_scores(c["qi"][t], c["w"][t], c["ki"][:S - 128])
+        sel = orc.select_keys(np.concatenate([sc, np.zeros(128, np.float32)]), S).astype(np.uint32)
+        out[t] = np.frombuffer(hashlib.sha256(sel.tobytes()).digest(), np.uint8)
+    return dict(row_sha256=out, digest=digest(c["qi"], c["w"], c["ki"]))
+
+
 FIXTURES = {"c1_decode": c1_decode, "c4_select_4k": c4_select, "quant_rows": quant_rows,
-            "c5_prefill_small": c5_prefill, "c2_window_small": c2_window}
+            "c5_prefill_small": c5_prefill, "c2_window_small": c2_window,
+            "c5_sparse_selection": c5_sparse_selection}
 
 
 def main():
     import orc
     from embla_attn import synth
+    only = sys.argv[1:]
     for name, fn in FIXTURES.items():
+        if only and name not in only:
+            continue
         d = fn(orc, synth)
         np.savez_compressed(HERE / f"{name}.npz", **d)
         print(name, {k: (v.shape if hasattr(v, "shape") else v) for k, v in d.items()})

@@ -53,3 +53,13 @@ def upload_int8_case(c, max_s, scale_dtype=np.uint16):
     kreg = layout.pack_region(c["K"], c["ks"].astype(scale_dtype) if scale_dtype != np.uint16 else c["ks"], max_s, "k")
     vreg = layout.pack_region(c["V"], c["vs"].astype(scale_dtype) if scale_dtype != np.uint16 else c["vs"], max_s, "v")
     return dev(kreg), dev(vreg)
+
+
+def chunk_rows(T=2048, block=32):
+    """Rows of a prefill chunk to check at full size: one edge row of every `block`-row tile
+    (first rows of even tiles, last rows of odd ones), both edges of the chunk and of its halves:
+    at least T / block rows, every tile boundary touched."""
+    rows = {0, 1, T // 2 - 1, T // 2, T - 2, T - 1}
+    for b in range(T // block):
+        rows.add(block * b if b % 2 == 0 else block * b + block - 1)
+    return sorted(r for r in rows if r < T)

@@ -124,11 +124,3 @@ def test_decode_step_rejects_bad_arguments():
     assert step(scale=2) == _lib.EMBLA_ERR_UNSUPPORTED         # fp32 scales: no instance
     assert step(n_q=32, wb=L.embla_workspace_bytes(1024, 32)) == _lib.EMBLA_ERR_UNSUPPORTED   # 8 q heads a kv head
 
-
-def test_stream_read_rejects_bad_arguments():
-    L = _lib.lib()
-    d = C.c_void_p(256)
-    assert L.embla_stream_read(d, 100, d, 64, None) == _lib.EMBLA_ERR_INVALID        # not a multiple of 16
-    assert L.embla_stream_read(C.c_void_p(264), 1024, d, 64, None) == _lib.EMBLA_ERR_INVALID   # misaligned
-    assert L.embla_stream_read(d, 1024, None, 64, None) == _lib.EMBLA_ERR_INVALID
-    assert L.embla_stream_read(d, 1024, d, 0, None) == _lib.EMBLA_ERR_INVALID

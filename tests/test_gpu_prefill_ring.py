@@ -4,7 +4,7 @@ import numpy as np
 import pytest
 
 from conftest import gpu_available
-from gpu_util import assert_close, bf16_host, dev, f16_host, say
+from gpu_util import assert_close, bf16_host, chunk_rows, dev, f16_host, say
 from embla_attn import layout, synth
 
 pytestmark = pytest.mark.gpu
@@ -84,7 +84,7 @@ def test_prefill_ring_f16(torch_gpu, orc):
 
 def test_prefill_sliding_c5_size_sampled_rows(torch_gpu, orc):
     """C5 sliding at full size: 2048-token chunk after a 30720-token history, window 1024, bf16 ring
-    of 8192; rows sampled across the chunk (first, block edges, last)."""
+    of 8192; the edge rows of every 32-row tile checked."""
     from embla_attn import ops
     torch = torch_gpu
     R, W, p0, T, n_q, n_kv = 8192, 1024, 30720, 2048, 16, 4
@@ -107,7 +107,7 @@ def test_prefill_sliding_c5_size_sampled_rows(torch_gpu, orc):
     o = ops.prefill_sliding(dev(Q, torch.bfloat16), kn, vn, kring, vring, T, p0, R, W, n_kv)
     got = bf16_host(o)
     Kf, Vf, Qf = synth.bf16_val(K), synth.bf16_val(V), synth.bf16_val(Q)
-    for t in [0, 1, 31, 32, 500, 1023, 1024, 1500, 2046, 2047]:
+    for t in chunk_rows(T):
         p = p0 + t
         rows = np.arange(p - W + 1, p + 1, dtype=np.int32) - lo
         ref = orc.decode_rows(Qf[t], Kf, Vf, rows)
@@ -150,12 +150,11 @@ def test_attn_sliding8_b_reference_mode(torch_gpu, orc):
         p = p0 + t
         q = np.stack([prep(qkv[t, h * 128:(h + 1) * 128], qg, p) for h in range(16)])
         ref = orc.decode_rows(q, Kp, synth.bf16_val(Vb), np.arange(p - W + 1, p + 1, dtype=np.int32))
-        assert_close(got[t], ref, atol=4e-3, what=f"ref row {t}")
+        assert_close(got[t], ref, atol=2e-3, what=f"ref row {t}")
     torch.cuda.synchronize()
     got_k = layout.from_tiles(kc.cpu().numpy().view(np.uint16), n_kv, R, "k")
     exp_k = ring_rows(Kb, total, R)
-    # the GPU's norm sums in another order than the oracle: allow one bf16 ulp
-    diff = np.abs(synth.bf16_val(got_k) - synth.bf16_val(exp_k))
-    assert (diff <= np.abs(synth.bf16_val(exp_k)) * 2 ** -7 + 1e-30).all()
+    # the norm's butterfly order and RoPE's rounding are the oracle's: the bytes are equal
+    np.testing.assert_array_equal(got_k, exp_k)
     got_v = layout.from_tiles(vc.cpu().numpy().view(np.uint16), n_kv, R, "v")
     np.testing.assert_array_equal(got_v, ring_rows(Vb, total, R))

@@ -94,9 +94,8 @@ def test_attn_sliding_reference_mode(torch_gpu, orc):
         q = np.stack([prep(raws[pos][h * 128:(h + 1) * 128], qg, pos) for h in range(16)])
         lo = max(0, pos - W + 1)
         ref = orc.decode_rows(q, Kp, synth.bf16_val(Vb), np.arange(lo, pos + 1, dtype=np.int32))
-        assert_close(bf16_host(o), ref, atol=4e-3, what=f"ref step {s}")
+        assert_close(bf16_host(o), ref, atol=2e-3, what=f"ref step {s}")
     got_k = layout.from_tiles(kc.cpu().numpy().view(np.uint16), n_kv, R, "k")
     exp_k = ring_rows(Kb, total, R)
-    # the GPU's norm sums in another order than the oracle: allow one bf16 ulp
-    diff = np.abs(synth.bf16_val(got_k) - synth.bf16_val(exp_k))
-    assert (diff <= np.abs(synth.bf16_val(exp_k)) * 2 ** -7 + 1e-30).all()
+    # the norm's butterfly order and RoPE's rounding are the oracle's: the bytes are equal
+    np.testing.assert_array_equal(got_k, exp_k)

@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 
 from conftest import gpu_available
-from gpu_util import assert_close, bf16_host, dev, say
+from gpu_util import assert_close, bf16_host, chunk_rows, dev, say
 from embla_attn import synth
 from test_gpu_prefill import quant_rows
 
@@ -113,10 +113,19 @@ def test_prefill_sparse_all_equal_band_overflow(torch_gpu, orc):
     check_rows(orc, c, got, idx, range(T), oracle_cache(orc, c))
 
 
-def test_prefill_sparse_c5_size_sampled_rows(torch_gpu, orc):
-    """C5 sparse at full size: 2048 rows after 30720 cached positions; sampled rows checked."""
+def test_prefill_sparse_c5_size_all_rows(torch_gpu, orc):
+    """C5 sparse at full size: 2048 rows after 30720 cached positions. Every row's selection
+    against the SHA-256 of the oracle's (tests/golden/c5_sparse_selection.npz, same seeded
+    inputs); attention outputs and selections re-derived on the edge rows of every 32-row tile."""
+    import hashlib
+    from pathlib import Path
     p0, T = 30720, 2048
     say("prefill sparse C5 size")
     c = synth.sparse_prefill_case(seed=4, p0=p0, T=T)
     got, idx, _, _ = run(torch_gpu, c)
-    check_rows(orc, c, got, idx, [0, 1, 7, 8, 511, 1024, 2046, 2047], oracle_cache(orc, c))
+    want = np.load(Path(__file__).resolve().parent / "golden" / "c5_sparse_selection.npz", allow_pickle=False)
+    gotsha = np.stack([np.frombuffer(hashlib.sha256(idx[t].astype(np.uint32).tobytes()).digest(), np.uint8)
+                       for t in range(T)])
+    bad = np.nonzero((gotsha != want["row_sha256"]).any(1))[0]
+    assert bad.size == 0, f"{bad.size} of {T} rows select differently, first rows {bad[:8].tolist()}"
+    check_rows(orc, c, got, idx, chunk_rows(T), oracle_cache(orc, c))
