@@ -72,6 +72,8 @@ SIGNATURES = {
                                      vp, sz, vp]),
     "embla_decode_int8_partials": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32, vp, sz, vp]),
     "embla_decode_int8_merge": (i32, [vp, i32, i32, i32, i32, i32, i32, i32, vp, sz, vp]),
+    "embla_decode_int8_noalloc": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32, vp]),
+    "embla_decode_int8_noalloc_max_bytes": (sz, []),
     "embla_decode_int8_qraw": (i32, [vp, vp, vp, i32, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp, sz, vp]),
     "embla_argmax": (i32, [vp, vp, i32, vp, i32, i32, vp, sz, vp]),
     "embla_sample": (i32, [vp, vp, i32, vp, i32, i32, C.c_float, C.c_float, C.c_uint32, vp, sz, vp]),

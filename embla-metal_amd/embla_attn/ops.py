@@ -54,6 +54,17 @@ def decode_int8(q, kc, vc, S, max_s, n_kv, weights=SOFTMAX, scale_dtype=F16, out
     return out
 
 
+def decode_int8_noalloc(q, kc, vc, S, max_s, n_kv, weights=SOFTMAX, scale_dtype=F16, out_dtype=F16, chunk=0,
+                        scores=None, out=None, stream=None):
+    """decode_int8 with its partials in the library's own device array (no workspace argument)."""
+    n_q = q.shape[0]
+    if out is None:
+        out = torch.empty((n_q, 128), dtype=_DT[out_dtype], device=q.device)
+    call("embla_decode_int8_noalloc", _p(q), _p(kc), _p(vc), _p(out), _p(scores), S, max_s, n_q, n_kv,
+         weights, scale_dtype, out_dtype, chunk, stream_handle(stream))
+    return out
+
+
 def decode_int8_partials(q, kc, vc, S, max_s, n_kv, ws: Workspace, weights=SOFTMAX, scale_dtype=F16, out_dtype=F16,
                          chunk=0, scores=None, stream=None):
     """The split-K kernel of decode_int8 alone: chunk partials left in ws."""

@@ -91,6 +91,18 @@ int embla_decode_int8_partials(const void* q, const void* kc, const void* vc, fl
 int embla_decode_int8_merge(void* o, int S, int max_s, int n_q, int n_kv, int weights, int out_dtype, int chunk,
                             void* ws, size_t ws_bytes, hipStream_t stream);
 
+/* embla_decode_int8 without a workspace argument, for callers that cannot allocate (code under
+ * HIP graph capture, serving loops or harnesses that forbid hipMalloc). No counterpart in the
+ * reference. The split-K partials go to a file-scope device array of
+ * embla_decode_int8_noalloc_max_bytes() bytes (4.125 MiB: C chunks x n_q x 528 B must fit, or the
+ * call returns EMBLA_ERR_WORKSPACE). The call allocates nothing; each GPU holds one array for the
+ * life of the process, resolved on that GPU's first call. Calls that overlap on one GPU (other
+ * streams or threads) share that array and race; calls ordered on one stream do not. */
+int embla_decode_int8_noalloc(const void* q, const void* kc, const void* vc, void* o, float* scores, int S,
+                              int max_s, int n_q, int n_kv, int weights, int scale_dtype, int out_dtype,
+                              int chunk, hipStream_t stream);
+size_t embla_decode_int8_noalloc_max_bytes(void);
+
 /* Reference-signature full layer (attn_full8, attention.metal:235-363; bound at Engine.swift:
  * 800-818): raw bf16 q [16][128] normed with p->ng gains g1, g2 (common.metal:13-26) and rounded
  * to bf16, ReLU² with sink over the int8 cache of 2 kv heads with fp32 scales; o bf16 [16][128].

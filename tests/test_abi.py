@@ -124,3 +124,17 @@ def test_decode_step_rejects_bad_arguments():
     assert step(scale=2) == _lib.EMBLA_ERR_UNSUPPORTED         # fp32 scales: no instance
     assert step(n_q=32, wb=L.embla_workspace_bytes(1024, 32)) == _lib.EMBLA_ERR_UNSUPPORTED   # 8 q heads a kv head
 
+
+def test_decode_noalloc_rejects_beyond_its_array():
+    """The zero-allocation decode keeps its partials in a fixed device array: a call whose chunks
+    would not fit is refused on the host, before any HIP call."""
+    L = _lib.lib()
+    cap = L.embla_decode_int8_noalloc_max_bytes()
+    assert cap == 256 * 32 * 132 * 4
+    d = C.c_void_p(16)
+    # 256 chunks of 512 keys x 64 query heads x 528 B = 8.6 MB > 4.1 MB
+    rc = L.embla_decode_int8_noalloc(d, d, d, d, None, 131072, 131072, 64, 16, 0, 0, 0, 512, None)
+    assert rc == _lib.EMBLA_ERR_WORKSPACE
+    rc = L.embla_decode_int8_noalloc(d, d, d, d, None, 2000, 1024, 16, 4, 0, 0, 0, 0, None)
+    assert rc == _lib.EMBLA_ERR_INVALID
+    assert L.embla_decode_int8_noalloc(None, d, d, d, None, 10, 1024, 16, 4, 0, 0, 0, 0, None) == _lib.EMBLA_ERR_INVALID
