@@ -416,7 +416,8 @@ def bench_c5(torch, reps=10):
                        8, reps, 2)
     ms_sla = time_calls(torch, lambda: ops.prefill_ring(q, kring, vring, T, p0, R, W, n_kv, out=out, ws=ws), 8, reps, 2)
     sliding = dict(window=W, ring=R, gflop=sflops / 1e9, ms_attention=ms_sla,
-                   tflops_attention=sflops / (ms_sla * 1e-3) / 1e12, ms_fused=ms_sl,
+                   tflops_attention=sflops / (ms_sla * 1e-3) / 1e12,
+                   mfma_util_attention=sflops / (ms_sla * 1e-3) / 2.5e15, ms_fused=ms_sl,
                    tokens_per_s=T / (ms_sl * 1e-3))
     # sparse layer: the same chunk, per-row top-1024 + latest 128 by the index score, over a
     # row-major int8 cache (quantise-and-append, MFMA indexer, exact band select, gathered attention)
@@ -434,7 +435,8 @@ def bench_c5(torch, reps=10):
     att = 4.0 * 128 * 16 * T * 1152
     idxf = 4.0 * 128 * sum(p0 + t + 1 - 128 for t in range(T))
     sparse = dict(gflop_attention=att / 1e9, gflop_indexer=idxf / 1e9, ms_layer=ms_sp,
-                  tflops_layer=(att + idxf) / (ms_sp * 1e-3) / 1e12, tokens_per_s=T / (ms_sp * 1e-3))
+                  tflops_layer=(att + idxf) / (ms_sp * 1e-3) / 1e12,
+                  mfma_util_layer=(att + idxf) / (ms_sp * 1e-3) / 2.5e15, tokens_per_s=T / (ms_sp * 1e-3))
     return dict(full, sliding=sliding, sparse=sparse)
 
 

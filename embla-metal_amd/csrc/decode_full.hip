@@ -59,6 +59,10 @@ __device__ __forceinline__ void scales8(const u4_t* r, float* out) {
     }
 }
 
+// K and V tile rows are read once: nontemporal loads (9.86 -> 9.40 us a split-K launch at 32k,
+// 14.17 -> 13.55 us a layer, two A/B pairs on one box)
+#define TLD(p) ld16_stream(p)
+
 constexpr int DW = 8;            // waves a workgroup: one 32-key tile each a round
 
 /// The decode step's own append (workgroup C of each kv head): waves 0 and 1 quantise the new
@@ -212,7 +216,7 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
     auto load_k_scales = [&](int t0, Tile8& T) {
         const int8_t* pk = kc + tile_base(kvh, max_s, t0, 1) + lane * 16;
 #pragma unroll
-        for (int j = 0; j < 4; j++) T.k[j] = ld16(pk + 1024 * j);
+        for (int j = 0; j < 4; j++) T.k[j] = TLD(pk + 1024 * j);
 #pragma unroll
         for (int t = 0; t < 2; t++) {
             const size_t si = ((size_t)kvh * max_s + t0 + 16 * t + 4 * g) * ES;
@@ -244,7 +248,7 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
         if (nxt >= 0) {   // K is consumed: the next tile's K rows and scales go out now
             const int8_t* pk = kc + tile_base(kvh, max_s, nxt, 1) + lane * 16;
 #pragma unroll
-            for (int j = 0; j < 4; j++) T.k[j] = ld16(pk + 1024 * j);
+            for (int j = 0; j < 4; j++) T.k[j] = TLD(pk + 1024 * j);
 #pragma unroll
             for (int t = 0; t < 2; t++) {
                 const size_t si = ((size_t)kvh * max_s + nxt + 16 * t + 4 * g) * ES;
@@ -337,7 +341,7 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
         if (nxt >= 0) {   // V and its scales are consumed: the next tile's go out now
             const int8_t* pv = vc + tile_base(kvh, max_s, nxt, 1) + lane * 16;
 #pragma unroll
-            for (int j = 0; j < 4; j++) T.v[j] = ld16(pv + 1024 * j);
+            for (int j = 0; j < 4; j++) T.v[j] = TLD(pv + 1024 * j);
 #pragma unroll
             for (int t = 0; t < 2; t++) {
                 const size_t si = ((size_t)kvh * max_s + nxt + 16 * t + 4 * g) * ES;
@@ -361,7 +365,7 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
         if (t0 < j1) {
             const int8_t* pv = vc + tile_base(kvh, max_s, t0, 1) + lane * 16;
 #pragma unroll
-            for (int j = 0; j < 4; j++) A.v[j] = ld16(pv + 1024 * j);
+            for (int j = 0; j < 4; j++) A.v[j] = TLD(pv + 1024 * j);
         }
         // each tile's K (and K scales) for the next tile go out as soon as the score MFMAs have
         // consumed them, its V (and V scales) after the P·V MFMAs: 10.41 -> 9.92 µs a launch at 32k
