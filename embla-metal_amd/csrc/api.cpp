@@ -111,6 +111,34 @@ int full_decode_args(const void* q, const void* kc, const void* vc, void* o, flo
     return EMBLA_OK;
 }
 
+/// The bf16-cache decode of the reference's full (ReLU², optional scores) and sparse (softmax,
+/// optional SEL rows) layers: 16 query heads over 2 kv heads, part as the workspace.
+int attn16(const void* qraw, const void* g1, const void* g2, const void* kc, const void* vc, float* part,
+           float* scores, const uint32_t* idx, uint32_t* counter, void* o, const EmblaAttnParams* p, bool relu2,
+           hipStream_t stream) {
+    if (!p || !part || !counter || !kc || !vc || !o) return EMBLA_ERR_INVALID;
+    if (p->S <= 0 || p->maxS <= 0 || p->maxS % 32 || p->S > p->maxS) return EMBLA_ERR_INVALID;
+    if (!qraw || p->ng < 0 || p->ng > 2 || (p->ng >= 1 && !g1) || (p->ng >= 2 && !g2)) return EMBLA_ERR_INVALID;
+    (void)counter;   // no counters: the partials are merged by a second kernel
+    int ch = p->CH;
+    if (ch <= 0) {   // about 256 workgroups over the 2 kv heads, a 32-key tile a wave at least
+        ch = (p->S + 127) / 128;
+        ch = (ch + 31) / 32 * 32;
+        if (ch < 128) ch = 128;
+    }
+    if (ch % 32 || (p->S + ch - 1) / ch > kMaxChunks) return EMBLA_ERR_INVALID;
+    Full16Args a;
+    a.q = (const uint16_t*)qraw; a.g1 = (const uint16_t*)g1; a.g2 = (const uint16_t*)g2; a.ng = p->ng;
+    a.kc = (const uint16_t*)kc; a.vc = (const uint16_t*)vc;
+    a.idx = idx;
+    a.part = carve(part, p->maxS, 16).part;
+    a.scores = scores;
+    a.o = (uint16_t*)o;
+    a.S = p->S; a.CH = ch; a.C = (p->S + ch - 1) / ch; a.max_s = p->maxS; a.n_q = 16; a.n_kv = 2;
+    a.relu2 = relu2;
+    return launch_full16_decode(a, stream);
+}
+
 }  // namespace
 
 namespace embla {
@@ -292,6 +320,55 @@ int embla_attn_full8(const void* qraw, const void* g1, const void* g2, const voi
     a.S = p->S; a.CH = ch; a.C = (p->S + ch - 1) / ch; a.max_s = p->maxS; a.n_q = 16; a.n_kv = 2;
     a.relu2 = true; a.scale32 = true; a.out_bf16 = true;
     return launch_full_decode(a, stream);
+}
+
+int embla_attn_full(const void* qraw, const void* g1, const void* g2, const void* kc, const void* vc, float* part,
+                    float* scores, uint32_t* counter, void* o, const EmblaAttnParams* p, hipStream_t stream) {
+    return attn16(qraw, g1, g2, kc, vc, part, scores, nullptr, counter, o, p, true, stream);
+}
+
+int embla_attn_sparse(const void* qraw, const void* g1, const void* g2, const void* kc, const void* vc,
+                      float* part, const uint32_t* idx, uint32_t* counter, void* o, const EmblaAttnParams* p,
+                      hipStream_t stream) {
+    return attn16(qraw, g1, g2, kc, vc, part, nullptr, idx, counter, o, p, false, stream);
+}
+
+int embla_kv_append_bf16(const void* qkv, void* cache, const EmblaKVJob* jobs, int njobs, int pm_pos, int maxS, int T,
+                         hipStream_t stream) {
+    if (!qkv || !cache || !jobs || njobs <= 0 || T <= 0 || pm_pos < 0 || maxS <= 0 || maxS % 32) return EMBLA_ERR_INVALID;
+    if (pm_pos + T > maxS) return EMBLA_ERR_INVALID;
+    for (int i = 0; i < njobs; i++) {
+        const EmblaKVJob& j = jobs[i];
+        const uint16_t* base = (const uint16_t*)qkv;
+        uint16_t* c = (uint16_t*)cache;
+        RingAppendArgs a{base + j.k, base + j.v, 4096, T, pm_pos, 2, maxS, c + j.kc, c + j.vc, nullptr};
+        a.norm_k = true;
+        const int rc = launch_ring_append(a, stream);
+        if (rc) return rc;
+    }
+    return EMBLA_OK;
+}
+
+int embla_attn_full_b(const void* qkv, const void* g1, const void* g2, const void* kc, const void* vc, float* part,
+                      uint32_t* counter, void* o, const EmblaAttnB* p, int T, hipStream_t stream) {
+    if (!qkv || !g1 || !g2 || !kc || !vc || !part || !counter || !o || !p || T <= 0) return EMBLA_ERR_INVALID;
+    if (p->p0 < 0 || p->maxS <= 0 || p->maxS % 32 || p->p0 + T > p->maxS) return EMBLA_ERR_INVALID;
+    (void)counter;   // no counters: one pass over every key of a row, no chunk partials
+    // q_prep_b's queries (both gains, bf16) in the part buffer, token-major [T][16][128]; the
+    // ReLU² prefill over the bf16 cache (keys 0 .. p0 + t for row t) on the 16-bit tile path
+    uint16_t* qn = (uint16_t*)part;
+    QPrepArgs qa{(const uint16_t*)qkv, (const uint16_t*)g1, (const uint16_t*)g2, 2, 4096, T, 16, qn, true};
+    int rc = launch_q_prep(qa, stream);
+    if (rc) return rc;
+    PrefillArgs a;
+    a.q = qn; a.q_tok_stride = 16 * 128; a.q_head_stride = 128;
+    a.kc = nullptr; a.vc = nullptr;
+    a.o = (uint16_t*)o; a.o_tok_stride = 2048; a.o_head_stride = 128;
+    a.T = T; a.p0 = p->p0; a.max_s = p->maxS; a.n_q = 16; a.n_kv = 2; a.window = 0;
+    a.nsplit = 1; a.part = nullptr;
+    a.relu2 = true; a.scale32 = false; a.q_bf16 = true; a.out_bf16 = true;
+    a.kring = (const uint16_t*)kc; a.vring = (const uint16_t*)vc; a.R = p->maxS; a.qg = nullptr;
+    return launch_prefill_ring(a, stream);
 }
 
 int embla_attn_sparse8(const void* qraw, const void* g1, const void* g2, const void* kc, const void* vc,

@@ -88,6 +88,13 @@ __device__ __forceinline__ f4_t mfma16bf(b8_t a, b8_t b, f4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+/// 16x16x32 on 16-byte operands holding fp16 (BF = false) or bf16 (BF = true) values.
+template <bool BF>
+__device__ __forceinline__ f4_t mfma16x(u4_t a, u4_t b, f4_t c) {
+    if constexpr (BF) return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8_t, a), __builtin_bit_cast(b8_t, b), c, 0, 0, 0);
+    else return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, a), __builtin_bit_cast(h8_t, b), c, 0, 0, 0);
+}
+
 // ------------------------------------------------------------------ loads
 __device__ __forceinline__ u4_t ld16(const void* p) { return *reinterpret_cast<const u4_t*>(p); }
 __device__ __forceinline__ u2_t ld8(const void* p) { return *reinterpret_cast<const u2_t*>(p); }

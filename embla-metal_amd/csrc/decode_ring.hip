@@ -20,12 +20,6 @@ namespace embla {
 constexpr float RLOG2E = 1.4426950408889634f;
 constexpr int RPS = HD + 4;   // partial record stride, as decode_full.hip
 
-template <bool BF>
-__device__ __forceinline__ f4_t mfma16x(u4_t a, u4_t b, f4_t c) {
-    if constexpr (BF) return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8_t, a), __builtin_bit_cast(b8_t, b), c, 0, 0, 0);
-    else return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, a), __builtin_bit_cast(h8_t, b), c, 0, 0, 0);
-}
-
 /// Prepared row (norm with gains, RoPE, bf16 rounding when PREOPS), dims 32g .. 32g + 31 of a head
 /// held by the 4 lanes n, n+16, n+32, n+48 (lane group g), as fp32 in x[32].
 template <bool BF, bool PREOPS>

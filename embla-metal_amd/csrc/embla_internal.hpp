@@ -194,8 +194,26 @@ struct RingAppendArgs {
     uint16_t* kring;
     uint16_t* vring;
     const uint16_t* kg;      // gains: bf16 pre-ops on K (norm, RoPE); null: copy
+    bool norm_k = false;     // without gains: K RMS-normed (no gains, no RoPE) and rounded to bf16
 };
 int launch_ring_append(const RingAppendArgs& a, hipStream_t st);
+
+/// Decode over a bf16 full-layer cache in the 16-bit tile layout (decode_full16.hip).
+struct Full16Args {
+    const uint16_t* q;       // raw bf16 queries [n_q][128], normed with ng gains in the kernel
+    const uint16_t* g1;
+    const uint16_t* g2;
+    int ng;
+    const uint16_t* kc;      // [n_kv][max_s/32] tiles of 32 x 128 bf16
+    const uint16_t* vc;
+    const uint32_t* idx;     // SEL: rows [n_kv][S]; null: keys 0 .. S-1
+    float* part;             // [C][n_q][132] chunk partials
+    float* scores;           // optional [n_kv][max_s]: max over a kv head's query heads of q·k
+    uint16_t* o;             // bf16 [n_q][128]
+    int S, CH, C, max_s, n_q, n_kv;
+    bool relu2;
+};
+int launch_full16_decode(const Full16Args& a, hipStream_t st);
 
 /// A prefix-cache block copy (blocks.hip): 128 positions of every listed layer's K and V region.
 constexpr int kMaxBlockLayers = 64;

@@ -66,7 +66,9 @@ __global__ __launch_bounds__(64) void q_prep_kernel(QPrepArgs a) {
 
 /// T positions p0 .. of 16-bit K and V rows into a ring (slot p % R, tile layout with ES = 2). With
 /// gains (the reference's sliding layers, kv_sliding_b, prefill.metal:103-125) K is RMS-normed with
-/// them, rotated (RoPE at its position) and rounded to bf16; V is copied. One wave a (token, head).
+/// them, rotated (RoPE at its position) and rounded to bf16; with norm_k (a bf16 full-layer cache,
+/// R = max_s: kv_append / kv_append_b without KV8, attention.metal:113-140, prefill.metal:182-212)
+/// only RMS-normed and rounded; V is copied. One wave a (token, head).
 __global__ __launch_bounds__(64) void ring_append_kernel(RingAppendArgs a) {
     const int lane = threadIdx.x, t = blockIdx.x, h = blockIdx.y;
     const int pos = a.p0 + t, slot = pos % a.R;
@@ -89,6 +91,10 @@ __global__ __launch_bounds__(64) void ring_append_kernel(RingAppendArgs a) {
             else { x0 = o0 * s0 + x0 * c0; x1 = o1 * s1 + x1 * c1; }
         }
         kout = (uint32_t)f2bf(x0) | ((uint32_t)f2bf(x1) << 16);
+    } else if (a.norm_k) {   // bf16 rows of a full layer: RMS norm without gains (kv_append, no KV8)
+        float x0 = bf2f(kraw & 0xFFFF), x1 = bf2f(kraw >> 16);
+        const float r = rms_factor(x0, x1);
+        kout = (uint32_t)f2bf(x0 * r) | ((uint32_t)f2bf(x1 * r) << 16);
     }
     *(uint32_t*)(a.kring + kt_off(h, a.R, slot, 2 * lane, 2) / 2) = kout;
     a.vring[vt_off(h, a.R, slot, 2 * lane, 2) / 2] = (uint16_t)(vraw & 0xFFFF);

@@ -478,6 +478,12 @@ int launch_prefill_ring(const PrefillArgs& a, hipStream_t st) {
     const dim3 grid((a.T + 32 * (PF_WAVES / gq) - 1) / (32 * (PF_WAVES / gq)), a.n_kv, a.nsplit);
 #define EMBLA_PR(BF, PRE) \
     hipLaunchKernelGGL((prefill_int8_kernel<4, false, false, BF, BF, true, BF, PRE>), grid, dim3(64 * PF_WAVES), 0, st, a)
+    if (gq == 8 && a.relu2 && a.q_bf16 && a.out_bf16 && !a.qg && a.window == 0) {
+        // the reference's full layer over a bf16 cache (attn_full_b, prefill.metal:214-282)
+        hipLaunchKernelGGL((prefill_int8_kernel<8, true, false, true, true, true, true, false>), grid, dim3(64 * PF_WAVES),
+                           0, st, a);
+        return launch_prefill_tail(a, st);
+    }
     if (gq != 4 || a.relu2) return EMBLA_ERR_UNSUPPORTED;
     if (a.q_bf16 && a.out_bf16 && a.qg) EMBLA_PR(true, true);
     else if (a.q_bf16 && a.out_bf16) EMBLA_PR(true, false);

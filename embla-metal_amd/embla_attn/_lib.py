@@ -32,6 +32,11 @@ class AttnParams(C.Structure):
     _fields_ = [(n, C.c_int32) for n in ("S", "CH", "C", "maxS", "pos", "ng", "pad0", "pad1")]
 
 
+class AttnB(C.Structure):
+    """Mirrors AttnB (prefill.metal:217)."""
+    _fields_ = [(n, C.c_int32) for n in ("p0", "CH", "C", "maxS")]
+
+
 class KVJob(C.Structure):
     """Mirrors KVJob (attention.metal:108-111)."""
     _fields_ = [(n, C.c_uint32) for n in ("k", "v", "kc", "vc")]
@@ -72,6 +77,10 @@ SIGNATURES = {
                                      vp, sz, vp]),
     "embla_decode_int8_partials": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32, vp, sz, vp]),
     "embla_decode_int8_merge": (i32, [vp, i32, i32, i32, i32, i32, i32, i32, vp, sz, vp]),
+    "embla_kv_append_bf16": (i32, [vp, vp, C.POINTER(KVJob), i32, i32, i32, i32, vp]),
+    "embla_attn_full": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, C.POINTER(AttnParams), vp]),
+    "embla_attn_sparse": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, C.POINTER(AttnParams), vp]),
+    "embla_attn_full_b": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, C.POINTER(AttnB), i32, vp]),
     "embla_decode_int8_noalloc": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32, vp]),
     "embla_decode_int8_noalloc_max_bytes": (sz, []),
     "embla_decode_int8_qraw": (i32, [vp, vp, vp, i32, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp, sz, vp]),

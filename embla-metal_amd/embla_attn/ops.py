@@ -151,6 +151,33 @@ def attn_sparse8(qraw, g1, g2, kc, vc, part, idx, counter, o, S, maxS, ng=2, CH=
          _p(counter), _p(o), C.byref(p), stream_handle(stream))
 
 
+def attn_full(qraw, g1, g2, kc, vc, part, scores, counter, o, S, maxS, ng=2, CH=0, stream=None):
+    """attn_full without KV8 (attention.metal:148-220): bf16 caches in the 16-bit tile layout."""
+    p = _lib.AttnParams(S, CH, 0, maxS, S - 1, ng, 0, 0)
+    call("embla_attn_full", _p(qraw), _p(g1), _p(g2), _p(kc), _p(vc), _p(part), _p(scores),
+         _p(counter), _p(o), C.byref(p), stream_handle(stream))
+
+
+def attn_sparse(qraw, g1, g2, kc, vc, part, idx, counter, o, S, maxS, ng=2, CH=0, stream=None):
+    """attn_sparse without KV8 (attention.metal:370-441): idx None = every key 0 .. S-1."""
+    p = _lib.AttnParams(S, CH, 0, maxS, S - 1, ng, 0, 0)
+    call("embla_attn_sparse", _p(qraw), _p(g1), _p(g2), _p(kc), _p(vc), _p(part), _p(idx),
+         _p(counter), _p(o), C.byref(p), stream_handle(stream))
+
+
+def kv_append_bf16(qkv, cache, jobs, pm_pos, maxS, T=1, stream=None):
+    """kv_append(_b) without KV8: jobs a list of (k, v, kc, vc) element offsets."""
+    arr = (_lib.KVJob * len(jobs))(*[_lib.KVJob(*j) for j in jobs])
+    call("embla_kv_append_bf16", _p(qkv), _p(cache), arr, len(jobs), pm_pos, maxS, T, stream_handle(stream))
+
+
+def attn_full_b(qkv, g1, g2, kc, vc, part, counter, o, p0, T, maxS, stream=None):
+    """attn_full_b (prefill.metal:214-282) over bf16 caches; o bf16 [T][2048]."""
+    p = _lib.AttnB(p0, 0, 0, maxS)
+    call("embla_attn_full_b", _p(qkv), _p(g1), _p(g2), _p(kc), _p(vc), _p(part), _p(counter), _p(o),
+         C.byref(p), T, stream_handle(stream))
+
+
 def sliding_decode(q, k_new, v_new, kring, vring, pos, window, ring, n_kv, dtype=F16, chunk=0,
                    ws: Workspace | None = None, out=None, stream=None):
     """One decode step over a 16-bit ring: appends (k_new, v_new) at pos, attends the window."""

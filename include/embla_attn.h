@@ -50,6 +50,11 @@ typedef struct EmblaAttnParams {
     int32_t S, CH, C, maxS, pos, ng, pad0, pad1;
 } EmblaAttnParams;
 
+/* Mirrors AttnB (prefill.metal:217; Prefill.swift:327-328) field for field. */
+typedef struct EmblaAttnB {
+    int32_t p0, CH, C, maxS;
+} EmblaAttnB;
+
 /* Mirrors KVJob (attention.metal:108-111; Engine.swift:35): element offsets of k and v in qkv
  * and byte offsets of the layer's K and V regions in the cache. */
 typedef struct EmblaKVJob {
@@ -261,6 +266,39 @@ int embla_kv_quant_append(const void* k, const void* v, int in_dtype, int stride
 int embla_attn_sparse8(const void* qraw, const void* g1, const void* g2, const void* kc, const void* vc,
                        float* part, const uint32_t* idx, uint32_t* counter, void* o, const EmblaAttnParams* p,
                        hipStream_t stream);
+
+/* ---------------------------------------------------------------- bf16 full-layer caches
+ * The reference's full and sparse layers without KV8 (EMBLA_KV8=0, Engine.swift:162-163, 223-226,
+ * 278): the caches hold bf16 K and V, `maxS` rows a kv head of 2, in the 16-bit tile layout of the
+ * rings ([2][maxS/32] tiles of 32 x 128 bf16, no scales), the same bytes as the reference's
+ * 2 · maxS · 128 · 2 a region. */
+
+/* kv_append / kv_append_b without KV8 (attention.metal:113-140, prefill.metal:182-212; bound at
+ * Engine.swift:782-793, Prefill.swift:315-322): T tokens of qkv rows (4096 bf16 each, position
+ * pm_pos + t); K RMS-normed without gains and rounded to bf16, V copied; jobs[i].kc / .vc are
+ * ELEMENT offsets of the layer's K and V regions in cache (Engine.swift:457). */
+int embla_kv_append_bf16(const void* qkv, void* cache, const EmblaKVJob* jobs, int njobs, int pm_pos,
+                         int maxS, int T, hipStream_t stream);
+
+/* attn_full without KV8 (attention.metal:148-220; bound at Engine.swift:800-818): as
+ * embla_attn_full8 over bf16 caches; scores (optional) the max over the 8 query heads of q·k. */
+int embla_attn_full(const void* qraw, const void* g1, const void* g2, const void* kc, const void* vc,
+                    float* part, float* scores, uint32_t* counter, void* o, const EmblaAttnParams* p,
+                    hipStream_t stream);
+
+/* attn_sparse without KV8 (attention.metal:370-441): as embla_attn_sparse8 over bf16 caches;
+ * idx NULL: every key 0 .. p->S-1, else the rows idx[kv head][0 .. p->S) gathered from the tiles. */
+int embla_attn_sparse(const void* qraw, const void* g1, const void* g2, const void* kc, const void* vc,
+                      float* part, const uint32_t* idx, uint32_t* counter, void* o, const EmblaAttnParams* p,
+                      hipStream_t stream);
+
+/* attn_full_b (prefill.metal:214-282; bound at Prefill.swift:325-338): T tokens of qkv bf16
+ * [T][4096] at positions p->p0 .., q normed with both gains (g1, g2) and rounded to bf16, ReLU² with
+ * sink over keys 0 .. p->p0 + t of the bf16 caches; o bf16 [T][2048]. part: the reference's part
+ * buffer ([T][C][16][129] fp32, at least T · 16 · 128 · 2 bytes), used for the prepared queries;
+ * p->CH and p->C are not used (one pass over every key of a row); counter is not used. */
+int embla_attn_full_b(const void* qkv, const void* g1, const void* g2, const void* kc, const void* vc,
+                      float* part, uint32_t* counter, void* o, const EmblaAttnB* p, int T, hipStream_t stream);
 
 /* Reference-signature kv_append (attention.metal:113-140 / prefill.metal:182-212, bound at
  * Engine.swift:782-793, Prefill.swift:315-322): T tokens of qkv rows (4096 bf16 each, position

@@ -199,6 +199,54 @@ void orc_decode_int8(const float* q, const int8_t* K, const float* ks, const int
     }
 }
 
+/* ------------------------------------------------------------------ decode over a bf16 cache
+ * The full layers' caches without KV8 (bf16 rows, no scales; the rows passed here as their fp32
+ * values [n_kv][S_cache][128]): attn_full (attention.metal:148-220) with weights 1, ReLU² over
+ * s = q·k: w = relu(s / √128)², o = Σ w·v / (√128 + Σ w), scores (optional, [n_kv][S_cache]) the
+ * max over the kv head's query heads of the raw s (attention.metal:183, 193-202); attn_sparse
+ * (attention.metal:370-441) with weights 0, softmax of s / √128. rows (optional, [n_kv][S]):
+ * attend only those rows (SEL). The same arithmetic as orc_decode_int8 with unit scales. */
+void orc_decode_f32(const float* q, const float* K, const float* V, int S, int S_cache, int n_q, int n_kv,
+                    int weights, const uint32_t* rows, float* out, float* scores) {
+    const int gq = n_q / n_kv;
+    const float scale = 1.0f / sqrtf((float)HD);
+    if (scores)
+        for (int i = 0; i < n_kv * S_cache; i++) scores[i] = -INFINITY;
+#pragma omp parallel for schedule(static) if (!scores)
+    for (int h = 0; h < n_q; h++) {
+        const int kvh = h / gq;
+        const float* qh = q + (size_t)h * HD;
+        float m = -INFINITY, l = 0.0f, acc[HD];
+        memset(acc, 0, sizeof acc);
+        for (int j = 0; j < S; j++) {
+            const size_t r = rows ? rows[(size_t)kvh * S + j] : (size_t)j;
+            const float* kr = K + ((size_t)kvh * S_cache + r) * HD;
+            const float* vr = V + ((size_t)kvh * S_cache + r) * HD;
+            float dot = 0.0f;
+            for (int d = 0; d < HD; d++) dot += qh[d] * kr[d];
+            if (scores) {
+                float* sp = scores + (size_t)kvh * S_cache + r;
+                if (dot > *sp) *sp = dot;
+            }
+            if (weights == 1) {
+                const float a = fmaxf(dot * scale, 0.0f), w = a * a;
+                if (w != 0.0f) {
+                    l += w;
+                    for (int d = 0; d < HD; d++) acc[d] += w * vr[d];
+                }
+            } else {
+                const float x = dot * scale, mn = fmaxf(m, x);
+                const float cf = expf(m - mn), p = expf(x - mn);
+                l = l * cf + p;
+                for (int d = 0; d < HD; d++) acc[d] = acc[d] * cf + p * vr[d];
+                m = mn;
+            }
+        }
+        const float den = weights == 1 ? sqrtf((float)HD) + l : l;
+        for (int d = 0; d < HD; d++) out[(size_t)h * HD + d] = acc[d] / den;
+    }
+}
+
 /* ------------------------------------------------------------------ decode over 16-bit K/V
  * Softmax over explicit float K/V rows [n_kv][S_cache][128] at positions pos[j] (j < n): the
  * sliding window (attn_sliding, attention.metal:63-101: keys pos-n+1 .. pos) and the sparse

@@ -50,6 +50,7 @@ def lib() -> C.CDLL:
         L.orc_quant_row.argtypes = [f32, C.c_int, C.c_int, i8, P(np.float32)]
         L.orc_decode_int8.argtypes = [f32, i8, f32, i8, f32, C.c_int, C.c_int, C.c_int, C.c_int,
                                       C.c_int, opt, f32, opt]
+        L.orc_decode_f32.argtypes = [f32, f32, f32, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, opt, f32, opt]
         L.orc_decode_rows.argtypes = [f32, f32, f32, C.c_int, C.c_int, C.c_int, i32, C.c_int,
                                       C.c_int, f32]
         L.orc_order_bits.argtypes = [C.c_float]
@@ -123,6 +124,22 @@ def decode_int8(q, K, ks, V, vs, weights=0, rows=None, n_sel=None, want_scores=F
     out = np.empty((n_q, 128), np.float32)
     scores = np.empty((n_kv, S_cache), np.float32) if want_scores else None
     lib().orc_decode_int8(q, K, ks, V, vs, S, S_cache, n_q, n_kv, weights, _ptr(rows_c), out, _ptr(scores))
+    return (out, scores) if want_scores else out
+
+
+def decode_f32(q, K, V, S=None, weights=0, rows=None, want_scores=False):
+    """q [n_q][128]; K, V [n_kv][S_cache][128] fp32 values of bf16 rows; rows u32 [n_kv][S]."""
+    q = _c(q, np.float32)
+    K = _c(K, np.float32)
+    V = _c(V, np.float32)
+    n_q = q.shape[0]
+    n_kv, S_cache, _ = K.shape
+    rows_c = None if rows is None else _c(rows, np.uint32)
+    if S is None:
+        S = rows_c.shape[-1] if rows_c is not None else S_cache
+    out = np.empty((n_q, 128), np.float32)
+    scores = np.empty((n_kv, S_cache), np.float32) if want_scores else None
+    lib().orc_decode_f32(q, K, V, S, S_cache, n_q, n_kv, weights, _ptr(rows_c), out, _ptr(scores))
     return (out, scores) if want_scores else out
 
 

@@ -138,3 +138,18 @@ def test_decode_noalloc_rejects_beyond_its_array():
     rc = L.embla_decode_int8_noalloc(d, d, d, d, None, 2000, 1024, 16, 4, 0, 0, 0, 0, None)
     assert rc == _lib.EMBLA_ERR_INVALID
     assert L.embla_decode_int8_noalloc(None, d, d, d, None, 10, 1024, 16, 4, 0, 0, 0, 0, None) == _lib.EMBLA_ERR_INVALID
+
+
+def test_bf16_cache_entry_points_reject_bad_arguments():
+    """The bf16 full-layer cache entry points validate on the host, before any HIP call."""
+    L = _lib.lib()
+    d = C.c_void_p(16)
+    bad = _lib.AttnParams(2000, 0, 0, 1024, 1999, 2, 0, 0)   # S > maxS
+    assert L.embla_attn_full(d, d, d, d, d, d, None, d, d, C.byref(bad), None) == _lib.EMBLA_ERR_INVALID
+    assert L.embla_attn_sparse(d, d, d, d, d, d, None, d, d, C.byref(bad), None) == _lib.EMBLA_ERR_INVALID
+    ok = _lib.AttnParams(100, 48, 0, 1024, 99, 2, 0, 0)      # CH not a multiple of 32
+    assert L.embla_attn_full(d, d, d, d, d, d, None, d, d, C.byref(ok), None) == _lib.EMBLA_ERR_INVALID
+    jobs = (_lib.KVJob * 1)(_lib.KVJob(2048, 2304, 0, 4096))
+    assert L.embla_kv_append_bf16(d, d, jobs, 1, 1000, 1024, 30, None) == _lib.EMBLA_ERR_INVALID   # past maxS
+    pb = _lib.AttnB(1000, 0, 0, 1024)
+    assert L.embla_attn_full_b(d, d, d, d, d, d, d, d, C.byref(pb), 30, None) == _lib.EMBLA_ERR_INVALID

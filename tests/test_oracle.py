@@ -152,6 +152,34 @@ def test_decode_scores_and_selected_rows(orc):
     np.testing.assert_allclose(got, np_decode(q, Kg, ksg, Vg, vsg, 0), atol=2e-6, rtol=1e-5)
 
 
+@pytest.mark.parametrize("weights", [0, 1])
+def test_decode_f32_vs_fp64_and_int8(orc, weights):
+    """The bf16-cache decode (attn_full / attn_sparse without KV8): fp64 brute force on bf16 rows;
+    bit for bit the int8 decode's arithmetic on integer-valued rows with unit scales; scores the
+    raw q·k maximum; SEL equals the gathered rows."""
+    g = synth.SplitMix64(21)
+    n_kv, S = 2, 260
+    K = synth.bf16_val(synth.bf16_bits(g.normal(n_kv * S * 128))).reshape(n_kv, S, 128)
+    V = synth.bf16_val(synth.bf16_bits(g.normal(n_kv * S * 128))).reshape(n_kv, S, 128)
+    q = synth.bf16_val(synth.bf16_bits(g.normal(16 * 128) * (3.0 if weights else 1.0))).reshape(16, 128)
+    ones = np.ones((n_kv, S), np.float32)
+    got, sc = orc.decode_f32(q, K, V, weights=weights, want_scores=True)
+    np.testing.assert_allclose(got, np_decode(q, K, ones, V, ones, weights), atol=2e-6, rtol=1e-5)
+    for kv in range(n_kv):
+        dots = K[kv].astype(np.float64) @ q[kv * 8:(kv + 1) * 8].T.astype(np.float64)
+        np.testing.assert_allclose(sc[kv], dots.max(1), rtol=1e-5, atol=1e-4)
+    Ki = g.int8(n_kv * S * 128).reshape(n_kv, S, 128)
+    Vi = g.int8(n_kv * S * 128).reshape(n_kv, S, 128)
+    qi = q / 16
+    np.testing.assert_array_equal(orc.decode_f32(qi, Ki.astype(np.float32), Vi.astype(np.float32), weights=weights),
+                                  orc.decode_int8(qi, Ki, ones, Vi, ones, weights=weights))
+    rows = np.stack([np.sort(np.random.default_rng(kv).choice(S, 41, replace=False)) for kv in range(n_kv)])
+    gs = orc.decode_f32(q, K, V, weights=weights, rows=rows.astype(np.uint32))
+    Kg = np.stack([K[kv][rows[kv]] for kv in range(n_kv)])
+    Vg = np.stack([V[kv][rows[kv]] for kv in range(n_kv)])
+    np.testing.assert_array_equal(gs, orc.decode_f32(q, Kg, Vg, weights=weights))
+
+
 # ------------------------------------------------------------------ selection
 def np_select(sc, S, topk=1024, recent=128):
     n = S - recent
