@@ -35,14 +35,17 @@ def poisoned_regions(K, ks, V, vs, S, max_s, seed):
     return dev(layout.pack_region(Kp, ksp, max_s, "k")), dev(layout.pack_region(Vp, vsp, max_s, "v"))
 
 
-@pytest.mark.parametrize("S,max_s", [(1000, 1024), (33, 64), (4001, 4096)])
-def test_decode_ignores_poisoned_tail(torch_gpu, orc, S, max_s):
+@pytest.mark.parametrize("S,max_s,chunk", [(1000, 1024, 0), (33, 64, 0), (4001, 4096, 0),
+                                           # chunks of several tiles a wave: the in-tile reload of
+                                           # the next tile meets the partial, poisoned last tile
+                                           (4001, 4096, 2048), (4001, 4096, 4096), (30001, 30016, 4096)])
+def test_decode_ignores_poisoned_tail(torch_gpu, orc, S, max_s, chunk):
     from embla_attn import ops
     torch = torch_gpu
-    say(f"decode poisoned tail S={S} max_s={max_s}")
+    say(f"decode poisoned tail S={S} max_s={max_s} chunk={chunk}")
     c = synth.decode_int8_case(seed=31, S=S)
     kc, vc = poisoned_regions(c["K"], c["ks"], c["V"], c["vs"], S, max_s, 5)
-    o = ops.decode_int8(dev(c["q"], torch.float16), kc, vc, S, max_s, 4, ws=ops.Workspace(max_s, 16))
+    o = ops.decode_int8(dev(c["q"], torch.float16), kc, vc, S, max_s, 4, chunk=chunk, ws=ops.Workspace(max_s, 16))
     ref = orc.decode_int8(synth.f16_val(c["q"]), c["K"], synth.f16_val(c["ks"]), c["V"], synth.f16_val(c["vs"]))
     assert_close(f16_host(o), ref, what=f"S={S}")
 
@@ -145,3 +148,25 @@ def test_ring_prefill_ignores_unwritten_slots(torch_gpu, p0, T):
     a, b = (o.cpu().numpy() for o in outs)
     assert np.isfinite(f16_host(outs[1])).all()
     np.testing.assert_array_equal(b, a)
+
+
+@pytest.mark.parametrize("S,max_s,relu2", [(1000, 1024, True), (4001, 4096, False)])
+def test_bf16_cache_decode_ignores_poisoned_tail(torch_gpu, orc, S, max_s, relu2):
+    """The bf16 full-layer cache (no KV8): positions past S hold NaN bit patterns."""
+    from embla_attn import ops
+    torch = torch_gpu
+    say(f"bf16 cache decode poisoned tail S={S} relu2={relu2}")
+    g = synth.SplitMix64(35)
+    K = synth.bf16_bits(g.normal(2 * max_s * 128)).reshape(2, max_s, 128)
+    V = synth.bf16_bits(g.normal(2 * max_s * 128)).reshape(2, max_s, 128)
+    K[:, S:], V[:, S:] = 0x7FC1, 0xFFC3
+    qraw = synth.bf16_bits(g.normal(16 * 128) * 2).reshape(16, 128)
+    part = torch.zeros(ops.lib().embla_workspace_bytes(max_s, 16) // 4, dtype=torch.float32, device="cuda")
+    counter = torch.zeros(4, dtype=torch.int32, device="cuda")
+    o = torch.empty((16, 128), dtype=torch.bfloat16, device="cuda")
+    fn = ops.attn_full if relu2 else ops.attn_sparse
+    fn(dev(qraw.view(np.int16), torch.bfloat16), None, None, dev(layout.pack_ring16(K, "k").view(np.int16)),
+       dev(layout.pack_ring16(V, "v").view(np.int16)), part, None, counter, o, S, max_s, ng=0)
+    qn = np.stack([orc.head_norm(synth.bf16_val(qraw[h])) for h in range(16)])
+    ref = orc.decode_f32(qn, synth.bf16_val(K[:, :S]), synth.bf16_val(V[:, :S]), weights=int(relu2))
+    assert_close(bf16_host(o), ref, what=f"S={S}")
