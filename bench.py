@@ -676,7 +676,7 @@ def main():
             "per_call_bytes": layer_bytes(L),
         },
         "hbm_read_floor": {
-            "what": "a plain streaming read of one layer's K+V bytes in one launch (embla_stream_read), "
+            "what": "a plain streaming read of one layer's K+V bytes in one launch (the bench-only probe library), "
                     "16 distinct buffers a graph: the practical floor of the split-K pass at this size",
             "bytes": floor["bytes"], "grid": floor["grid"], "us_per_launch": round(floor["us_per_launch"], 3),
             "gbs": round(floor["gbs"], 1), "frac_of_peak": round(floor["gbs"] / HBM_PEAK_GBS, 4),
