@@ -16,7 +16,9 @@ int AttentionEngine::encodeAttention(const Layer& L, int pos, hipStream_t st, bo
     // the k/v appends of the full layers (Engine.swift:754-764, 782-793)
     const bool appends = L.kind != LayerKind::sliding && !L.kvJobs.empty();
     if (appends) {
-        rc = embla_kv_append(b_.qkv, b_.cache, L.kvJobs.data(), (int)L.kvJobs.size(), pos, maxContext_, 1, st);
+        rc = kv8_ ? embla_kv_append(b_.qkv, b_.cache, L.kvJobs.data(), (int)L.kvJobs.size(), pos, maxContext_, 1, st)
+                  : embla_kv_append_bf16(b_.qkv, b_.cache, L.kvJobs.data(), (int)L.kvJobs.size(), pos, maxContext_, 1,
+                                         st);
         if (rc) return rc;
     }
     if (kvOnly) return EMBLA_OK;
@@ -31,13 +33,16 @@ int AttentionEngine::encodeAttention(const Layer& L, int pos, hipStream_t st, bo
         const bool sel = selecting(pos), score = scoring(L, pos);
         const int rows = sel && L.kind == LayerKind::sparse ? topk + recent : keys;
         EmblaAttnParams ap{rows, 0, 0, maxContext_, pos, L.nGains, 0, 0};
+        // the pipelines (Engine.swift:223-226): attn_full8 / attn_sparse8, or without KV8 the bf16 ones
+        const auto full = kv8_ ? embla_attn_full8 : embla_attn_full;
+        const auto sparse = kv8_ ? embla_attn_sparse8 : embla_attn_sparse;
         if (L.kind == LayerKind::full) {
-            rc = embla_attn_full8(b_.qkv, qg, kg, at(b_.cache, L.kOffset), at(b_.cache, L.vOffset), b_.apart,
-                                  score ? b_.scores : nullptr, b_.counter, b_.o, &ap, st);
+            rc = full(b_.qkv, qg, kg, at(b_.cache, L.kOffset), at(b_.cache, L.vOffset), b_.apart,
+                      score ? b_.scores : nullptr, b_.counter, b_.o, &ap, st);
             if (!rc && score) rc = embla_select_keys(b_.scores, b_.sel, keys, maxContext_, st);   // 819-827
         } else {
-            rc = embla_attn_sparse8(b_.qkv, qg, kg, at(b_.cache, L.kOffset), at(b_.cache, L.vOffset), b_.apart,
-                                    sel ? b_.sel : nullptr, b_.counter, b_.o, &ap, st);
+            rc = sparse(b_.qkv, qg, kg, at(b_.cache, L.kOffset), at(b_.cache, L.vOffset), b_.apart,
+                        sel ? b_.sel : nullptr, b_.counter, b_.o, &ap, st);
         }
     }
     if (rc) return rc;
@@ -48,6 +53,7 @@ int AttentionEngine::encodeAttention(const Layer& L, int pos, hipStream_t st, bo
 
 int AttentionEngine::copyFullBlock(const std::vector<const Layer*>& full, int p0, void* stored, bool save,
                                    hipStream_t st) const {
+    if (!kv8_) return EMBLA_ERR_UNSUPPORTED;
     std::vector<unsigned long long> regions;
     for (const Layer* L : full) {
         if (!L || L->kind != LayerKind::full) return EMBLA_ERR_INVALID;
@@ -102,13 +108,21 @@ int PrefillEncoder::encode(const Layer& L, int p0, int T, hipStream_t st, bool k
         rc = embla_attn_sliding8_b(b_.qkv, qg, kg, at(b_.cache, L.kOffset), at(b_.cache, L.vOffset), b_.o, p0, T, st);
     } else {                              // Prefill.swift:315-340, 378-407
         if (!L.kvJobs.empty()) {
-            rc = embla_kv_append(b_.qkv, b_.cache, L.kvJobs.data(), (int)L.kvJobs.size(), p0, maxContext_, T, st);
+            rc = kv8_ ? embla_kv_append(b_.qkv, b_.cache, L.kvJobs.data(), (int)L.kvJobs.size(), p0, maxContext_, T, st)
+                      : embla_kv_append_bf16(b_.qkv, b_.cache, L.kvJobs.data(), (int)L.kvJobs.size(), p0, maxContext_,
+                                             T, st);
             if (rc) return rc;
         }
         if (kvOnly) return EMBLA_OK;
-        rc = embla_q_prep_b(b_.qkv, qg, kg, b_.qn, T, st);
-        if (!rc) rc = embla_relu2_prefill(b_.qn, at(b_.cache, L.kOffset), at(b_.cache, L.vOffset), b_.o, T, p0 + T,
-                                          maxContext_, st);
+        if (kv8_) {
+            rc = embla_q_prep_b(b_.qkv, qg, kg, b_.qn, T, st);
+            if (!rc) rc = embla_relu2_prefill(b_.qn, at(b_.cache, L.kOffset), at(b_.cache, L.vOffset), b_.o, T, p0 + T,
+                                              maxContext_, st);
+        } else {   // attn_full_b over the bf16 caches (Prefill.swift:325-338)
+            const EmblaAttnB ap{p0, 0, 0, maxContext_};
+            rc = embla_attn_full_b(b_.qkv, qg, kg, at(b_.cache, L.kOffset), at(b_.cache, L.vOffset),
+                                   static_cast<float*>(b_.qn), b_.counter, b_.o, &ap, T, st);
+        }
     }
     if (rc) return rc;
     // the o-projection GEMM into the residual (Prefill.swift:337-339)

@@ -61,9 +61,11 @@ public:
     static constexpr int d = 2048, headDim = 128, topk = 1024, recent = 128;   // Engine.swift:7-27
 
     /// selects: the full layers that score every key for the sparse layers after them
-    /// (Embla.selects).
-    AttentionEngine(int maxContext, Buffers buffers, std::set<int> selects)
-        : maxContext_(maxContext), b_(buffers), selects_(std::move(selects)) {}
+    /// (Embla.selects). kv8: the full layers' caches in int8 with fp32 scales (the reference's
+    /// default, Engine.kv8); false: bf16 caches (EMBLA_KV8=0), whose KV jobs carry element
+    /// offsets (Engine.swift:457).
+    AttentionEngine(int maxContext, Buffers buffers, std::set<int> selects, bool kv8 = true)
+        : maxContext_(maxContext), b_(buffers), selects_(std::move(selects)), kv8_(kv8) {}
 
     /// Engine.encodeAttention: the layer's attention sub-layer at position pos. With kvOnly, only
     /// the q/k/v projection and the k/v append (a prompt token's last layer).
@@ -72,6 +74,7 @@ public:
     /// The full layers' int8 keys and values of positions p0 ..< p0 + 128 (p0 % 128 == 0) to or
     /// from a stored block (Engine.fullSpans + copy, PrefixCache.swift:153-200; one launch for every
     /// layer): stored holds embla_kv_block_bytes(layers, 2, EMBLA_F32) bytes in fullSpans' order.
+    /// int8 caches only (EMBLA_ERR_UNSUPPORTED without kv8).
     int copyFullBlock(const std::vector<const Layer*>& full, int p0, void* stored, bool save, hipStream_t stream) const;
     /// The sliding layers' ring slots of positions p0 ..< p0 + 128 (Engine.windowSpans' K/V spans):
     /// stored holds embla_ring_block_bytes(layers, 4) bytes.
@@ -103,6 +106,7 @@ private:
     int maxContext_;
     Buffers b_;
     std::set<int> selects_;
+    bool kv8_;
 };
 
 /// Device buffers of a prefill chunk of up to T tokens (Prefill.swift's own buffers): hs bf16
@@ -116,6 +120,7 @@ struct PrefillBuffers {
     void* qn = nullptr;
     void* o = nullptr;
     float* x = nullptr;
+    uint32_t* counter = nullptr;   // the reference's counter words (attn_full_b's argument; unused)
 };
 
 /// The attention parts of Prefill.encode (Sources/EmblaMetal/Prefill.swift:285-341, 378-407) for
@@ -123,10 +128,13 @@ struct PrefillBuffers {
 /// a sliding layer's ring append with its pre-ops and windowed attention (kv_sliding_b +
 /// attn_sliding8_b); a full or sparse layer's int8 append, q preparation and causal ReLU² attention
 /// with sink over every key (kv_append_b, q_prep_b, relu2_prefill_nax: the reference prefills its
-/// sparse layers with the full layers' kernel too); then the o-projection GEMM into x.
+/// sparse layers with the full layers' kernel too; without kv8, kv_append_b and attn_full_b over
+/// bf16 caches, Prefill.swift:315-338, with qn as attn_full_b's part buffer); then the o-projection
+/// GEMM into x.
 class PrefillEncoder {
 public:
-    PrefillEncoder(int maxContext, PrefillBuffers buffers) : maxContext_(maxContext), b_(buffers) {}
+    PrefillEncoder(int maxContext, PrefillBuffers buffers, bool kv8 = true)
+        : maxContext_(maxContext), b_(buffers), kv8_(kv8) {}
     /// With kvOnly, only the q/k/v GEMM and the k/v append (the prompt's last layer, Prefill.swift:287,
     /// 323).
     int encode(const Layer& L, int p0, int T, hipStream_t stream, bool kvOnly = false) const;
@@ -134,6 +142,7 @@ public:
 private:
     int maxContext_;
     PrefillBuffers b_;
+    bool kv8_;
 };
 
 }  // namespace embla_host

@@ -1,6 +1,7 @@
 """The C++ host side (embla-metal_amd/host: Engine.encodeAttention and Prefill.encode mirrored over
 the C ABI): a three-layer decode stack checked stage by stage against the C oracle, and prefill
-against token-by-token decode, by tests/cpp's test binary."""
+against token-by-token decode, with the full layers' caches in int8 and then in bf16 (the
+reference's EMBLA_KV8=0), by tests/cpp's test binary."""
 import subprocess
 from pathlib import Path
 
