@@ -643,6 +643,12 @@ int embla_attn_sliding8_b(const void* qkv, const void* qg, const void* kg, void*
                               nullptr, 0, stream);
 }
 
+int embla_attn_sliding_b(const void* qkv, const void* qg, const void* kg, void* kc, void* vc, void* o, int p0, int T,
+                         hipStream_t stream) {
+    // the scalar prefill's math is attn_sliding8_b's (prefill.metal:129-180 against 428-548)
+    return embla_attn_sliding8_b(qkv, qg, kg, kc, vc, o, p0, T, stream);
+}
+
 size_t embla_sparse_prefill_workspace_bytes(int T, int p0) {
     if (T <= 0 || p0 < 0) return 0;
     const size_t ld = round_up((size_t)(p0 + T > kRecent ? p0 + T - kRecent : 1), kIndexChunk);

@@ -93,6 +93,7 @@ SIGNATURES = {
                                  i32, vp, vp, sz, vp]),
     "embla_prefill_sliding": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, sz, vp]),
     "embla_attn_sliding8_b": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, vp]),
+    "embla_attn_sliding_b": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, vp]),
     "embla_sparse_layer_decode": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, sz, vp]),
 }
 

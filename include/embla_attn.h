@@ -232,6 +232,12 @@ int embla_prefill_sliding(const void* q, const void* k, const void* v, void* kri
 int embla_attn_sliding8_b(const void* qkv, const void* qg, const void* kg, void* kc, void* vc, void* o, int p0, int T,
                           hipStream_t stream);
 
+/* attn_sliding_b (prefill.metal:129-180), the reference's scalar sliding prefill chosen with
+ * SLIDING8=0 (Prefill.swift:27-31, 311-312): the same ring writes and the same attention as
+ * embla_attn_sliding8_b, which it calls. */
+int embla_attn_sliding_b(const void* qkv, const void* qg, const void* kg, void* kc, void* vc, void* o, int p0, int T,
+                         hipStream_t stream);
+
 /* ---------------------------------------------------------------- sparse-layer batched prefill
  * Config C5's sparse layer: T rows at p0 .. (q bf16 [T][n_q][128]); the chunk's K, V (bf16
  * [T][n_kv][128]) are quantised into a ROW-MAJOR int8 cache (kc, vc: [n_kv][max_s][128] int8, then
