@@ -155,6 +155,30 @@ def bench_read_floor(torch, n_layers=16, max_s=32768, n_kv=4, reps=20):
     return dict(bytes=nbytes, grid=best[0], us_per_launch=best[1], gbs=nbytes / (best[1] * 1e-6) / 1e9)
 
 
+def bench_mfma_ceiling(torch, reps=5):
+    """The dense fp16 MFMA rate the chip sustains: the bench-only probe's back-to-back
+    v_mfma_f32_32x32x16_f16 (4 independent chains a wave, no memory traffic), 512 workgroups of 4
+    waves for about as long as C5's full prefill (~0.7 ms a launch); the best of `reps` launches."""
+    from embla_attn import ops
+    grid, iters = 512, 4000
+    sink = torch.empty(grid * 4, dtype=torch.float32, device="cuda")
+    ops.mfma_rate(grid, 100, sink)
+    torch.cuda.synchronize()
+    best = None
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        ops.mfma_rate(grid, iters, sink)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1)
+        best = ms if best is None else min(best, ms)
+    flops = grid * 4 * 4 * iters * 32768.0
+    tf = flops / (best * 1e-3) / 1e12
+    return dict(what="back-to-back v_mfma_f32_32x32x16_f16, no memory traffic (the bench-only probe)",
+                ms=best, tflops=tf, frac_of_peak=tf / (MFMA_PEAK_TFLOPS))
+
+
 def bench_c2(torch, n_steps=512, reps=5):
     """Config C2: 512 consecutive decode steps over an fp16 ring of 8192, window 1024, each
     appending one K/V pair; one graph of the 512 steps."""
@@ -634,6 +658,8 @@ def main():
     c2 = bench_c2(torch)
     c4 = bench_c4(torch)
     c5 = bench_c5(torch)
+    mfma_ceiling = bench_mfma_ceiling(torch)
+    c5["frac_of_sustained_mfma"] = c5["tflops_attention"] / mfma_ceiling["tflops"]
     blocks = bench_blocks(torch)
     gemv = bench_gemv(torch)
     gemm = bench_gemm(torch)
@@ -689,6 +715,7 @@ def main():
         "c4_sparse": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in c4.items()},
         "c5_prefill_full": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c5.items()
                             if k not in ("sliding", "sparse")},
+        "mfma_ceiling": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in mfma_ceiling.items()},
         "c5_prefill_sparse": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c5["sparse"].items()},
         "kv_block_save_restore": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in blocks.items()},
         "qkv_o_projections_decode": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in gemv.items()},

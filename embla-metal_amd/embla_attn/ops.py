@@ -79,10 +79,8 @@ def decode_int8_merge(out, S, max_s, n_kv, ws: Workspace, weights=SOFTMAX, out_d
     return out
 
 
-def stream_read(buf, sink, grid=1024, depth=4, mode=0, stream=None):
-    """One streaming read of buf by the bench-only probe library (libembla_probe.so); sink: int32
-    [grid]; depth 16-byte loads in flight a thread (4, 8, 16, 32); mode 0: into registers, grid-
-    strided; 1: into LDS; 2: into registers, a contiguous slice a workgroup."""
+def _probe():
+    """The bench-only probe library (libembla_probe.so), loaded once."""
     global _PROBE
     if _PROBE is None:
         path = Path(__file__).resolve().parent / "libembla_probe.so"
@@ -92,10 +90,27 @@ def stream_read(buf, sink, grid=1024, depth=4, mode=0, stream=None):
         _PROBE.embla_probe_stream_read.restype = C.c_int
         _PROBE.embla_probe_stream_read.argtypes = [C.c_void_p, C.c_size_t, C.c_void_p, C.c_int, C.c_int, C.c_int,
                                                    C.c_void_p]
-    rc = _PROBE.embla_probe_stream_read(_p(buf), buf.numel() * buf.element_size(), _p(sink), grid, depth, int(mode),
-                                        stream_handle(stream))
+        _PROBE.embla_probe_mfma_rate.restype = C.c_int
+        _PROBE.embla_probe_mfma_rate.argtypes = [C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+    return _PROBE
+
+
+def stream_read(buf, sink, grid=1024, depth=4, mode=0, stream=None):
+    """One streaming read of buf by the bench-only probe library; sink: int32 [grid]; depth 16-byte
+    loads in flight a thread (4, 8, 16, 32); mode 0: into registers, grid-strided; 1: into LDS;
+    2: into registers, a contiguous slice a workgroup."""
+    rc = _probe().embla_probe_stream_read(_p(buf), buf.numel() * buf.element_size(), _p(sink), grid, depth,
+                                          int(mode), stream_handle(stream))
     if rc != 0:
         raise RuntimeError(f"embla_probe_stream_read failed ({rc})")
+
+
+def mfma_rate(grid, iters, sink, stream=None):
+    """The bench-only MFMA rate probe: grid workgroups of 4 waves, each wave 4 independent chains
+    of iters v_mfma_f32_32x32x16_f16 (32768 flop each); sink float [grid * 4]."""
+    rc = _probe().embla_probe_mfma_rate(grid, iters, _p(sink), stream_handle(stream))
+    if rc != 0:
+        raise RuntimeError(f"embla_probe_mfma_rate failed ({rc})")
 
 
 

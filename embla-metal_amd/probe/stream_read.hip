@@ -1,4 +1,4 @@
-// Bench-only bandwidth probe (libembla_probe.so, not part of the attention library): one streaming
+// Bench-only probes (libembla_probe.so, not part of the attention library). The bandwidth probe: one streaming
 // read of a buffer, nothing written but one word a workgroup. It gives the time a single launch
 // needs to move the same bytes as a decode layer's split-K pass, the practical floor that pass is
 // compared against, and the rate a large read sustains.
@@ -105,6 +105,50 @@ int embla_probe_stream_read(const void* p, size_t bytes, uint32_t* sink, int gri
         default: return -1;
     }
 #undef PROBE_CASE
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------ MFMA rate probe
+// Back-to-back v_mfma_f32_32x32x16_f16 with nothing else to do: each wave keeps CH independent
+// accumulator chains and runs `iters` rounds of one MFMA a chain (operands in registers, no
+// memory traffic but one result word a wave). The rate it reaches is the dense fp16 matrix rate
+// the chip sustains at the clock it grants under MFMA load.
+namespace {
+typedef _Float16 h8p_t __attribute__((ext_vector_type(8)));
+typedef float f16p_t __attribute__((ext_vector_type(16)));
+
+template <int CH>
+__global__ __launch_bounds__(256) void mfma_rate_kernel(int iters, float* __restrict__ sink) {
+    const int lane = threadIdx.x & 63;
+    h8p_t a, b;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        a[i] = (_Float16)(0.001f * (lane + i));
+        b[i] = (_Float16)(0.002f * (lane - i));
+    }
+    f16p_t acc[CH];
+#pragma unroll
+    for (int c = 0; c < CH; c++) acc[c] = (f16p_t){};
+    for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int c = 0; c < CH; c++) acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[c], 0, 0, 0);
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CH; c++) s += acc[c][lane & 15];
+    if (lane == 0) sink[blockIdx.x * 4 + (threadIdx.x >> 6)] = s;
+}
+}  // namespace
+
+extern "C" {
+
+/// grid workgroups of 4 waves, each wave 4 chains x iters MFMAs (32768 flop each); sink: grid * 4
+/// floats. 0 on success, -1 on a bad argument, -2 on a launch error.
+int embla_probe_mfma_rate(int grid, int iters, float* sink, hipStream_t stream) {
+    if (grid <= 0 || grid > 65536 || iters <= 0 || !sink) return -1;
+    hipLaunchKernelGGL(mfma_rate_kernel<4>, dim3(grid), dim3(256), 0, stream, iters, sink);
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
