@@ -78,7 +78,7 @@ __global__ __launch_bounds__(256) void full16_decode_kernel(Full16Args a) {
                 uint32_t kp = 0;
                 uint16_t v0 = 0, v1 = 0;
                 if (j < j1) {
-                    const int r = (int)ix[j];
+                    const int r = (int)min(ix[j], (uint32_t)(a.max_s - 1));   // a stray index reads a real row
                     kp = *(const uint32_t*)(a.kc + kt_off(kvh, a.max_s, r, 2 * lane, 2) / 2);
                     v0 = a.vc[vt_off(kvh, a.max_s, r, 2 * lane, 2) / 2];
                     v1 = a.vc[vt_off(kvh, a.max_s, r, 2 * lane + 1, 2) / 2];
