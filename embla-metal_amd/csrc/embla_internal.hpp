@@ -158,7 +158,10 @@ int launch_index_scores(const uint16_t* qi, const float* w, const uint16_t* ki, 
 /// Words (4 bytes) of the wide select's workspace: two histogram buffers (8 copies of 256 coarse
 /// and 4096 fine bins), counters (first digit, keys above it, epoch), the candidate counts of the
 /// classify workgroups, the bitmap and their candidate regions (1024 pairs each).
-constexpr size_t kWideSelectWords = 2 * 8 * (256 + 4096) + 64 + 32768 / 1024 + 32768 / 32 + 2 * 32768;
+#ifndef WSEL_NCP
+#define WSEL_NCP 16   // histogram copies of the wide select (C4 step: 8 -> 32.1 us, 16 -> 29.5, 32 -> 29.6, 64 -> 31.4)
+#endif
+constexpr size_t kWideSelectWords = 2 * WSEL_NCP * (256 + 4096) + 64 + 32768 / 1024 + 32768 / 32 + 2 * 32768;
 /// Index scores of keys [0, S - recent), then their exact top-k + recent into idx, on many
 /// workgroups (one set). sw: kWideSelectWords words, zero before the first call.
 int launch_wide_select(const uint16_t* qi, const float* w, const uint16_t* ki, float* scores, int S, int n_ih,

@@ -30,7 +30,7 @@ constexpr int LCAP = 2048;                  // bucket list capacity (else passes
 constexpr int SEL_OUTCAP = HCOPIES * HSTRIDE + LCAP;   // topk indices staged in hist + list
 constexpr int DB = 4096;                    // the wide select's 12-bit digits: bits 31..20, 19..8
 constexpr int CB = 256;                     // its coarse first digit: bits 31..24
-constexpr int NCP = 8;                      // histogram copies (scorer workgroup % 8)
+constexpr int NCP = WSEL_NCP;               // histogram copies (scorer workgroup % NCP)
 constexpr int HCOPY = CB + DB;              // words a copy: coarse bins, then fine bins
 constexpr int HWORDS = NCP * HCOPY;         // words a histogram buffer (two, by call parity)
 
@@ -374,7 +374,7 @@ __global__ __launch_bounds__(256) void wsel_classify_kernel(const float* __restr
     if (w == 0) pick256(ch, (uint32_t)topk, sel);
     __syncthreads();
     const uint32_t cd = sel[0] & (CB - 1), above_c = sel[1];
-    if (tid < NCP * 16) fh[tid >> 4][tid & 15] = H[(tid >> 4) * HCOPY + CB + 16 * cd + (tid & 15)];
+    for (int i = tid; i < NCP * 16; i += 256) fh[i >> 4][i & 15] = H[(i >> 4) * HCOPY + CB + 16 * cd + (i & 15)];
     if (tid == 0) sel[0] = 16 * cd;
     __syncthreads();
     if (w == 0) {   // lanes < 16: fine bins 16 cd + 15 - lane, from the top
@@ -567,7 +567,7 @@ int launch_wide_select(const uint16_t* qi, const float* w, const uint16_t* ki, f
 /// A wave takes 64 keys a round: load j (16 bytes a lane) covers keys 8j .. 8j + 7, lane l holding
 /// key 8j + l / 8, dims 8 (l % 8) .. + 7, so every load of the wave reads 1 KB contiguous.
 /// With the wide select's workspace `sw`, each workgroup also counts its scores' top 12 order bits
-/// in LDS and adds them to histogram copy blockIdx % 8 of this call's buffer (sw's epoch word
+/// in LDS and adds them to histogram copy blockIdx % NCP of this call's buffer (sw's epoch word
 /// picks one of two): fine bins (12 bits) and coarse bins (top 8), thread t adding the 16 fine
 /// bins of coarse bin t. It also clears its slice of the other buffer for the next call.
 template <int NIH>
