@@ -17,7 +17,10 @@ constexpr int kRefWindow = 128;         // the reference's sliding window (Engin
 constexpr int kRefRing = 4096;          // the reference's ring (attention.metal:6)
 constexpr int kTopK = 1024, kRecent = 128;   // Engine.swift:9 (topk, recent)
 constexpr int kSparseRefCH = 128;        // keys a chunk of the gathered reference sparse decode
-constexpr int kIndexChunk = 2048;         // keys a workgroup of the MFMA indexer
+#ifndef IDX_CHUNK
+#define IDX_CHUNK 512   // C5 sparse layer: 0.428 ms at 2048 keys, 0.417-0.424 at 512, 0.426 at 256, 0.469 at 4096
+#endif
+constexpr int kIndexChunk = IDX_CHUNK;    // keys a workgroup of the MFMA indexer
 constexpr int kPrefillSplits = 4;       // most key-range splits of a prefill chunk (workspace sizing)
 
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
