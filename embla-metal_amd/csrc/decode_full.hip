@@ -434,12 +434,19 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
 
 /// Merges the C chunk partials of query head blockIdx.x, dims 32 * blockIdx.y .. + 31: thread
 /// (slice s of 4 dims, chunk group r) loads its chunks' slices, maxima and sums in one round.
+#ifndef MERGE_DPW
+#define MERGE_DPW 8   // C3 layer: 13.52 us with the LDS-loop merge, 12.98 (32 dims), 12.30 (16), 12.22-12.27 (8)
+#endif
+constexpr int MDPW = MERGE_DPW;   // dims a merge workgroup
+
 template <bool RELU2, bool OBF>
 __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ part, uint16_t* __restrict__ o,
                                                            int C, int n_q, float sink, float oscale) {
-    constexpr int NR = 32, MAXK = 8;   // chunk groups; chunks a thread (C <= 256)
-    const int h = blockIdx.x, d0 = 32 * blockIdx.y;
-    const int tid = threadIdx.x, sl = tid & 7, r = tid >> 3;
+    // thread (slice sl of 4 dims, chunk group r); the chunk groups of a wave reduce by shuffles, the
+    // 4 waves through LDS
+    constexpr int SLC = MDPW / 4, NR = 256 / SLC, MAXK = 256 / NR;   // C <= 256
+    const int h = blockIdx.x, d0 = MDPW * blockIdx.y;
+    const int tid = threadIdx.x, sl = tid % SLC, r = tid / SLC, w = tid >> 6;
     const int d = d0 + 4 * sl;
     u4_t v[MAXK];
     float mk[MAXK], lk[MAXK];
@@ -449,21 +456,23 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
         if (cc < C) {
             const float* p = part + ((size_t)cc * n_q + h) * PS;
             v[k] = ld16(p + d);
-            mk[k] = p[HD];
-            lk[k] = p[HD + 1];
+            const u2_t ml = ld8(p + HD);
+            mk[k] = __uint_as_float(ml[0]);
+            lk[k] = __uint_as_float(ml[1]);
         }
     }
-    __shared__ float sm[NR], sl_[NR];
-    __shared__ f4_t sa[NR][8];
+    __shared__ float sm[4], sl_[4][SLC];
+    __shared__ f4_t sa[4][SLC];
     float M = RELU2 ? 0.0f : NEG_INF;
     if constexpr (!RELU2) {
 #pragma unroll
         for (int k = 0; k < MAXK; k++)
             if (r + NR * k < C) M = fmaxf(M, mk[k]);
-        if (sl == 0) sm[r] = M;
+#pragma unroll
+        for (int m = SLC; m < 64; m <<= 1) M = fmaxf(M, shfl_xor(M, m));
+        if ((tid & 63) == 0) sm[w] = M;
         __syncthreads();
-        M = NEG_INF;
-        for (int i = 0; i < NR; i++) M = fmaxf(M, sm[i]);
+        M = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
     }
     f4_t A = {0, 0, 0, 0};
     float Lr = 0.0f;
@@ -476,13 +485,17 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
             for (int i = 0; i < 4; i++) A[i] += __uint_as_float(v[k][i]) * f;
         }
     }
-    sa[r][sl] = A;
-    if (sl == 0) sl_[r] = Lr;
+#pragma unroll
+    for (int m = SLC; m < 64; m <<= 1) {
+        Lr += shfl_xor(Lr, m);
+#pragma unroll
+        for (int i = 0; i < 4; i++) A[i] += shfl_xor(A[i], m);
+    }
+    if ((tid & 63) < SLC) { sa[w][sl] = A; sl_[w][sl] = Lr; }
     __syncthreads();
-    if (tid >= 8) return;
-    f4_t T = {0, 0, 0, 0};
-    float L = 0.0f;
-    for (int i = 0; i < NR; i++) { T += sa[i][sl]; L += sl_[i]; }
+    if (tid >= SLC) return;
+    const f4_t T = sa[0][sl] + sa[1][sl] + sa[2][sl] + sa[3][sl];
+    const float L = sl_[0][sl] + sl_[1][sl] + sl_[2][sl] + sl_[3][sl];
     const float inv = 1.0f / (RELU2 ? oscale * (sink + L) : oscale * L);
 #pragma unroll
     for (int i = 0; i < 4; i++) o[(size_t)h * HD + d + i] = f2a<OBF>(T[i] * inv);
@@ -534,7 +547,7 @@ int launch_full_decode_merge(const FullDecodeArgs& a, hipStream_t st) {
 
 int launch_decode_merge(const float* part, uint16_t* o, int C, int n_q, bool relu2, bool out_bf16, float oscale,
                         hipStream_t st) {
-    const dim3 mg(n_q, HD / 32), block(256);
+    const dim3 mg(n_q, HD / MDPW), block(256);
     const float sink = 11.313708498984761f;   // sqrt(128)
     if (relu2 && out_bf16) hipLaunchKernelGGL((decode_merge_kernel<true, true>), mg, block, 0, st, part, o, C, n_q, sink, oscale);
     else if (!relu2 && out_bf16) hipLaunchKernelGGL((decode_merge_kernel<false, true>), mg, block, 0, st, part, o, C, n_q, sink, oscale);
