@@ -436,27 +436,41 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
         }
 }
 
-/// Merges the nsplit partial rows of (token, head) = (blockIdx.x * 4 + wave, blockIdx.y): a wave
-/// a row, two dims a lane.
+/// Merges the nsplit partial rows of (token, head): 32 lanes a row, 4 dims a lane (16-byte loads),
+/// 8 rows a workgroup: rows (blockIdx.x * 8 + tid / 32) of head blockIdx.y.
 template <bool RELU2, bool OBF>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
-    const int lane = threadIdx.x & 63, tok = blockIdx.x * 4 + (threadIdx.x >> 6), hq = blockIdx.y;
+    const int lane = threadIdx.x & 31, tok = blockIdx.x * 8 + (threadIdx.x >> 5), hq = blockIdx.y;
     if (tok >= a.T) return;
-    float M = RELU2 ? 0.0f : NEG_INF;
-    if constexpr (!RELU2)
-        for (int z = 0; z < a.nsplit; z++) M = fmaxf(M, a.part[(((size_t)z * a.T + tok) * a.n_q + hq) * PPS + HD]);
-    float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
-    for (int z = 0; z < a.nsplit; z++) {
-        const float* pp = a.part + (((size_t)z * a.T + tok) * a.n_q + hq) * PPS;
-        const float mz = pp[HD];
-        const float f = RELU2 ? 1.0f : (mz == NEG_INF ? 0.0f : exp2f(mz - M));
-        L += pp[HD + 1] * f;
-        o0 += pp[2 * lane] * f;
-        o1 += pp[2 * lane + 1] * f;
+    float M = RELU2 ? 0.0f : NEG_INF, mz[4], lz[4];
+    u4_t v[4];
+#pragma unroll
+    for (int z = 0; z < 4; z++) {
+        if (z < a.nsplit) {
+            const float* pp = a.part + (((size_t)z * a.T + tok) * a.n_q + hq) * PPS;
+            v[z] = ld16(pp + 4 * lane);
+            const u2_t ml = ld8(pp + HD);
+            mz[z] = __uint_as_float(ml[0]);
+            lz[z] = __uint_as_float(ml[1]);
+            if constexpr (!RELU2) M = fmaxf(M, mz[z]);
+        }
+    }
+    float L = 0.0f, acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int z = 0; z < 4; z++) {
+        if (z < a.nsplit) {
+            const float f = RELU2 ? 1.0f : (mz[z] == NEG_INF ? 0.0f : exp2f(mz[z] - M));
+            L += lz[z] * f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i] += __uint_as_float(v[z][i]) * f;
+        }
     }
     const float inv = RELU2 ? 1.0f / (11.313708498984761f + L) : 1.0f / L;
     uint16_t* orow = a.o + (size_t)tok * a.o_tok_stride + (size_t)hq * a.o_head_stride;
-    *(uint32_t*)(orow + 2 * lane) = (uint32_t)f2a<OBF>(o0 * inv) | ((uint32_t)f2a<OBF>(o1 * inv) << 16);
+    u2_t pk;
+    pk[0] = (uint32_t)f2a<OBF>(acc[0] * inv) | ((uint32_t)f2a<OBF>(acc[1] * inv) << 16);
+    pk[1] = (uint32_t)f2a<OBF>(acc[2] * inv) | ((uint32_t)f2a<OBF>(acc[3] * inv) << 16);
+    *(u2_t*)(orow + 4 * lane) = pk;
 }
 
 int launch_prefill_int8(const PrefillArgs& a, hipStream_t st) {
@@ -495,7 +509,7 @@ int launch_prefill_ring(const PrefillArgs& a, hipStream_t st) {
 
 int launch_prefill_tail(const PrefillArgs& a, hipStream_t st) {
     if (a.nsplit > 1) {
-        const dim3 mg((a.T + 3) / 4, a.n_q);
+        const dim3 mg((a.T + 7) / 8, a.n_q);
         if (a.relu2) hipLaunchKernelGGL((prefill_merge_kernel<true, true>), mg, dim3(256), 0, st, a);
         else if (a.out_bf16) hipLaunchKernelGGL((prefill_merge_kernel<false, true>), mg, dim3(256), 0, st, a);
         else hipLaunchKernelGGL((prefill_merge_kernel<false, false>), mg, dim3(256), 0, st, a);
