@@ -105,6 +105,23 @@ __device__ __forceinline__ u4_t ld16_stream(const void* p) {
 
 // ------------------------------------------------------------------ wave helpers (wave64)
 __device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
+/// v_max3_f32 / v_max_f32 with no canonicalisation of the inputs: for values that are never NaN
+/// (fmaxf makes the compiler quiet each MFMA result first, one more VALU a value).
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float vmax2(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+/// max(v, v of lane xor 32) in every lane, on v_permlane32_swap (VALU, no LDS round trip).
+__device__ __forceinline__ float max_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return vmax2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 __device__ __forceinline__ float readlane(float v, int l) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }

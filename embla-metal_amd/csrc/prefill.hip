@@ -123,7 +123,8 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
     static_assert(PER >= 1, "a piece a thread at least");
     struct Stage {
         u4_t kr[PER], vr[PER];
-        float ksr[PER], vsr[PER][8];              // int8: the pieces' scales
+        float ksr[PER];                           // int8: the K pieces' scales
+        uint32_t vsh[PER][4];                     // int8: the V pieces' 8 scales, fp16 pairs
     };
     Stage SA;                                     // the next tile's loads
     auto tile_key = [&](int key) -> int {         // the 32-key tile's first key, clamped in range
@@ -135,7 +136,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
         u4_t* kr = S.kr;
         u4_t* vr = S.vr;
         float* ksr = S.ksr;
-        float (*vsr)[8] = S.vsr;
+        uint32_t (*vsh)[4] = S.vsh;
 #pragma unroll
         for (int i = 0; i < PER; i++) {
             const int q = tid + NT * i, gt = q / (256 * EB), jl = q % (256 * EB);
@@ -164,8 +165,19 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
                 const size_t kidx = (size_t)kvh * a.max_s + kt + 16 * (j >> 1) + (l & 15);
                 ksr[i] = SCALE32 ? *(const float*)(ksb + kidx * 4) : h2f(*(const uint16_t*)(ksb + kidx * 2));
                 const size_t vidx = (size_t)kvh * a.max_s + kt + 4 * (l >> 4);
-                scales4<SCALE32>(vsb, vidx, vsr[i]);
-                scales4<SCALE32>(vsb, vidx + 16, vsr[i] + 4);
+                if constexpr (SCALE32) {
+                    float t[8];
+                    scales4<true>(vsb, vidx, t);
+                    scales4<true>(vsb, vidx + 16, t + 4);
+#pragma unroll
+                    for (int k = 0; k < 4; k++) vsh[i][k] = (uint32_t)f2h(t[2 * k]) | ((uint32_t)f2h(t[2 * k + 1]) << 16);
+                } else {   // fp16 scales stay fp16 pairs: the staging multiplies in fp16 anyway
+                    const u2_t s0 = ld8(vsb + vidx * 2), s1 = ld8(vsb + (vidx + 16) * 2);
+                    vsh[i][0] = s0[0];
+                    vsh[i][1] = s0[1];
+                    vsh[i][2] = s1[0];
+                    vsh[i][3] = s1[1];
+                }
                 // keys past the last one the workgroup needs (the last staged tile; maybe never
                 // written) are staged as zero rows: masked keys then add exactly 0 to P·V
                 const int lk = k0 + 32 * gt;   // the tile's logical first key (kt may be clamped)
@@ -173,7 +185,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
                     if (lk + 16 * (j >> 1) + (l & 15) > hi) ksr[i] = 0.0f;
 #pragma unroll
                     for (int e = 0; e < 8; e++)
-                        if (lk + 16 * (e >> 2) + 4 * (l >> 4) + (e & 3) > hi) vsr[i][e] = 0.0f;
+                        if (lk + 16 * (e >> 2) + 4 * (l >> 4) + (e & 3) > hi) vsh[i][e >> 1] &= (e & 1) ? 0x0000FFFFu : 0xFFFF0000u;
                 }
             }
         }
@@ -182,7 +194,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
         const u4_t* kr = S.kr;
         const u4_t* vr = S.vr;
         const float* ksr = S.ksr;
-        const float (*vsr)[8] = S.vsr;
+        const uint32_t (*vsh)[4] = S.vsh;
 #pragma unroll
         for (int i = 0; i < PER; i++) {
             const int q = tid + NT * i, gt = q / (256 * EB), j = (q % (256 * EB)) >> 6, l = q & 63;
@@ -205,8 +217,8 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
                 *(h8_t*)(sm.k[b] + key * KROW + d0 + 8) = i8x8_scaled(kr[i][2], kr[i][3], s2, s2, s2, s2);
                 // V piece (j, l): rows u = 2j, 2j + 1 of slot l, 8 keys {16t + 4g + i} each (item
                 // 4t + i), times their scales
-                const h2_t v01 = {(_Float16)vsr[i][0], (_Float16)vsr[i][1]}, v23 = {(_Float16)vsr[i][2], (_Float16)vsr[i][3]};
-                const h2_t v45 = {(_Float16)vsr[i][4], (_Float16)vsr[i][5]}, v67 = {(_Float16)vsr[i][6], (_Float16)vsr[i][7]};
+                const h2_t v01 = __builtin_bit_cast(h2_t, vsh[i][0]), v23 = __builtin_bit_cast(h2_t, vsh[i][1]);
+                const h2_t v45 = __builtin_bit_cast(h2_t, vsh[i][2]), v67 = __builtin_bit_cast(h2_t, vsh[i][3]);
                 _Float16* base = sm.vt[b] + gt * VTILE + l * 8;
                 *(h8_t*)(base + (2 * j) * VUROW) = i8x8_scaled(vr[i][0], vr[i][1], v01, v23, v45, v67);
                 *(h8_t*)(base + (2 * j + 1) * VUROW) = i8x8_scaled(vr[i][2], vr[i][3], v01, v23, v45, v67);
@@ -350,10 +362,14 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
             }
             float msub = 0.0f;
             if constexpr (!RELU2) {
-                float mt = fmaxf(x[0], x[1]);
+                // two max3 chains over the 32 scores, then across the row's two lanes
+                float ma = vmax3(x[0], x[1], x[2]), mb = vmax3(x[16], x[17], x[18]);
 #pragma unroll
-                for (int e = 2; e < 32; e += 2) mt = fmaxf(mt, fmaxf(x[e], x[e + 1]));
-                mt = fmaxf(mt, shfl_xor(mt, 32));
+                for (int e = 3; e < 15; e += 2) {
+                    ma = vmax3(ma, x[e], x[e + 1]);
+                    mb = vmax3(mb, x[16 + e], x[17 + e]);
+                }
+                const float mt = max_xor32(vmax3(vmax3(ma, mb, x[15]), x[31], x[31]));
                 // the running maximum moves only when a row's grows by more than 2^8: weights stay
                 // <= 256 (fp16-safe), O and l share the stale m
                 if (__any(mt > m + 8.0f)) {
