@@ -53,6 +53,9 @@ struct __attribute__((aligned(16))) PrefillSmem {
 
 constexpr int PPS = HD + 4;        // floats a split partial row: O[128], m, l, pad
 constexpr int PF_WAVES = 8;        // waves a workgroup: GQ query heads x (8 / GQ) 32-row blocks
+#ifndef PF_XCD
+#define PF_XCD 1                   // workgroups of one (kv head, split) spread over one XCD
+#endif
 int launch_prefill_tail(const PrefillArgs& a, hipStream_t st);
 
 /// Scales of the four keys kt + 4g .. + 3 (fp16 pair or fp32 quad) as fp32.
@@ -90,7 +93,18 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
     constexpr int NT = 64 * PF_WAVES;
     constexpr int RB = PF_WAVES / GQ;                       // 32-row blocks a workgroup
     __shared__ PrefillSmem sm;
-    const int tb = blockIdx.x, kvh = blockIdx.y;
+    // full caches: consecutive workgroup ids go to consecutive XCDs, and id % (n_kv * nsplit)
+    // picks the (kv head, split), so that each XCD streams as few key ranges as possible and its L2
+    // holds them (C5 full: -2%); a ring's windows differ from row block to row block (no gain)
+    int tb = blockIdx.x, kvh = blockIdx.y, zz = blockIdx.z;
+    if constexpr (PF_XCD && !RING) {
+        const int nc = gridDim.y * gridDim.z;
+        const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+        const int combo = lin % nc;
+        tb = lin / nc;
+        kvh = combo % gridDim.y;
+        zz = combo / gridDim.y;
+    }
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int r = lane & 31, h = lane >> 5;
     const int hq = kvh * GQ + w % GQ;
@@ -105,7 +119,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
     const int kfirst = lo & ~(PBK - 1);
     const int ntot = (hi - kfirst) / PBK + 1;
     // split z of nsplit takes an equal share of the block's key tiles (the prefix splits evenly)
-    const int z = blockIdx.z, t_lo = ntot * z / a.nsplit, t_hi = ntot * (z + 1) / a.nsplit;
+    const int z = zz, t_lo = ntot * z / a.nsplit, t_hi = ntot * (z + 1) / a.nsplit;
     const int kstart = kfirst + t_lo * PBK;
     const int ntiles = t_hi - t_lo;
 
