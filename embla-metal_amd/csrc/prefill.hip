@@ -105,7 +105,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
         kvh = combo % gridDim.y;
         zz = combo / gridDim.y;
     }
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane & 31, h = lane >> 5;
     const int hq = kvh * GQ + w % GQ;
     const int wt0 = tb * 32 * RB;                             // the workgroup's first token
@@ -153,7 +153,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
         uint32_t (*vsh)[4] = S.vsh;
 #pragma unroll
         for (int i = 0; i < PER; i++) {
-            const int q = tid + NT * i, gt = q / (256 * EB), jl = q % (256 * EB);
+            const int qw = 64 * w + NT * i, gt = qw / (256 * EB), jl = qw % (256 * EB) + lane;
             if constexpr (RING) {
                 const size_t off = tile_base(kvh, a.R, (k0 + 32 * gt) % a.R, 2) + (size_t)jl * 16;
                 kr[i] = ld16((const char*)a.kring + off);
@@ -170,14 +170,17 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
                     }
                 }
             } else {
-                const int kt = tile_key(k0 + 32 * gt);
-                const size_t off = tile_base(kvh, a.max_s, kt, 1) + (size_t)jl * 16;
-                kr[i] = ld16(a.kc + off);
-                vr[i] = ld16(a.vc + off);
-                const int j = jl >> 6, l = jl & 63;
+                // the piece's tile and row j are the wave's (uniform: scalar base addresses, the
+                // lane's part a 32-bit offset)
+                const int gtw = gt, j = (qw % 256) >> 6, l = lane;
+                const int kt = tile_key(k0 + 32 * gtw);
+                const size_t tb0 = tile_base(kvh, a.max_s, kt, 1) + (size_t)(qw % 256) * 16;
+                kr[i] = ld16(a.kc + tb0 + 16 * l);
+                vr[i] = ld16(a.vc + tb0 + 16 * l);
                 // K piece: key kt + 16 (j / 2) + l % 16; V piece: keys kt + 16t + 4 (l / 16) + i
-                const size_t kidx = (size_t)kvh * a.max_s + kt + 16 * (j >> 1) + (l & 15);
-                ksr[i] = SCALE32 ? *(const float*)(ksb + kidx * 4) : h2f(*(const uint16_t*)(ksb + kidx * 2));
+                const size_t kbase = (size_t)kvh * a.max_s + kt + 16 * (j >> 1);
+                ksr[i] = SCALE32 ? *(const float*)(ksb + kbase * 4 + 4 * (l & 15))
+                                 : h2f(*(const uint16_t*)(ksb + kbase * 2 + 2 * (l & 15)));
                 const size_t vidx = (size_t)kvh * a.max_s + kt + 4 * (l >> 4);
                 if constexpr (SCALE32) {
                     float t[8];
@@ -194,7 +197,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
                 }
                 // keys past the last one the workgroup needs (the last staged tile; maybe never
                 // written) are staged as zero rows: masked keys then add exactly 0 to P·V
-                const int lk = k0 + 32 * gt;   // the tile's logical first key (kt may be clamped)
+                const int lk = k0 + 32 * gtw;   // the tile's logical first key (kt may be clamped)
                 if (lk + 31 > hi) {
                     if (lk + 16 * (j >> 1) + (l & 15) > hi) ksr[i] = 0.0f;
 #pragma unroll
@@ -211,7 +214,8 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
         const uint32_t (*vsh)[4] = S.vsh;
 #pragma unroll
         for (int i = 0; i < PER; i++) {
-            const int q = tid + NT * i, gt = q / (256 * EB), j = (q % (256 * EB)) >> 6, l = q & 63;
+            // piece q = 64 w + NT i + lane: its tile gt and row j are the wave's
+            const int qw = 64 * w + NT * i, gt = qw / (256 * EB), j = (qw % (256 * EB)) >> 6, l = lane;
             if constexpr (RING) {
                 // K piece (j, l): key 16 (j / 4) + l % 16, dims 32 (l / 16) + 8 (j % 4) .. + 7
                 const int key = 32 * gt + 16 * (j >> 2) + (l & 15), d0 = 32 * (l >> 4) + 8 * (j & 3);
