@@ -51,7 +51,10 @@ struct __attribute__((aligned(16))) PrefillSmem {
     _Float16 vt[2][NSUB * VTILE];
 };
 
-constexpr int PPS = HD + 4;        // floats a split partial row: O[128], m, l, pad
+// a split's partial record (floats): O / l as 128 fp16 (a convex combination of V rows, which the
+// P·V products already take in fp16), then m and l in fp32, padded to 16 bytes: half the bytes of
+// an fp32 O for the split pass to write and the merge to read
+constexpr int PPH = 68;
 constexpr int PF_WAVES = 8;        // waves a workgroup: GQ query heads x (8 / GQ) 32-row blocks
 #ifndef PF_XCD
 #define PF_XCD 1                   // workgroups of one (kv head, split) spread over one XCD
@@ -455,21 +458,27 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
     const bool coalesced = ((uintptr_t)a.o % 16) == 0 && a.o_tok_stride % 8 == 0 && a.o_head_stride % 8 == 0;
     __syncthreads();
     float* stg = (float*)&sm;
-    if (a.nsplit > 1) {   // this split's partial rows: unnormalised O, m, l
-        constexpr int TS = GQ * PPS + 4;   // floats a token: 16-byte writes of 16 rows on distinct banks
-        float* rec = stg + tl * TS + hl * PPS;
+    if (a.nsplit > 1) {   // this split's partial records: O / l (fp16), m, l
+        constexpr int TS = GQ * PPH + 4;   // floats a token: the 8-byte writes of 16 rows on distinct banks
+        float* rec = stg + tl * TS + hl * PPH;
+        const float il = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+        uint16_t* r16 = (uint16_t*)rec;
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
-            for (int bb = 0; bb < 4; bb++)
-                *(f4_t*)(rec + 32 * i + 8 * bb + 4 * h) = (f4_t){O[i][4 * bb], O[i][4 * bb + 1], O[i][4 * bb + 2], O[i][4 * bb + 3]};
-        if (h == 0) *(f4_t*)(rec + HD) = (f4_t){m, lsum, 0.0f, 0.0f};
+            for (int bb = 0; bb < 4; bb++) {
+                u2_t pk;
+                pk[0] = (uint32_t)f2h(O[i][4 * bb] * il) | ((uint32_t)f2h(O[i][4 * bb + 1] * il) << 16);
+                pk[1] = (uint32_t)f2h(O[i][4 * bb + 2] * il) | ((uint32_t)f2h(O[i][4 * bb + 3] * il) << 16);
+                *(u2_t*)(r16 + 32 * i + 8 * bb + 4 * h) = pk;
+            }
+        if (h == 0) *(f4_t*)(rec + HD / 2) = (f4_t){m, lsum, 0.0f, 0.0f};
         __syncthreads();
-        constexpr int CPT = GQ * PPS / 4;   // 16-byte chunks a token
-        float* pz = a.part + ((size_t)z * a.T + wt0) * a.n_q * PPS + (size_t)kvh * GQ * PPS;
+        constexpr int CPT = GQ * PPH / 4;   // 16-byte chunks a token
+        float* pz = a.part + ((size_t)z * a.T + wt0) * a.n_q * PPH + (size_t)kvh * GQ * PPH;
         for (int cidx = tid; cidx < ntok * CPT; cidx += NT) {
             const int t = cidx / CPT, off = 4 * (cidx % CPT);
-            *(f4_t*)(pz + (size_t)t * a.n_q * PPS + off) = *(const f4_t*)(stg + t * TS + off);
+            *(f4_t*)(pz + (size_t)t * a.n_q * PPH + off) = *(const f4_t*)(stg + t * TS + off);
         }
         return;
     }
@@ -509,20 +518,20 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
     }
 }
 
-/// Merges the nsplit partial rows of (token, head): 32 lanes a row, 4 dims a lane (16-byte loads),
+/// Merges the nsplit partial records of (token, head): 32 lanes a row, 4 dims a lane (8-byte loads),
 /// 8 rows a workgroup: rows (blockIdx.x * 8 + tid / 32) of head blockIdx.y.
 template <bool RELU2, bool OBF>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
     const int lane = threadIdx.x & 31, tok = blockIdx.x * 8 + (threadIdx.x >> 5), hq = blockIdx.y;
     if (tok >= a.T) return;
     float M = RELU2 ? 0.0f : NEG_INF, mz[4], lz[4];
-    u4_t v[4];
+    u2_t v[4];
 #pragma unroll
     for (int z = 0; z < 4; z++) {
         if (z < a.nsplit) {
-            const float* pp = a.part + (((size_t)z * a.T + tok) * a.n_q + hq) * PPS;
-            v[z] = ld16(pp + 4 * lane);
-            const u2_t ml = ld8(pp + HD);
+            const float* pp = a.part + (((size_t)z * a.T + tok) * a.n_q + hq) * PPH;
+            v[z] = ld8((const uint16_t*)pp + 4 * lane);   // O / l, fp16
+            const u2_t ml = ld8(pp + HD / 2);
             mz[z] = __uint_as_float(ml[0]);
             lz[z] = __uint_as_float(ml[1]);
             if constexpr (!RELU2) M = fmaxf(M, mz[z]);
@@ -532,10 +541,13 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
 #pragma unroll
     for (int z = 0; z < 4; z++) {
         if (z < a.nsplit) {
-            const float f = RELU2 ? 1.0f : (mz[z] == NEG_INF ? 0.0f : exp2f(mz[z] - M));
-            L += lz[z] * f;
-#pragma unroll
-            for (int i = 0; i < 4; i++) acc[i] += __uint_as_float(v[z][i]) * f;
+            // split z's share: its l, rescaled to the common maximum
+            const float f = lz[z] * (RELU2 ? 1.0f : (mz[z] == NEG_INF ? 0.0f : exp2f(mz[z] - M)));
+            L += f;
+            acc[0] += h2f((uint16_t)(v[z][0] & 0xFFFF)) * f;
+            acc[1] += h2f((uint16_t)(v[z][0] >> 16)) * f;
+            acc[2] += h2f((uint16_t)(v[z][1] & 0xFFFF)) * f;
+            acc[3] += h2f((uint16_t)(v[z][1] >> 16)) * f;
         }
     }
     const float inv = RELU2 ? 1.0f / (11.313708498984761f + L) : 1.0f / L;
