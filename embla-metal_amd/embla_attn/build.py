@@ -25,6 +25,9 @@ FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     # packed fp32 instructions stay off (they have given silent wrong results on this pool)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the AGPR form costs a v_accvgpr_read per result the VALU then
+    # uses (C2 step 9.05 -> 8.78 us; neutral on the other configs)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wno-unused-result", f"-I{INCLUDE}", f"-I{CSRC}",
 ]
 
