@@ -74,6 +74,34 @@ def test_prefill_full_small(torch_gpu, orc, p0, T, window, split):
     assert_close(bf16_host(o), ref, what=f"p0={p0} T={T} w={window}")
 
 
+@pytest.mark.parametrize("tok_pad,head_stride,split", [(4, 128, False), (0, 136, False), (4, 128, True),
+                                                       (0, 136, True)])
+def test_prefill_output_strides(torch_gpu, orc, tok_pad, head_stride, split):
+    """Output rows at general strides: a token stride that breaks 16-byte alignment (the kernel
+    then stores one row a lane) and heads that are not contiguous (coalesced runs of one row)."""
+    from embla_attn import ops
+    torch = torch_gpu
+    say(f"prefill output strides pad={tok_pad} head_stride={head_stride} split={split}")
+    p0, T = 1000, 96
+    c = synth.prefill_case(seed=4, p0=p0, T=T)
+    max_s = ((p0 + T + 31) // 32) * 32
+    kc, vc = upload_prefix(c, max_s)
+    q = dev(c["q"], torch.bfloat16)
+    ops.kv_quant_append(dev(c["kn"], torch.bfloat16), dev(c["vn"], torch.bfloat16), T, p0, 4, kc, vc, max_s)
+    ts = 15 * head_stride + 128 + tok_pad
+    buf = torch.full((T * ts,), float("nan"), dtype=torch.bfloat16, device="cuda")
+    ws = ops.PrefillWorkspace(T, 16) if split else None
+    ops.prefill_int8(q, kc, vc, T, p0, max_s, 4, out=buf, out_strides=(ts, head_stride), ws=ws)
+    got = torch.as_strided(buf, (T, 16, 128), (ts, head_stride, 1))
+    K, ks, V, vs = cache_after_chunk(orc, c)
+    ref = orc.prefill_int8(synth.bf16_val(c["q"]), K, ks, V, vs, p0, weights=0)
+    assert_close(bf16_host(got.contiguous()), ref, what=f"strides ({ts}, {head_stride})")
+    # nothing written between the rows
+    mask = torch.ones(T * ts, dtype=torch.bool, device="cuda")
+    torch.as_strided(mask, (T, 16, 128), (ts, head_stride, 1)).fill_(False)
+    assert torch.isnan(buf[mask].float()).all(), "stores outside the output rows"
+
+
 def test_prefill_c5_full_size_sampled_rows(torch_gpu, orc):
     """Config C5 at full size (T = 2048 after 30720 cached): the edge rows of every 32-row tile
     checked against decode-at-position."""
