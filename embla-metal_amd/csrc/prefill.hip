@@ -372,8 +372,12 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
             const f16_t s0 = s_block(kb0), s1 = s_block(kb0 + 1);
             // scores of the tile's 64 keys: item e of block kb is x[16 kb + e]
             float x[32];
+            // a ring's scores are unscaled (x c): ReLU² scales them here, softmax in the exponent
 #pragma unroll
-            for (int e = 0; e < 16; e++) { x[e] = RING ? s0[e] * c : s0[e]; x[16 + e] = RING ? s1[e] * c : s1[e]; }
+            for (int e = 0; e < 16; e++) {
+                x[e] = RING && RELU2 ? s0[e] * c : s0[e];
+                x[16 + e] = RING && RELU2 ? s1[e] * c : s1[e];
+            }
             if (!full_tile) {   // uniform: only the diagonal (and window-edge) tiles
 #pragma unroll
                 for (int e = 0; e < 32; e++) {
@@ -390,7 +394,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
                     ma = vmax3(ma, x[e], x[e + 1]);
                     mb = vmax3(mb, x[16 + e], x[17 + e]);
                 }
-                const float mt = max_xor32(vmax3(vmax3(ma, mb, x[15]), x[31], x[31]));
+                const float mt = max_xor32(vmax3(vmax3(ma, mb, x[15]), x[31], x[31])) * (RING ? c : 1.0f);
                 // the running maximum moves only when a row's grows by more than 2^8: weights stay
                 // <= 256 (fp16-safe), O and l share the stale m
                 if (__any(mt > m + 8.0f)) {
@@ -412,7 +416,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
                     const float t = fmaxf(v, 0.0f);
                     return t * t;
                 } else {
-                    return __builtin_amdgcn_exp2f(v - msub);
+                    return __builtin_amdgcn_exp2f(RING ? __builtin_fmaf(v, c, -msub) : v - msub);
                 }
             };
             float pw[16];
