@@ -142,7 +142,7 @@ struct PrefillArgs {
     long o_tok_stride, o_head_stride;
     int T, p0, max_s, n_q, n_kv, window;
     int nsplit;              // key-range splits (> 1: partial rows in part, then a merge)
-    float* part;             // [nsplit][T][n_q][132]
+    float* part;             // [nsplit][T][n_q] records of 68 floats: O / l (128 fp16), m, l, pad
     bool relu2, scale32, q_bf16, out_bf16;
     // 16-bit ring source (kring/vring non-null): keys at slot p % R, no scales, MFMA in the ring's type
     const uint16_t* kring;
