@@ -336,13 +336,6 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
         // S^T for keys k0 + 32kb + {8b + 4h + i}: the lane's 16 items e = 4b + i. Both blocks'
         // products are issued before either block's softmax, so one chain runs under the other's
         // VALU work.
-        auto s_block = [&](int kb) -> f16_t {
-            const u4_t* krow = (const u4_t*)(sm.k[b] + (32 * kb + r) * KROW) + h;
-            f16_t st = mfma32x<BF>(krow[0], qb[0], (f16_t){});
-#pragma unroll
-            for (int s = 1; s < 8; s++) st = mfma32x<BF>(krow[2 * s], qb[s], st);
-            return st;
-        };
         // P^T B operands (fp16) of a block's two 16-key k-steps: step s = items b = s (slots
         // 0..3) and b = 2 + s (slots 4..7)
         auto pack = [&](const float* pw, u4_t* pb) {
@@ -369,7 +362,19 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
         };
         // two 32-key blocks kb0, kb0 + 1 of the staged tile: one max and rescale decision
         auto pair = [&](int kb0) {
-            const f16_t s0 = s_block(kb0), s1 = s_block(kb0 + 1);
+            // the two blocks' score chains interleaved (one chain's MFMA under the other's latency)
+            f16_t s0, s1;
+            {
+                const u4_t* k0r = (const u4_t*)(sm.k[b] + (32 * kb0 + r) * KROW) + h;
+                const u4_t* k1r = k0r + 32 * KROW / 8;
+                s0 = mfma32x<BF>(k0r[0], qb[0], (f16_t){});
+                s1 = mfma32x<BF>(k1r[0], qb[0], (f16_t){});
+#pragma unroll
+                for (int s = 1; s < 8; s++) {
+                    s0 = mfma32x<BF>(k0r[2 * s], qb[s], s0);
+                    s1 = mfma32x<BF>(k1r[2 * s], qb[s], s1);
+                }
+            }
             // scores of the tile's 64 keys: item e of block kb is x[16 kb + e]
             float x[32];
             // a ring's scores are unscaled (x c): ReLU² scales them here, softmax in the exponent
