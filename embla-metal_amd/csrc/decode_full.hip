@@ -435,7 +435,7 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
 /// Merges the C chunk partials of query head blockIdx.x, dims 32 * blockIdx.y .. + 31: thread
 /// (slice s of 4 dims, chunk group r) loads its chunks' slices, maxima and sums in one round.
 #ifndef MERGE_DPW
-#define MERGE_DPW 8   // C3 layer: 13.52 us with the LDS-loop merge, 12.98 (32 dims), 12.30 (16), 12.22-12.27 (8)
+#define MERGE_DPW 8   // C3 layer: 13.52 us with the LDS-loop merge, 12.98 (32 dims), 12.30 (16), 12.22-12.27 (8), 12.58 (4)
 #endif
 constexpr int MDPW = MERGE_DPW;   // dims a merge workgroup
 
