@@ -105,18 +105,14 @@ __device__ __forceinline__ u4_t ld16_stream(const void* p) {
 
 // ------------------------------------------------------------------ wave helpers (wave64)
 __device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
-/// v_max3_f32 / v_max_f32 with no canonicalisation of the inputs: for values that are never NaN
-/// (fmaxf makes the compiler quiet each MFMA result first, one more VALU a value).
+/// Maxima on v_maximum3_f32 (IEEE 754-2019 maximum: NaN-propagating, so the compiler quiets no
+/// input first; fmaxf's maxNum made it canonicalise each MFMA result, one more VALU a value). The
+/// compiler sees these operations, so it also keeps the wait states a VALU read of an MFMA result
+/// needs (inline asm here went without them).
 __device__ __forceinline__ float vmax3(float a, float b, float c) {
-    float r;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-    return r;
+    return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
 }
-__device__ __forceinline__ float vmax2(float a, float b) {
-    float r;
-    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-    return r;
-}
+__device__ __forceinline__ float vmax2(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 /// max(v, v of lane xor 32) in every lane, on v_permlane32_swap (VALU, no LDS round trip).
 __device__ __forceinline__ float max_xor32(float v) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);

@@ -99,7 +99,7 @@ __global__ __launch_bounds__(256) void index_mfma_kernel(IndexMfmaArgs a) {
                 float sc = 0.0f;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const float r = vmax2(d[rt][4 * b + i], 0.0f);   // MFMA results: never NaN
+                    const float r = vmax2(d[rt][4 * b + i], 0.0f);
                     sc = __builtin_fmaf(wq[rt][b][i], r * r, sc);
                 }
                 const int row = r0 + 8 * rt + 2 * b + hh;
