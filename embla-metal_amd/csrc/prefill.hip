@@ -175,8 +175,8 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
             } else {
                 // the piece's tile and row j are the wave's (uniform: scalar base addresses, the
                 // lane's part a 32-bit offset)
-                const int gtw = gt, j = (qw % 256) >> 6, l = lane;
-                const int kt = tile_key(k0 + 32 * gtw);
+                const int j = (qw % 256) >> 6, l = lane;
+                const int kt = tile_key(k0 + 32 * gt);
                 const size_t tb0 = tile_base(kvh, a.max_s, kt, 1) + (size_t)(qw % 256) * 16;
                 kr[i] = ld16(a.kc + tb0 + 16 * l);
                 vr[i] = ld16(a.vc + tb0 + 16 * l);
@@ -200,7 +200,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
                 }
                 // keys past the last one the workgroup needs (the last staged tile; maybe never
                 // written) are staged as zero rows: masked keys then add exactly 0 to P·V
-                const int lk = k0 + 32 * gtw;   // the tile's logical first key (kt may be clamped)
+                const int lk = k0 + 32 * gt;   // the tile's logical first key (kt may be clamped)
                 if (lk + 31 > hi) {
                     if (lk + 16 * (j >> 1) + (l & 15) > hi) ksr[i] = 0.0f;
 #pragma unroll
@@ -453,7 +453,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
     // ---- normalise and store: lane (row r, half h) holds dims 32i + 8b + 4h .. + 3. The
     // workgroup's rows are staged in LDS (the tile buffers are free once every wave is past the
     // loop) and written coalesced: a token's GQ heads are one contiguous run, GQ partial records
-    // (132 floats each) or GQ output rows. Each lane holding one row, 32 rows 4 KB apart a store
+    // (PPH floats each) or GQ output rows. Each lane holding one row, 32 rows 4 KB apart a store
     // instruction, cost 4.2 µs a call on the sliding layer's 8.4 MB output.
     lsum += shfl_xor(lsum, 32);
     const float inv = RELU2 ? 1.0f / (11.313708498984761f + lsum) : 1.0f / lsum;
