@@ -45,26 +45,30 @@ typedef _Float16 h8v_t __attribute__((ext_vector_type(8)));
 /// .. + 7 of k-step s. B: lane l: key l % 32, the same dims. D lane (key l % 32, half hh = l / 32)
 /// item e: A row 8 (e / 4) + 4 hh + e % 4, i.e. row ρ = 2 (e / 4) + hh, head e % 4: the 4 heads of
 /// a (row, key) score sit in one lane.
+// 8-row MFMA row tiles a wave (8 rows x 4 heads each): 16 rows a wave; 32 rows (4 tiles, half the
+// key loads an MFMA) measured the same, so the key loads are not what bounds this kernel
+constexpr int IXRT = 2;
 __global__ __launch_bounds__(256) void index_mfma_kernel(IndexMfmaArgs a) {
     const int rb = blockIdx.x, ch = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int c = lane & 31, hh = lane >> 5;
-    const int r0 = 64 * rb + 16 * w;   // the wave's first row
-    h8v_t qa[2][4];
-    float wq[2][4][4];
+    const int r0 = 32 * IXRT * rb + 8 * IXRT * w;   // the wave's first row
+    h8v_t qa[IXRT][4];
+    // the 4 head weights of the workgroup's rows, in LDS (in registers, 16 a row tile: 148 against
+    // 117 VGPRs, and 88-91 against 81-84 us a C5 chunk)
+    __shared__ f4_t wl[32 * IXRT];
+    for (int i = tid; i < 32 * IXRT; i += 256) {
+        const int rw = min(32 * IXRT * rb + i, a.T - 1);
+        wl[i] = (f4_t){a.w[rw * 4], a.w[rw * 4 + 1], a.w[rw * 4 + 2], a.w[rw * 4 + 3]};
+    }
 #pragma unroll
-    for (int rt = 0; rt < 2; rt++) {
+    for (int rt = 0; rt < IXRT; rt++) {
         const int R = lane & 31, row = min(r0 + 8 * rt + (R >> 2), a.T - 1), h = R & 3;
         const uint16_t* qr = a.qi + ((size_t)row * 4 + h) * 64;
 #pragma unroll
         for (int s = 0; s < 4; s++) qa[rt][s] = __builtin_bit_cast(h8v_t, ld16(qr + 16 * s + 8 * hh));
-#pragma unroll
-        for (int b = 0; b < 4; b++) {
-            const int rw = min(r0 + 8 * rt + 2 * b + hh, a.T - 1);
-#pragma unroll
-            for (int i = 0; i < 4; i++) wq[rt][b][i] = a.w[rw * 4 + i];
-        }
     }
+    __syncthreads();
     const int k0 = ch * a.kchunk, k1 = min(a.ld, k0 + a.kchunk);
     const bool norms = rb == 0 && w == 0;   // one wave a chunk takes the key norms
     float nmax = 0.0f;
@@ -73,11 +77,11 @@ __global__ __launch_bounds__(256) void index_mfma_kernel(IndexMfmaArgs a) {
         u4_t kr[4];
 #pragma unroll
         for (int s = 0; s < 4; s++) kr[s] = key < a.nk ? ld16(a.ki + (size_t)key * 64 + 16 * s + 8 * hh) : (u4_t){0, 0, 0, 0};
-        f16_t d[2] = {};
+        f16_t d[IXRT] = {};
 #pragma unroll
         for (int s = 0; s < 4; s++)
 #pragma unroll
-            for (int rt = 0; rt < 2; rt++)
+            for (int rt = 0; rt < IXRT; rt++)
                 d[rt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(qa[rt][s], __builtin_bit_cast(h8v_t, kr[s]), d[rt], 0, 0, 0);
         if (norms) {   // this key's squared norm (half the dims a lane), for the chunk maximum
             float ss = 0.0f;
@@ -93,14 +97,15 @@ __global__ __launch_bounds__(256) void index_mfma_kernel(IndexMfmaArgs a) {
             nmax = fmaxf(nmax, ss);
         }
 #pragma unroll
-        for (int rt = 0; rt < 2; rt++)
+        for (int rt = 0; rt < IXRT; rt++)
 #pragma unroll
             for (int b = 0; b < 4; b++) {
                 float sc = 0.0f;
+                const f4_t wv = wl[8 * IXRT * w + 8 * rt + 2 * b + hh];
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const float r = vmax2(d[rt][4 * b + i], 0.0f);
-                    sc = __builtin_fmaf(wq[rt][b][i], r * r, sc);
+                    sc = __builtin_fmaf(wv[i], r * r, sc);
                 }
                 const int row = r0 + 8 * rt + 2 * b + hh;
                 if (row < a.T) a.keys[(size_t)row * a.ld + key] = key < row + a.lim0 ? (uint16_t)(ob32(sc) >> 16) : 0;
@@ -115,7 +120,7 @@ __global__ __launch_bounds__(256) void index_mfma_kernel(IndexMfmaArgs a) {
 }
 
 int launch_index_mfma(const IndexMfmaArgs& a, hipStream_t st) {
-    const dim3 grid((a.T + 63) / 64, (a.ld + a.kchunk - 1) / a.kchunk);
+    const dim3 grid((a.T + 32 * IXRT - 1) / (32 * IXRT), (a.ld + a.kchunk - 1) / a.kchunk);
     hipLaunchKernelGGL(index_mfma_kernel, grid, dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
 }
