@@ -656,7 +656,8 @@ size_t embla_sparse_prefill_workspace_bytes(int T, int p0) {
     if (T <= 0 || p0 < 0) return 0;
     const size_t ld = round_up((size_t)(p0 + T > kRecent ? p0 + T - kRecent : 1), kIndexChunk);
     const size_t nch = ld / kIndexChunk;
-    return round_up((size_t)T * ld * 2, 256) + round_up(nch * 4, 256) + (size_t)T * (kTopK + kRecent) * 4;
+    return round_up((size_t)T * ld * 2, 256) + round_up(nch * 4, 256) + round_up((size_t)T * 8, 256) +
+           (size_t)T * (kTopK + kRecent) * 4;
 }
 
 int embla_prefill_sparse(const void* q, const void* k, const void* v, const void* qi, const float* w, const void* ki,
@@ -673,6 +674,8 @@ int embla_prefill_sparse(const void* q, const void* k, const void* v, const void
     wp += round_up((size_t)T * ld * 2, 256);
     float* kmax = (float*)wp;
     wp += round_up((size_t)nch * 4, 256);
+    uint32_t* ovf = (uint32_t*)wp;   // the band select's overflow records
+    wp += round_up((size_t)T * 8, 256);
     uint32_t* sel = idx ? idx : (uint32_t*)wp;
     // the chunk's K, V quantised into the row-major int8 cache
     KVQuantArgs qa{(const uint16_t*)k, (const uint16_t*)v, n_kv * 128, T, p0, n_kv, max_s,
@@ -683,7 +686,7 @@ int embla_prefill_sparse(const void* q, const void* k, const void* v, const void
                      p0 + 1 - kRecent};
     if ((rc = launch_index_mfma(ia, stream))) return rc;
     BandSelectArgs ba{keys, ld, (const uint16_t*)qi, w, (const uint16_t*)ki, kmax, nch, sel, kTopK + kRecent,
-                      T, p0, kTopK, kRecent};
+                      T, p0, kTopK, kRecent, ovf};
     if ((rc = launch_select_band(ba, stream))) return rc;
     SparseRows8Args sa{(const uint16_t*)q, (long)n_q * 128, (const int8_t*)kc, (const int8_t*)vc, sel,
                        kTopK + kRecent, 0, kTopK + kRecent, p0, T, (uint16_t*)o, (long)n_q * 128, nullptr,

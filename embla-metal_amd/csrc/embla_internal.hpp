@@ -129,6 +129,7 @@ struct BandSelectArgs {
     uint32_t* idx;
     int idx_stride;
     int T, p0, topk, recent;
+    uint32_t* ovf;         // [T][2]: a row's band bounds {kin, kout} when its band overflows, else {0, 0}
 };
 int launch_select_band(const BandSelectArgs& a, hipStream_t st);
 int launch_select_topk(const float* scores, int score_stride, uint32_t* idx, int idx_stride, int S, int n_sets,

@@ -18,7 +18,8 @@
 //     hi(T) + 2ε are selected, entirely below lo(T) − 2ε rejected, and only the band between is
 //     rescored with the spec itself (a handful of keys a row) and ranked exactly. Every decision
 //     is therefore the spec's. The ordered compaction then writes the indices in select_keys'
-//     order.
+//     order. A band too large to list (scores massed at the k-th value) is left to
+//     band_overflow_kernel, which scores it once into LDS and ranks it there.
 //  3. sparse_rows8_kernel (decode_sparse.hip): gathered attention over a row-major int8 cache.
 #include "common.hpp"
 #include "embla_internal.hpp"
@@ -148,9 +149,10 @@ struct BandSmem {
     uint32_t kin, kout;
 };
 
-/// The spec score of key j (index_scores_kernel's order), the row's queries and weights in LDS:
-/// chain k of head h is dims 8k .. 8k + 7, one 16-byte load of the key.
-__device__ __noinline__ float spec_score(const BandSmem& sm, const uint16_t* __restrict__ ki, int j) {
+/// The spec score of key j (index_scores_kernel's order), the row's queries qf[4][64] and weights
+/// wq[4] in LDS: chain k of head h is dims 8k .. 8k + 7, one 16-byte load of the key.
+__device__ __forceinline__ float spec_score_q(const float (*qf)[64], const float* wq, const uint16_t* __restrict__ ki,
+                                              int j) {
     float cc[4][8];
     const u4_t* kr = (const u4_t*)(ki + (size_t)j * 64);
 #pragma unroll
@@ -163,7 +165,7 @@ __device__ __noinline__ float spec_score(const BandSmem& sm, const uint16_t* __r
         for (int h = 0; h < 4; h++) {
             float acc = 0.0f;
 #pragma unroll
-            for (int d = 0; d < 8; d++) acc = __builtin_fmaf(sm.qf[h][8 * k + d], kf[d], acc);
+            for (int d = 0; d < 8; d++) acc = __builtin_fmaf(qf[h][8 * k + d], kf[d], acc);
             cc[h][k] = acc;
         }
     }
@@ -172,14 +174,18 @@ __device__ __noinline__ float spec_score(const BandSmem& sm, const uint16_t* __r
     for (int h = 0; h < 4; h++) {
         const float dot = ((cc[h][0] + cc[h][1]) + (cc[h][2] + cc[h][3])) + ((cc[h][4] + cc[h][5]) + (cc[h][6] + cc[h][7]));
         const float r = fmaxf(dot, 0.0f);
-        s = __builtin_fmaf(sm.wq[h], r * r, s);
+        s = __builtin_fmaf(wq[h], r * r, s);
     }
     return s;
+}
+__device__ __noinline__ float spec_score(const BandSmem& sm, const uint16_t* __restrict__ ki, int j) {
+    return spec_score_q(sm.qf, sm.wq, ki, j);
 }
 
 /// Digit (of 256, histogram copies `nc` at stride BS_HS) holding the k-th largest: sel = {digit,
 /// keys in digits above}. Wave 0, 4 digits a lane from the top.
-__device__ void bs_pick(BandSmem& sm, int nc, uint32_t k) {
+template <class Sm>
+__device__ void bs_pick(Sm& sm, int nc, uint32_t k) {
     const int tid = threadIdx.x, lane = tid & 63;
     if (tid < 64) {
         uint32_t cc[4], s = 0;
@@ -243,6 +249,50 @@ __device__ void bs_pick1(BandSmem& sm, uint32_t k) {
         if (base + incl - c < k && base + incl >= k) { sm.sel[0] = (uint32_t)d; sm.sel[1] = base + incl - c; }
     }
     __syncthreads();
+}
+
+/// The selection in select_keys' order from the bitmaps sm.gt (keys above the k-th's score) and
+/// sm.eq (keys equal to it): the keys of gt by index, then the first k of eq by index, then the
+/// latest positions n .. n + recent - 1. Thread i holds keys 64 i .. + 63 of each bitmap; a block
+/// scan of the counts gives its first slot. BS_T threads.
+template <class Sm>
+__device__ void bs_emit(Sm& sm, uint32_t k, uint32_t* __restrict__ out, int n, int topk, int recent) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    auto block_scan = [&](uint32_t c, uint32_t& total) -> uint32_t {
+        uint32_t incl = c;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t x = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += x;
+        }
+        if (lane == 63) sm.wsum[w] = incl;
+        __syncthreads();
+        uint32_t before = 0;
+        total = 0;
+#pragma unroll
+        for (int i = 0; i < BS_T / 64; i++) {
+            const uint32_t x = sm.wsum[i];
+            before += i < w ? x : 0u;
+            total += x;
+        }
+        __syncthreads();   // wsum is reused by the next scan
+        return before + incl - c;
+    };
+    uint32_t ngt;
+    {
+        uint32_t g0 = sm.gt[2 * tid], g1 = sm.gt[2 * tid + 1];
+        uint32_t p = block_scan(__popc(g0) + __popc(g1), ngt);
+        for (; g0; g0 &= g0 - 1) out[p++] = 64u * tid + __ffs(g0) - 1;
+        for (; g1; g1 &= g1 - 1) out[p++] = 64u * tid + 32u + __ffs(g1) - 1;
+    }
+    if (k > 0) {   // ties (k is uniform)
+        uint32_t e0 = sm.eq[2 * tid], e1 = sm.eq[2 * tid + 1];
+        uint32_t neq;
+        uint32_t p = block_scan(__popc(e0) + __popc(e1), neq);
+        for (; e0 && p < k; e0 &= e0 - 1) out[ngt + p++] = 64u * tid + __ffs(e0) - 1;
+        for (; e1 && p < k; e1 &= e1 - 1) out[ngt + p++] = 64u * tid + 32u + __ffs(e1) - 1;
+    }
+    for (int j = tid; j < recent; j += BS_T) out[topk + j] = (uint32_t)(n + j);
 }
 
 __global__ __launch_bounds__(BS_T) __attribute__((amdgpu_waves_per_eu(6))) void select_band_kernel(BandSelectArgs a) {
@@ -353,9 +403,14 @@ __global__ __launch_bounds__(BS_T) __attribute__((amdgpu_waves_per_eu(6))) void 
                 const bool above = key >= kin;
                 sa += (uint32_t)__popcll(__ballot(above));
                 bits |= (uint32_t)above << e;
-                if (key >= kout && !above) {
-                    const uint32_t p = atomicAdd(&sm.cnt[0], 1u);
-                    if (p < BS_LB) sm.bj[p] = (uint32_t)(j + e);
+                const bool inb = key >= kout && !above;
+                const uint64_t bm = __ballot(inb);
+                if (bm) {   // one LDS atomic a wave (scores massed at the k-th value put every lane here)
+                    uint32_t p0 = 0;
+                    if (lane == __ffsll((long long)bm) - 1) p0 = atomicAdd(&sm.cnt[0], (uint32_t)__popcll(bm));
+                    p0 = __shfl(p0, __ffsll((long long)bm) - 1, 64);
+                    const uint32_t p = p0 + (uint32_t)__popcll(bm & ((1ull << lane) - 1));
+                    if (inb && p < BS_LB) sm.bj[p] = (uint32_t)(j + e);
                 }
             }
             ((uint8_t*)sm.gt)[j >> 3] = (uint8_t)bits;
@@ -365,28 +420,20 @@ __global__ __launch_bounds__(BS_T) __attribute__((amdgpu_waves_per_eu(6))) void 
     __syncthreads();
     const uint32_t nband = sm.cnt[0];
     k = (uint32_t)a.topk - sm.cnt[1];   // rank of the spec's k-th largest among the band
-    const bool listed = nband <= BS_LB;
-    if (listed)
-        for (uint32_t q = tid; q < nband; q += BS_T) sm.bx[q] = ob32(spec_score(sm, a.ki, sm.bj[q]));
+    // a band too large to list goes to band_overflow_kernel, which ranks it from an LDS array of
+    // every key's spec score: the row's bounds are its record there (kin = 0: no overflow)
+    if (tid == 0) *(uint2*)(a.ovf + 2 * t) = nband <= BS_LB ? make_uint2(0u, 0u) : make_uint2(kin, kout);
+    if (nband > BS_LB) return;   // uniform
+    for (uint32_t q = tid; q < nband; q += BS_T) sm.bx[q] = ob32(spec_score(sm, a.ki, sm.bj[q]));
     __syncthreads();
     // ---- exact rank within the band: four 8-bit passes over the band's spec scores
     uint32_t pre = 0, msk = 0;
     for (int shift = 24; shift >= 0; shift -= 8) {
         for (int q = tid; q < BS_HS; q += BS_T) sm.hist[q] = 0;
         __syncthreads();
-        if (listed) {
-            for (uint32_t q = tid; q < nband; q += BS_T) {
-                const uint32_t x = sm.bx[q];
-                if ((x & msk) == pre) atomicAdd(&sm.hist[(x >> shift) & 255u], 1u);
-            }
-        } else {   // a band too large to list: rescore it from the keys on every pass
-            for (int j = tid; j < n; j += BS_T) {
-                const uint32_t key = kr[j];
-                if (key >= kout && key < kin) {
-                    const uint32_t x = ob32(spec_score(sm, a.ki, j));
-                    if ((x & msk) == pre) atomicAdd(&sm.hist[(x >> shift) & 255u], 1u);
-                }
-            }
+        for (uint32_t q = tid; q < nband; q += BS_T) {
+            const uint32_t x = sm.bx[q];
+            if ((x & msk) == pre) atomicAdd(&sm.hist[(x >> shift) & 255u], 1u);
         }
         __syncthreads();
         bs_pick(sm, 1, k);
@@ -403,58 +450,209 @@ __global__ __launch_bounds__(BS_T) __attribute__((amdgpu_waves_per_eu(6))) void 
         if (x > E) atomicOr(&sm.gt[j >> 5], 1u << (j & 31));
         else if (x == E) atomicOr(&sm.eq[j >> 5], 1u << (j & 31));
     };
-    if (listed) {
-        for (uint32_t q = tid; q < nband; q += BS_T) mark((int)sm.bj[q], sm.bx[q]);
-    } else {
-        for (int j = tid; j < n; j += BS_T) {
-            const uint32_t key = kr[j];
-            if (key >= kout && key < kin) mark(j, ob32(spec_score(sm, a.ki, j)));
-        }
-    }
+    for (uint32_t q = tid; q < nband; q += BS_T) mark((int)sm.bj[q], sm.bx[q]);
     __syncthreads();
-    // ---- the output in select_keys' order: the keys above E by index, then the first k equal
-    // to E by index. Thread i holds keys 64 i .. + 63 of each bitmap; a block scan of the counts
-    // gives its first slot.
-    auto block_scan = [&](uint32_t c, uint32_t& total) -> uint32_t {
-        uint32_t incl = c;
+    bs_emit(sm, k, out, n, a.topk, a.recent);
+}
+
+// ------------------------------------------------------------------ 2b. bands too large to list
+// A row whose band holds more than BS_LB keys (scores massed at the k-th value, such as many exact
+// zeros of ReLU²) is ranked here: each band key's spec score is computed once into an LDS array
+// indexed by key (128 KB, one workgroup a CU), then the same four 8-bit rank passes and the same
+// output as select_band_kernel run over that array. Persistent: workgroup b takes rows b, b +
+// gridDim.x, ...; a row without an overflow record costs one 8-byte load.
+struct OvfSmem {
+    uint32_t xs[BS_MAXN];        // order bits of band key j's spec score (set for band keys only)
+    uint32_t bd[BS_MAXN / 32];   // bitmap of the band keys
+    uint32_t gt[BS_MAXN / 32];   // bitmap of the selected keys above the k-th's score
+    uint32_t eq[BS_MAXN / 32];   // bitmap of the band keys whose spec score equals the k-th's
+    uint32_t hist[BS_HS];
+    float qf[4][64];
+    float wq[4];
+    uint32_t sel[2];
+    uint32_t above;              // keys surely above (keys >= kin)
+    uint32_t wsum[8];
+};
+constexpr int BO_GRID = 256;   // one workgroup a CU (fewer measured slower when many rows overflow)
+
+constexpr int OV_NK = 2;   // band keys a thread scores at once (1 and 4 measured slower)
+static_assert(BS_MAXN / 32 == 2 * BS_T, "two bitmap words a thread");
+
+/// spec_score_q of the NK keys j[], their loads all in flight together. The queries are read from
+/// LDS a chunk of 8 dims at a time; the arithmetic is spec_score_q's, operation for operation.
+template <int NK>
+__device__ __forceinline__ void spec_scores_n(const float (*qf)[64], const float* wq, const uint16_t* __restrict__ ki,
+                                              const int (&j)[NK], float (&x)[NK]) {
+    u4_t kv[NK][8];
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t x = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += x;
+    for (int n = 0; n < NK; n++)
+#pragma unroll
+        for (int k = 0; k < 8; k++) kv[n][k] = ((const u4_t*)(ki + (size_t)j[n] * 64))[k];
+    float cc[NK][4][8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        // chunk k - 1's sums are done before chunk k's queries are read, which are read here and
+        // not earlier: one chunk of queries in registers (else all 256 are hoisted and spill)
+        if (k > 0)
+#pragma unroll
+            for (int n = 0; n < NK; n++)
+#pragma unroll
+                for (int h = 0; h < 4; h++) __asm__ volatile("" : : "v"(cc[n][h][k - 1]));
+        int z = 0;
+        __asm__ volatile("" : "+s"(z) : : "memory");
+        float qv[4][8];
+#pragma unroll
+        for (int h = 0; h < 4; h++)
+#pragma unroll
+            for (int d = 0; d < 8; d++) qv[h][d] = qf[h][8 * k + d + z];
+#pragma unroll
+        for (int n = 0; n < NK; n++) {
+            float kf[8];
+#pragma unroll
+            for (int i = 0; i < 4; i++) { kf[2 * i] = h2f(kv[n][k][i] & 0xFFFF); kf[2 * i + 1] = h2f(kv[n][k][i] >> 16); }
+#pragma unroll
+            for (int h = 0; h < 4; h++) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int d = 0; d < 8; d++) acc = __builtin_fmaf(qv[h][d], kf[d], acc);
+                cc[n][h][k] = acc;
+            }
         }
-        if (lane == 63) sm.wsum[w] = incl;
+    }
+#pragma unroll
+    for (int n = 0; n < NK; n++) {
+        float s = 0.0f;
+#pragma unroll
+        for (int h = 0; h < 4; h++) {
+            const float* c = cc[n][h];
+            const float dot = ((c[0] + c[1]) + (c[2] + c[3])) + ((c[4] + c[5]) + (c[6] + c[7]));
+            const float r = fmaxf(dot, 0.0f);
+            s = __builtin_fmaf(wq[h], r * r, s);
+        }
+        x[n] = s;
+    }
+}
+
+__global__ __launch_bounds__(BS_T) void band_overflow_kernel(BandSelectArgs a) {
+    __shared__ OvfSmem sm;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int G = gridDim.x;
+    for (int i0 = 0; (int)blockIdx.x + G * i0 < a.T; i0 += 64) {
+      // the records of rows blockIdx.x + G (i0 + lane), read by every wave alike: a mask of the
+      // rows that overflowed (select_band_kernel writes no record for a row without selection)
+      const int tl = (int)blockIdx.x + G * (i0 + lane);
+      const bool ov = tl < a.T && a.p0 + tl + 1 > a.topk + a.recent && a.ovf[2 * tl] != 0;
+      for (uint64_t rows = __ballot(ov); rows; rows &= rows - 1) {
+        const int t = (int)blockIdx.x + G * (i0 + __ffsll((long long)rows) - 1);
+        const int S = a.p0 + t + 1;
+        const uint2 rec = *(const uint2*)(a.ovf + 2 * t);
+        const uint32_t kin = rec.x, kout = rec.y;
+        const int n = S - a.recent;
+        uint32_t* out = a.idx + (size_t)t * a.idx_stride;
+        const uint16_t* kr = a.keys + (size_t)t * a.ld;
+        __syncthreads();   // the previous row is done with sm
+        if (tid < 256) sm.qf[tid >> 6][tid & 63] = h2f(a.qi[(size_t)t * 256 + tid]);
+        if (tid < 4) sm.wq[tid] = a.w[t * 4 + tid];
+        if (tid == 0) sm.above = 0;
         __syncthreads();
-        uint32_t before = 0;
-        total = 0;
+        // words tid and tid + BS_T: keys 32 wd .. + 31 (ld is a multiple of 32; the index kernel
+        // stored 0, below kout, for keys past n); bit e of a word is key 32 wd + e, as bs_emit
+        // reads the bitmaps
+        uint32_t nab = 0;
+        uint64_t band = 0;
 #pragma unroll
-        for (int i = 0; i < BS_T / 64; i++) {
-            const uint32_t x = sm.wsum[i];
-            before += i < w ? x : 0u;
-            total += x;
+        for (int hw = 0; hw < 2; hw++) {
+            const int wd = tid + BS_T * hw;
+            uint32_t ab = 0, bd = 0;
+            if (32 * wd < n) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const u4_t v = ld16(kr + 32 * wd + 8 * c);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        const uint32_t key = (v[e >> 1] >> (16 * (e & 1))) & 0xFFFF;
+                        ab |= (uint32_t)(key >= kin) << (8 * c + e);
+                        bd |= (uint32_t)(key >= kout && key < kin) << (8 * c + e);
+                    }
+                }
+            }
+            sm.gt[wd] = ab;
+            sm.bd[wd] = bd;
+            nab += __popc(ab);
+            band |= (uint64_t)bd << (32 * hw);
         }
-        __syncthreads();   // wsum is reused by the next scan
-        return before + incl - c;
-    };
-    uint32_t ngt;
-    {
-        uint32_t g0 = sm.gt[2 * tid], g1 = sm.gt[2 * tid + 1];
-        uint32_t p = block_scan(__popc(g0) + __popc(g1), ngt);
-        for (; g0; g0 &= g0 - 1) out[p++] = 64u * tid + __ffs(g0) - 1;
-        for (; g1; g1 &= g1 - 1) out[p++] = 64u * tid + 32u + __ffs(g1) - 1;
+        while (band) {   // the thread's band keys, OV_NK at a time (spare slots repeat the first)
+            int jj[OV_NK];
+            bool ok[OV_NK];
+#pragma unroll
+            for (int i = 0; i < OV_NK; i++) {
+                ok[i] = band != 0;
+                const int e = ok[i] ? __ffsll((long long)band) - 1 : 0;
+                const int j = e < 32 ? 32 * tid + e : 32 * (tid + BS_T) + e - 32;
+                jj[i] = i == 0 || ok[i] ? j : jj[0];
+                band &= band - 1;
+            }
+            float x[OV_NK];
+            spec_scores_n<OV_NK>(sm.qf, sm.wq, a.ki, jj, x);
+#pragma unroll
+            for (int i = 0; i < OV_NK; i++)
+                if (ok[i]) sm.xs[jj[i]] = ob32(x[i]);
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) nab += (uint32_t)__shfl_xor((int)nab, o, 64);
+        if (lane == 0 && nab) atomicAdd(&sm.above, nab);
+        __syncthreads();
+        uint32_t k = (uint32_t)a.topk - sm.above;   // rank of the spec's k-th largest in the band
+        const int nw = (n + 31) / 32;
+        uint32_t pre = 0, msk = 0;
+        for (int shift = 24; shift >= 0; shift -= 8) {
+            for (int q = tid; q < BS_HS; q += BS_T) sm.hist[q] = 0;
+            __syncthreads();
+            for (int wd = tid; wd < nw; wd += BS_T) {
+                uint32_t rd = 0, rc = 0;   // a run of equal digits: one atomic a run
+                for (uint32_t b = sm.bd[wd]; b; b &= b - 1) {
+                    const uint32_t x = sm.xs[32 * wd + __ffs(b) - 1];
+                    if ((x & msk) != pre) continue;
+                    const uint32_t d = (x >> shift) & 255u;
+                    if (rc && d != rd) {
+                        atomicAdd(&sm.hist[rd], rc);
+                        rc = 0;
+                    }
+                    rd = d;
+                    rc++;
+                }
+                if (rc) atomicAdd(&sm.hist[rd], rc);
+            }
+            __syncthreads();
+            bs_pick(sm, 1, k);
+            pre |= sm.sel[0] << shift;
+            msk |= 255u << shift;
+            k -= sm.sel[1];
+            __syncthreads();
+        }
+        const uint32_t E = pre;   // the spec's k-th largest score; k = ties to take, first by index
+        for (int wd = tid; wd < BS_MAXN / 32; wd += BS_T) {
+            uint32_t g = 0, q = 0;
+            for (uint32_t b = sm.bd[wd]; b; b &= b - 1) {
+                const int e = __ffs(b) - 1;
+                const uint32_t x = sm.xs[32 * wd + e];
+                g |= (uint32_t)(x > E) << e;
+                q |= (uint32_t)(x == E) << e;
+            }
+            sm.gt[wd] |= g;
+            sm.eq[wd] = q;
+        }
+        __syncthreads();
+        bs_emit(sm, k, out, n, a.topk, a.recent);
+      }
     }
-    if (k > 0) {   // ties (k is uniform)
-        uint32_t e0 = sm.eq[2 * tid], e1 = sm.eq[2 * tid + 1];
-        uint32_t neq;
-        uint32_t p = block_scan(__popc(e0) + __popc(e1), neq);
-        for (; e0 && p < k; e0 &= e0 - 1) out[ngt + p++] = 64u * tid + __ffs(e0) - 1;
-        for (; e1 && p < k; e1 &= e1 - 1) out[ngt + p++] = 64u * tid + 32u + __ffs(e1) - 1;
-    }
-    for (int j = tid; j < a.recent; j += BS_T) out[a.topk + j] = (uint32_t)(n + j);
 }
 
 int launch_select_band(const BandSelectArgs& a, hipStream_t st) {
-    if (a.p0 + a.T - a.recent > BS_MAXN) return EMBLA_ERR_UNSUPPORTED;
+    if (a.p0 + a.T - a.recent > BS_MAXN || a.ld % 32 || !a.ovf) return EMBLA_ERR_UNSUPPORTED;
     hipLaunchKernelGGL(select_band_kernel, dim3(a.T), dim3(BS_T), 0, st, a);
+    if (hipGetLastError() != hipSuccess) return EMBLA_ERR_HIP;
+    hipLaunchKernelGGL(band_overflow_kernel, dim3(a.T < BO_GRID ? a.T : BO_GRID), dim3(BS_T), 0, st, a);
     return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
 }
 

@@ -113,6 +113,33 @@ def test_prefill_sparse_all_equal_band_overflow(torch_gpu, orc):
     check_rows(orc, c, got, idx, range(T), oracle_cache(orc, c))
 
 
+def test_prefill_sparse_zero_ties_band_overflow(torch_gpu, orc):
+    """Most index keys zero: their scores are exactly 0 and fewer than 1024 keys score above 0, so
+    the 1024th score is a tie at 0 among ~3800 keys (a band too large to list: the overflow kernel),
+    taken by lower index."""
+    p0, T = 4000, 6
+    c = synth.sparse_prefill_case(seed=9, p0=p0, T=T)
+    c["ki"][150:3950] = 0
+    say("prefill sparse zero ties")
+    got, idx, _, _ = run(torch_gpu, c)
+    check_rows(orc, c, got, idx, range(T), oracle_cache(orc, c))
+
+
+def test_prefill_sparse_small_scores_band_overflow(torch_gpu, orc):
+    """Most index keys 1000x smaller than the rest: their distinct scores all lie within the error
+    bound of the 1024th (set by the largest key norm), so the band overflows and is ranked exactly
+    by the overflow kernel; a few mid-sized keys make the selection mix both kinds."""
+    p0, T = 3000, 5
+    c = synth.sparse_prefill_case(seed=10, p0=p0, T=T)
+    ki = synth.f16_val(c["ki"])
+    ki[:p0 - 200] *= 1e-3
+    ki[500:p0 - 200:40] *= 30.0
+    c["ki"] = synth.f16_bits(ki)
+    say("prefill sparse small scores")
+    got, idx, _, _ = run(torch_gpu, c)
+    check_rows(orc, c, got, idx, range(T), oracle_cache(orc, c))
+
+
 def test_prefill_sparse_c5_size_all_rows(torch_gpu, orc):
     """C5 sparse at full size: 2048 rows after 30720 cached positions. Every row's selection
     against the SHA-256 of the oracle's (tests/golden/c5_sparse_selection.npz, same seeded
