@@ -500,9 +500,12 @@ int embla_select_keys(const float* scores, uint32_t* idx, int S, int maxS, hipSt
     return embla_select_topk(scores, maxS, idx, kTopK + kRecent, S, 2, kTopK, kRecent, stream);
 }
 
-int embla_sparse_decode(const void* q, const void* kc, const void* vc, const uint32_t* idx, int idx_stride,
-                        int nsel, void* o, int max_s, int n_q, int n_kv, int dtype, int chunk, void* ws,
-                        size_t ws_bytes, hipStream_t stream) {
+namespace {
+/// embla_sparse_decode, optionally with the wide select's last step fused (fs: its fields of
+/// SparseArgs, sel_* set).
+int sparse_decode_impl(const void* q, const void* kc, const void* vc, const uint32_t* idx, int idx_stride, int nsel,
+                       void* o, int max_s, int n_q, int n_kv, int dtype, int chunk, void* ws, size_t ws_bytes,
+                       const SparseArgs* fs, hipStream_t stream) {
     if (!q || !kc || !vc || !o || nsel <= 0 || max_s <= 0 || idx_stride < 0) return EMBLA_ERR_INVALID;
     if (!idx && nsel > max_s) return EMBLA_ERR_INVALID;
     if (n_kv <= 0 || n_q % n_kv || n_kv > kMaxKV || !valid_act(dtype)) return EMBLA_ERR_INVALID;
@@ -518,7 +521,19 @@ int embla_sparse_decode(const void* q, const void* kc, const void* vc, const uin
     a.part = ws ? carve(ws, 32 * C, n_q).part : nullptr;
     a.o = (uint16_t*)o;
     a.CH = ch; a.C = C; a.max_s = max_s; a.n_q = n_q; a.n_kv = n_kv; a.bf16 = dtype == EMBLA_BF16;
+    if (fs) {
+        a.sel_ws = fs->sel_ws; a.sel_n = fs->sel_n; a.sel_topk = fs->sel_topk;
+        a.sel_out = fs->sel_out; a.sel_epoch = fs->sel_epoch;
+    }
     return launch_sparse_decode(a, stream);
+}
+}  // namespace
+
+int embla_sparse_decode(const void* q, const void* kc, const void* vc, const uint32_t* idx, int idx_stride,
+                        int nsel, void* o, int max_s, int n_q, int n_kv, int dtype, int chunk, void* ws,
+                        size_t ws_bytes, hipStream_t stream) {
+    return sparse_decode_impl(q, kc, vc, idx, idx_stride, nsel, o, max_s, n_q, n_kv, dtype, chunk, ws, ws_bytes,
+                              nullptr, stream);
 }
 
 size_t embla_sparse_workspace_bytes(int max_s, int n_q) {
@@ -543,10 +558,16 @@ int embla_sparse_layer_decode(const void* q, const void* qi, const float* w, con
     // index scores, then the exact top-k on many workgroups (the select's workspace follows the
     // decode's; it is zero before the first call and every call leaves it zero)
     uint32_t* sel_ws = (uint32_t*)((char*)aws + round_up(abytes, 256));
+    // (its last step runs inside the attention's workgroups, each ranking the rows it attends;
+    // the selection still lands in idx)
     const int rc = launch_wide_select((const uint16_t*)qi, w, (const uint16_t*)ki, scores, S, n_ih, kTopK, kRecent,
-                                      sel_ws, idx, stream);
+                                      sel_ws, nullptr, stream);
     if (rc) return rc;
-    return embla_sparse_decode(q, kc, vc, idx, 0, kTopK + kRecent, o, max_s, n_q, n_kv, dtype, 0, aws, abytes, stream);
+    SparseArgs fs;
+    fs.sel_ws = sel_ws; fs.sel_n = S - kRecent; fs.sel_topk = kTopK; fs.sel_out = idx;
+    fs.sel_epoch = sel_ws + kWideSelectEpoch;
+    return sparse_decode_impl(q, kc, vc, nullptr, 0, kTopK + kRecent, o, max_s, n_q, n_kv, dtype, 0, aws, abytes, &fs,
+                              stream);
 }
 
 size_t embla_prefill_workspace_bytes(int T, int n_q) {

@@ -10,8 +10,14 @@
 // operand of S^T = K q^T is read back from it as 16-byte rows, and the V operand of O += W V is
 // assembled from eight 16-byte row reads a lane (a register transpose), so both products run on
 // v_mfma_f32_16x16x32_{f16,bf16}.
+//
+// In the sparse-layer step (embla_sparse_layer_decode) the rows come straight from the wide select:
+// each workgroup runs the select's last step for the ranks it attends (wsel_slice, wsel.hpp) in
+// its staging LDS before the first gather, so the selection needs no launch of its own and no
+// round trip through the index list; kv head 0's workgroups still write the list.
 #include "common.hpp"
 #include "embla_internal.hpp"
+#include "wsel.hpp"
 
 namespace embla {
 
@@ -31,7 +37,9 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int GQ, bool BF>
+constexpr int SPD_FS_MAXCH = 256;   // keys a workgroup with the select's last step fused
+
+template <int GQ, bool BF, bool FS>
 __global__ __launch_bounds__(256) void sparse_decode_kernel(SparseArgs a) {
     const int c = blockIdx.x, kvh = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -41,9 +49,19 @@ __global__ __launch_bounds__(256) void sparse_decode_kernel(SparseArgs a) {
     const uint16_t* kb = a.kc + (size_t)kvh * a.max_s * HD;
     const uint16_t* vb = a.vc + (size_t)kvh * a.max_s * HD;
 
-    __shared__ uint16_t stage[4][2][32 * SROW];
+    __shared__ __attribute__((aligned(16))) uint16_t stage[4][2][32 * SROW];
     uint16_t* Ks = stage[w][0];
     uint16_t* Vs = stage[w][1];
+    __shared__ uint32_t srows[FS ? SPD_FS_MAXCH : 1];   // FS: the chunk's selected rows
+    if constexpr (FS) {
+        // ranks j0 .. ts - 1 of the selection, from the wide select's last step (its scratch is
+        // the staging LDS, free until the first gather); the rows go to the output at the end
+        const int ts = min(j1, a.sel_topk);
+        if (j0 < ts)   // uniform
+            wsel_slice<256>(a.sel_n, a.sel_topk, a.sel_ws, (uint32_t*)&stage[0][0][0], (int)(sizeof(stage) / 4),
+                            (uint32_t)j0, (uint32_t)(ts - j0), srows, nullptr);
+        __syncthreads();
+    }
 
     // q^T, B operand: lane (head n, group g), MFMA u: dims 32g + 8u .. + 7
     u4_t qb[4];
@@ -64,7 +82,10 @@ __global__ __launch_bounds__(256) void sparse_decode_kernel(SparseArgs a) {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int p = t0 + 4 * j + (lane >> 4);
-            const size_t row = p < j1 ? (size_t)min(rows ? (int)rows[p] : p, a.max_s - 1) : 0;   // rows clamped in range
+            int r = p;
+            if constexpr (FS) r = p < a.sel_topk ? (int)srows[p - j0] : a.sel_n + p - a.sel_topk;
+            else if (rows) r = (int)rows[p];
+            const size_t row = p < j1 ? (size_t)min(r, a.max_s - 1) : 0;   // rows clamped in range
             kr[j] = ld16(kb + row * HD + 8 * n);
             vr[j] = ld16(vb + row * HD + 8 * n);
         }
@@ -165,6 +186,12 @@ __global__ __launch_bounds__(256) void sparse_decode_kernel(SparseArgs a) {
         acc[e] = s;
     }
     const int hq = kvh * GQ + oh;
+    if constexpr (FS) {   // kv head 0's workgroups write the selection; one thread advances the epoch
+        if (kvh == 0 && a.sel_out)
+            for (int p = j0 + tid; p < j1; p += 256)
+                a.sel_out[p] = p < a.sel_topk ? srows[p - j0] : (uint32_t)(a.sel_n + p - a.sel_topk);
+        if (c == 0 && kvh == 0 && tid == 0) *a.sel_epoch += 1;   // the next call's histogram buffer
+    }
     if (a.C == 1) {
 #pragma unroll
         for (int e = 0; e < PER; e++) a.o[(size_t)hq * HD + od + e] = f2a<BF>(acc[e] / L);
@@ -179,11 +206,21 @@ __global__ __launch_bounds__(256) void sparse_decode_kernel(SparseArgs a) {
 int launch_sparse_decode(const SparseArgs& a, hipStream_t st) {
     const dim3 grid(a.C, a.n_kv), block(256);
     const int gq = a.n_q / a.n_kv;
-    if (gq == 4 && !a.bf16) hipLaunchKernelGGL((sparse_decode_kernel<4, false>), grid, block, 0, st, a);
-    else if (gq == 4 && a.bf16) hipLaunchKernelGGL((sparse_decode_kernel<4, true>), grid, block, 0, st, a);
-    else if (gq == 8 && a.bf16) hipLaunchKernelGGL((sparse_decode_kernel<8, true>), grid, block, 0, st, a);
-    else if (gq == 8 && !a.bf16) hipLaunchKernelGGL((sparse_decode_kernel<8, false>), grid, block, 0, st, a);
+    const bool fs = a.sel_ws != nullptr;
+    if (fs && (a.CH > SPD_FS_MAXCH || !a.sel_epoch || a.sel_topk <= 0 || a.sel_n <= a.sel_topk ||
+               a.sel_n > SEL_MAXN || a.nsel < a.sel_topk))
+        return EMBLA_ERR_INVALID;
+#define EMBLA_SPD(G, B)                                                                         \
+    do {                                                                                        \
+        if (fs) hipLaunchKernelGGL((sparse_decode_kernel<G, B, true>), grid, block, 0, st, a);  \
+        else hipLaunchKernelGGL((sparse_decode_kernel<G, B, false>), grid, block, 0, st, a);    \
+    } while (0)
+    if (gq == 4 && !a.bf16) EMBLA_SPD(4, false);
+    else if (gq == 4 && a.bf16) EMBLA_SPD(4, true);
+    else if (gq == 8 && a.bf16) EMBLA_SPD(8, true);
+    else if (gq == 8 && !a.bf16) EMBLA_SPD(8, false);
     else return EMBLA_ERR_UNSUPPORTED;
+#undef EMBLA_SPD
     if (a.C > 1) return launch_decode_merge(a.part, a.o, a.C, a.n_q, false, a.bf16, 1.0f, st);
     return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
 }

@@ -77,6 +77,14 @@ struct SparseArgs {
     uint16_t* o;
     int CH, C, max_s, n_q, n_kv;
     bool bf16;
+    // Non-null sel_ws: rows 0 .. sel_topk - 1 are the wide select's output, its last step run by
+    // each workgroup for the ranks it attends (idx unused, CH <= 256), and rows sel_topk .. nsel - 1
+    // are keys sel_n .. (the recent ones). sel_out (optional) receives the selection in
+    // select_keys' order; the select's epoch word is advanced once.
+    const uint32_t* sel_ws = nullptr;
+    int sel_n = 0, sel_topk = 0;
+    uint32_t* sel_out = nullptr;
+    uint32_t* sel_epoch = nullptr;
 };
 int launch_sparse_decode(const SparseArgs& a, hipStream_t st);
 
@@ -163,8 +171,10 @@ int launch_index_scores(const uint16_t* qi, const float* w, const uint16_t* ki, 
 #define WSEL_NCP 16   // histogram copies of the wide select (C4 step: 8 -> 32.1 us, 16 -> 29.5, 32 -> 29.6, 64 -> 31.4)
 #endif
 constexpr size_t kWideSelectWords = 2 * WSEL_NCP * (256 + 4096) + 64 + 32768 / 1024 + 32768 / 32 + 2 * 32768;
+constexpr size_t kWideSelectEpoch = 2 * WSEL_NCP * (256 + 4096) + 3;   // the epoch word's index
 /// Index scores of keys [0, S - recent), then their exact top-k + recent into idx, on many
-/// workgroups (one set). sw: kWideSelectWords words, zero before the first call.
+/// workgroups (one set). sw: kWideSelectWords words, zero before the first call. idx null: the
+/// last step is left to the consumer (SparseArgs::sel_ws), which also advances the epoch.
 int launch_wide_select(const uint16_t* qi, const float* w, const uint16_t* ki, float* scores, int S, int n_ih,
                        int topk, int recent, uint32_t* sw, uint32_t* idx, hipStream_t st);
 

@@ -16,23 +16,18 @@
 // r = max(dot, 0), s = fma(w_h, r * r, s) over h = 0 .. from s = 0. oracle/oracle.c restates it.
 #include "common.hpp"
 #include "embla_internal.hpp"
+#include "wsel.hpp"
 
 #pragma clang fp contract(off)
 
 namespace embla {
 
 constexpr int SEL_T = 1024;                 // threads of the select workgroup (16 waves)
-constexpr int SEL_MAXN = 32768;             // candidates: their order bits stay in LDS
 constexpr int HBINS = 2048;                 // 11-bit radix digits: bits 31..21, 20..10, 9..0
 constexpr int HCOPIES = 2;                  // copies of the first pass's histogram
 constexpr int HSTRIDE = HBINS + 1;          // words a copy (offset by one word: other banks)
 constexpr int LCAP = 2048;                  // bucket list capacity (else passes 2-3 read every key)
 constexpr int SEL_OUTCAP = HCOPIES * HSTRIDE + LCAP;   // topk indices staged in hist + list
-constexpr int DB = 4096;                    // the wide select's 12-bit digits: bits 31..20, 19..8
-constexpr int CB = 256;                     // its coarse first digit: bits 31..24
-constexpr int NCP = WSEL_NCP;               // histogram copies (scorer workgroup % NCP)
-constexpr int HCOPY = CB + DB;              // words a copy: coarse bins, then fine bins
-constexpr int HWORDS = NCP * HCOPY;         // words a histogram buffer (two, by call parity)
 
 __device__ __forceinline__ uint32_t order_bits(float f) {
     const uint32_t u = __float_as_uint(f);
@@ -290,58 +285,6 @@ int launch_select_topk(const float* scores, int score_stride, uint32_t* idx, int
 }
 
 // ------------------------------------------------------------------ wide select (one set)
-/// Digit (of 4096) holding the k-th largest of h: sel = {digit, keys in digits above}. Wave 0:
-/// each lane sums 64 digits from the top; the lane whose digits hold the k-th is found by a scan
-/// and a ballot, then its 64 digits go one a lane through a second scan.
-__device__ __forceinline__ void pick4096(const uint32_t* h, uint32_t k, uint32_t* sel) {
-    const int lane = threadIdx.x & 63;
-    const int b0 = DB - 64 - 64 * lane;   // the lane's digits b0 .. b0 + 63
-    uint32_t s = 0;
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const u4_t x = *(const u4_t*)(h + b0 + 4 * i);
-        s += (x[0] + x[1]) + (x[2] + x[3]);
-    }
-    uint32_t above = s;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t x = __shfl_up(above, o, 64);
-        if (lane >= o) above += x;
-    }
-    above -= s;
-    const int L = max(__ffsll((long long)__ballot(above < k && above + s >= k)) - 1, 0);   // 0 if none
-    const uint32_t base = __shfl(above, L, 64);
-    const int d = DB - 1 - 64 * L - lane;
-    const uint32_t c = h[d];
-    uint32_t incl = c;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t y = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += y;
-    }
-    if (base + incl - c < k && base + incl >= k) { sel[0] = (uint32_t)d; sel[1] = base + incl - c; }
-}
-
-/// Digit (of 256) holding the k-th largest: wave 0, 4 digits a lane from the top.
-__device__ __forceinline__ void pick256(const uint32_t* h, uint32_t k, uint32_t* sel) {
-    const int lane = threadIdx.x & 63;
-    uint32_t cc[4], s = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) { cc[i] = h[255 - 4 * lane - i]; s += cc[i]; }
-    uint32_t above = s;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t x = __shfl_up(above, o, 64);
-        if (lane >= o) above += x;
-    }
-    above -= s;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        if (above < k && above + cc[i] >= k) { sel[0] = 255u - (4 * lane + i); sel[1] = above; }
-        above += cc[i];
-    }
-}
-
 /// The wide select's second step, a 256-thread workgroup a 1024 keys. Every workgroup finds the
 /// 12-bit first digit d1 holding the topk-th largest from the scorer's histograms: the coarse
 /// digit from the 256 coarse bins (summed over the copies), then d1 among that digit's 16 fine
@@ -420,135 +363,15 @@ __global__ __launch_bounds__(256) void wsel_classify_kernel(const float* __restr
     if (tid == 0) cnts[blockIdx.x] = lcnt;
 }
 
-/// Exclusive prefix sum over a 1024-thread workgroup, and the total.
-__device__ __forceinline__ uint32_t wsel_scan(uint32_t v, uint32_t* wsum, uint32_t& total) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    uint32_t incl = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t x = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += x;
-    }
-    if (lane == 63) wsum[w] = incl;
-    __syncthreads();
-    uint32_t before = 0;
-    total = 0;
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const uint32_t x = wsum[i];
-        before += i < w ? x : 0u;
-        total += x;
-    }
-    __syncthreads();   // wsum is reused by the next scan
-    return before + incl - v;
-}
-
-/// The wide select's last step, one 1024-thread workgroup: the second (bits 19..8) and third
-/// (7..0) radix levels over the candidate list give the topk-th largest value E and how many
-/// keys equal to it are taken; candidates above E join the bitmap, those equal to E form the tie
-/// bitmap; block scans of the bitmaps' popcounts give the output in select_keys' order. It then
-/// advances the epoch (the next call's histogram buffer). Counts are clamped and every write is
-/// bounded, so a workspace that was not zeroed gives a wrong selection, never a stray access.
+/// The wide select's last step over the whole output (one 1024-thread workgroup), then the
+/// recent keys, and the epoch advanced (the next call's histogram buffer): wsel_slice over every
+/// rank. The sparse-layer decode runs the same step inside its own workgroups instead.
 __global__ __launch_bounds__(1024) void wsel_final_kernel(int n, int topk, int recent, uint32_t* __restrict__ sw,
                                                           uint32_t* __restrict__ out) {
-    __shared__ __attribute__((aligned(16))) uint32_t h2[DB];
-    __shared__ uint32_t gts[SEL_MAXN / 32], eqs[SEL_MAXN / 32], wsum[16], sel[2];
-    const int tid = threadIdx.x, w = tid >> 6;
-    __shared__ uint32_t coff[SEL_MAXN / 1024 + 1];
-    __shared__ __attribute__((aligned(16))) uint32_t cl[2 * SEL_MAXN / 4];   // candidates, when they fit (else in place)
-    uint32_t* meta = sw + 2 * HWORDS;
-    const uint32_t* cnts = meta + 64;
-    const uint32_t* gt = cnts + SEL_MAXN / 1024;
-    const uint32_t* creg = gt + SEL_MAXN / 32;
-    const uint32_t d1 = meta[1] & (DB - 1);
-    uint32_t k = (uint32_t)topk - min(meta[2], (uint32_t)topk - 1);
-    const int nw = (n + 31) / 32, nb = (n + 1023) / 1024;
-    for (int q = tid; q < DB; q += 1024) h2[q] = 0;
-    gts[tid] = tid < nw ? gt[tid] : 0u;
-    eqs[tid] = 0;
-    if (w == 0) {   // offsets of the workgroups' candidate regions in the list (nb <= 32)
-        const int lane = tid & 63;
-        const uint32_t c = lane < nb ? min(cnts[lane], 1024u) : 0u;
-        uint32_t incl = c;
-#pragma unroll
-        for (int o = 1; o < 32; o <<= 1) {
-            const uint32_t x = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += x;
-        }
-        if (lane < nb) coff[lane] = incl - c;
-        if (lane == nb - 1) coff[nb] = incl;
-    }
-    __syncthreads();
-    const uint32_t cnt = coff[nb];
-    const bool inl = cnt <= SEL_MAXN / 4;
-    // the list: candidate q of region b at creg[2 (1024 b + q - coff[b])]
-    auto cand_at = [&](uint32_t q, uint32_t& key, uint32_t& j) {
-        int b = 0;
-        while (b + 1 < nb && coff[b + 1] <= q) b++;
-        const uint32_t* c2 = creg + 2 * (1024 * b + (q - coff[b]));
-        key = c2[0];
-        j = c2[1];
-    };
-    if (inl) {   // wave w copies regions w, w + 16: no search
-        for (int b = w; b < nb; b += 16) {
-            const uint32_t nc = coff[b + 1] - coff[b];
-            for (uint32_t q = tid & 63; q < nc; q += 64) {
-                const u2_t v = *(const u2_t*)(creg + 2 * (1024 * b + q));
-                *(u2_t*)(cl + 2 * (coff[b] + q)) = v;
-            }
-        }
-        __syncthreads();
-    }
-    auto cand = [&](uint32_t q, uint32_t& key, uint32_t& j) {
-        if (inl) { key = cl[2 * q]; j = cl[2 * q + 1]; }
-        else cand_at(q, key, j);
-    };
-    for (uint32_t q = tid; q < cnt; q += 1024) {
-        uint32_t key, j;
-        cand(q, key, j);
-        atomicAdd(&h2[(key >> 8) & 0xFFF], 1u);
-    }
-    if (tid == 0) { sel[0] = 0; sel[1] = 0; }
-    __syncthreads();
-    if (w == 0) pick4096(h2, k, sel);
-    __syncthreads();
-    const uint32_t p2 = (d1 << 12) | (sel[0] & (DB - 1));
-    k -= sel[1];
-    __syncthreads();
-    if (tid < 256) h2[tid] = 0;
-    __syncthreads();
-    for (uint32_t q = tid; q < cnt; q += 1024) {
-        uint32_t key, j;
-        cand(q, key, j);
-        if ((key >> 8) == p2) atomicAdd(&h2[key & 255], 1u);
-    }
-    if (tid == 0) { sel[0] = 0; sel[1] = 0; }
-    __syncthreads();
-    if (w == 0) pick256(h2, k, sel);
-    __syncthreads();
-    const uint32_t E = (p2 << 8) | (sel[0] & 255);
-    k -= sel[1];   // keys equal to E to take (>= 1)
-    for (uint32_t q = tid; q < cnt; q += 1024) {
-        uint32_t key, j;
-        cand(q, key, j);
-        j &= SEL_MAXN - 1;
-        if (key > E) atomicOr(&gts[j >> 5], 1u << (j & 31));
-        else if (key == E) atomicOr(&eqs[j >> 5], 1u << (j & 31));
-    }
-    __syncthreads();
-    uint32_t ngt, neq;
-    {
-        uint32_t g = gts[tid];
-        uint32_t p = wsel_scan(__popc(g), wsum, ngt);
-        for (; g && p < (uint32_t)topk; g &= g - 1) out[p++] = 32u * tid + __ffs(g) - 1;
-    }
-    {
-        uint32_t e = eqs[tid];
-        uint32_t p = wsel_scan(__popc(e), wsum, neq);
-        for (; e && p < k && ngt + p < (uint32_t)topk; e &= e - 1) out[ngt + p++] = 32u * tid + __ffs(e) - 1;
-    }
-    for (int j = tid; j < recent; j += 1024) out[topk + j] = (uint32_t)(n + j);
-    if (tid == 0) meta[3] += 1;   // the next call uses the other histogram buffer
+    __shared__ __attribute__((aligned(16))) uint32_t L[WSL_FIXED + 2 * SEL_MAXN / 4];
+    wsel_slice<1024>(n, topk, sw, L, WSL_FIXED + 2 * SEL_MAXN / 4, 0, (uint32_t)topk, nullptr, out);
+    for (int j = threadIdx.x; j < recent; j += 1024) out[topk + j] = (uint32_t)(n + j);
+    if (threadIdx.x == 0) sw[2 * HWORDS + 3] += 1;
 }
 
 int launch_wide_select(const uint16_t* qi, const float* w, const uint16_t* ki, float* scores, int S, int n_ih,
@@ -558,7 +381,7 @@ int launch_wide_select(const uint16_t* qi, const float* w, const uint16_t* ki, f
     int rc = launch_index_scores(qi, w, ki, scores, n, n_ih, st, sw);
     if (rc) return rc;
     hipLaunchKernelGGL(wsel_classify_kernel, dim3((n + 1023) / 1024), dim3(256), 0, st, scores, n, topk, sw);
-    hipLaunchKernelGGL(wsel_final_kernel, dim3(1), dim3(1024), 0, st, n, topk, recent, sw, idx);
+    if (idx) hipLaunchKernelGGL(wsel_final_kernel, dim3(1), dim3(1024), 0, st, n, topk, recent, sw, idx);
     return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
 }
 
