@@ -256,6 +256,38 @@ __device__ __forceinline__ void wsel_slice_block(int n, int topk, const uint32_t
 constexpr int WSL_WSPEC = 32;    // candidates a region the fast path reads (its limit a region)
 constexpr int WSL_WMAX = 256;    // candidates the fast path ranks (one a thread)
 
+/// Digit (of 1024) holding the k-th largest of h: sel = {digit, keys in digits above}. Wave 0:
+/// each lane sums 16 digits from the top; the lane whose digits hold the k-th is found by a scan
+/// and a ballot, then its 16 digits go one a lane through a second scan.
+__device__ __forceinline__ void pick1024(const uint32_t* h, uint32_t k, uint32_t* sel) {
+    const int lane = threadIdx.x & 63;
+    const int b0 = 1024 - 16 - 16 * lane;   // the lane's digits b0 .. b0 + 15
+    uint32_t s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const u4_t x = *(const u4_t*)(h + b0 + 4 * i);
+        s += (x[0] + x[1]) + (x[2] + x[3]);
+    }
+    uint32_t above = s;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t x = __shfl_up(above, o, 64);
+        if (lane >= o) above += x;
+    }
+    above -= s;
+    const int L = max(__ffsll((long long)__ballot(above < k && above + s >= k)) - 1, 0);   // 0 if none
+    const uint32_t base = __shfl(above, L, 64);
+    const int d = 1023 - 16 * L - (lane & 15);
+    const uint32_t c = lane < 16 ? h[d] : 0u;
+    uint32_t incl = c;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+        const uint32_t y = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += y;
+    }
+    if (lane < 16 && base + incl - c < k && base + incl >= k) { sel[0] = (uint32_t)d; sel[1] = base + incl - c; }
+}
+
 /// The n-th (from 0) set bit of x (n < popcount(x)), by halving.
 __device__ __forceinline__ uint32_t nth_set_bit(uint32_t x, uint32_t n) {
     uint32_t pos = 0;
@@ -277,9 +309,10 @@ __device__ __forceinline__ uint32_t nth_set_bit(uint32_t x, uint32_t n) {
 ///  - wave 0 requests, in one memory round, the bitmap of keys above the first digit (16 words a
 ///    lane), the candidate counts and the first WSL_WSPEC candidates of every region (16 a
 ///    lane), and compacts the candidates into LDS;
-///  - thread t ranks candidate t against all the others (broadcast LDS reads, four keys a read):
-///    it is above the topk-th value E iff fewer than k candidates are not below it, equal to E iff
-///    fewer than k are above it; it marks itself in the bitmap or in the tie bitmap;
+///  - the topk-th value E comes from two 10-bit digits of the candidates' low 20 bits (they share
+///    the first 12): a candidate a thread adds itself to an LDS histogram, wave 0 picks the digit
+///    holding the k-th; then every candidate marks itself in the bitmap (above E) or in the tie
+///    bitmap (equal to E);
 ///  - wave 0 scans the bitmaps' popcounts into per-word prefixes, and lane i finds rank r0 + i by
 ///    a binary search over them and a halving search in the word.
 /// A region with more than WSL_WSPEC candidates, more than WSL_WMAX in all, or a slice of more
@@ -289,11 +322,11 @@ __device__ __forceinline__ void wsel_slice(int n, int topk, const uint32_t* __re
                                            uint32_t r0, uint32_t nr, uint32_t* rows, uint32_t* __restrict__ out) {
     constexpr int NW = SEL_MAXN / 32, NR = SEL_MAXN / 1024;
     static_assert(NW == 16 * 64 && NR == 32 && 2 * WSL_WSPEC == 64 && BT >= WSL_WMAX, "the fast path's shape");
-    __shared__ uint32_t wsl_ok, wsl_tot, wsl_k, wsl_kt;
+    __shared__ uint32_t wsl_ok, wsl_tot, wsl_k, wsl_kt, wsl_sel[2];
     uint32_t* gts = L;                          // NW: keys above E
     uint32_t* eqs = L + NW;                     // NW: keys equal to E
-    uint32_t* pg = L + 2 * NW;                  // NW: keys above E before word w
-    uint32_t* pe = L + 3 * NW;                  // NW: keys equal to E before word w
+    uint32_t* pg = L + 2 * NW;                  // NW: keys above E before word w (first: a histogram)
+    uint32_t* pe = L + 3 * NW;                  // NW: keys equal to E before word w (first: a histogram)
     uint32_t* cj = L + 4 * NW;                  // WSL_WMAX candidate indices
     uint32_t* ck = cj + WSL_WMAX;               // WSL_WMAX + 16 candidate keys (16-byte aligned)
     const int tid = threadIdx.x, lane = tid & 63;
@@ -330,7 +363,7 @@ __device__ __forceinline__ void wsel_slice(int n, int topk, const uint32_t* __re
                     ck[off + i] = cv[i >> 1][2 * (i & 1)];
                     cj[off + i] = cv[i >> 1][2 * (i & 1) + 1] & (SEL_MAXN - 1);
                 }
-            if (lane < 16) ck[tot + lane] = 0;   // padding, never counted
+            if (lane < 16) ck[tot + lane] = 0;   // zero keys up to a multiple of 4 (and beyond)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 u4_t v = gw[i];
@@ -347,41 +380,33 @@ __device__ __forceinline__ void wsel_slice(int n, int topk, const uint32_t* __re
             wsl_kt = 0;
         }
     }
+    else   // the other waves clear the two digit histograms meanwhile
+        for (int q = tid - 64; q < 2 * NW / 4; q += BT - 64) *(u4_t*)(pg + 4 * q) = (u4_t){0, 0, 0, 0};
     __syncthreads();
     if (!wsl_ok) {   // uniform
         wsel_slice_block<BT>(n, topk, sw, L, lwords, r0, nr, rows, out);
         return;
     }
     const uint32_t tot = wsl_tot, k = wsl_k;
+    // E by two 10-bit digits of the low 20 bits (the candidates share the first 12): histograms,
+    // picks by wave 0; then each candidate marks itself above E or equal to it
+    const uint32_t key = tid < (int)tot ? ck[tid] : 0u;
+    if (tid < (int)tot) atomicAdd(&pg[(key >> 10) & 1023], 1u);
+    __syncthreads();
+    if (tid < 64) pick1024(pg, k, wsl_sel);
+    __syncthreads();
+    const uint32_t da = wsl_sel[0] & 1023, ka = k - wsl_sel[1];
+    if (tid < (int)tot && ((key >> 10) & 1023) == da) atomicAdd(&pe[key & 1023], 1u);
+    __syncthreads();
+    if (tid < 64) pick1024(pe, ka, wsl_sel);
+    __syncthreads();
+    const uint32_t E = ((meta[1] & (DB - 1)) << 20) | (da << 10) | (wsl_sel[0] & 1023);
     if (tid < (int)tot) {
-        const uint32_t key = ck[tid];
-        uint32_t ab[4] = {0, 0, 0, 0}, nb4[4] = {0, 0, 0, 0};
-        const uint32_t full = tot & ~15u;
-        for (uint32_t q = 0; q < full; q += 16) {
-            u4_t v[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) v[i] = *(const u4_t*)(ck + q + 4 * i);
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int x = 0; x < 4; x++) {
-                    ab[x] += v[i][x] > key;
-                    nb4[x] += v[i][x] >= key;
-                }
-        }
-        for (uint32_t q = full; q < tot; q++) {
-            const uint32_t x = ck[q];
-            ab[0] += x > key;
-            nb4[0] += x >= key;
-        }
-        const uint32_t above = (ab[0] + ab[1]) + (ab[2] + ab[3]), notbelow = (nb4[0] + nb4[1]) + (nb4[2] + nb4[3]);
         const uint32_t j = cj[tid];
-        if (notbelow < k) atomicOr(&gts[j >> 5], 1u << (j & 31));
-        else if (above < k) {
-            atomicOr(&eqs[j >> 5], 1u << (j & 31));
-            wsl_kt = k - above;   // the ties to take: the same for every tie
-        }
+        if (key > E) atomicOr(&gts[j >> 5], 1u << (j & 31));
+        else if (key == E) atomicOr(&eqs[j >> 5], 1u << (j & 31));
     }
+    if (tid == 0) wsl_kt = ka - wsl_sel[1];   // the ties to take
     __syncthreads();
     if (tid < 64) {
         uint32_t g[16], e[16], cg = 0, ce = 0;
