@@ -45,7 +45,7 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(GemvArgs a) {
         for (int sp = 0; sp < MAXS; sp++)
             if (sp < spans) {
                 const size_t r = (size_t)(r0 + u);
-                wd[u][sp] = ld16(W + sg.w + (r * wpr + 256 * sp + 4 * lane) * 4);
+                wd[u][sp] = ld16_stream(W + sg.w + (r * wpr + 256 * sp + 4 * lane) * 4);   // read once
                 sc[u][sp] = bf2f(*(const uint16_t*)(W + sg.s + (r * gpr + 32 * sp + lane / 2) * 2));
                 bi[u][sp] = bf2f(*(const uint16_t*)(W + sg.b + (r * gpr + 32 * sp + lane / 2) * 2));
             }
@@ -132,7 +132,9 @@ int launch_gemv_q4_rw(const GemvArgs& a, int epi, hipStream_t st) {
 }
 
 // One row a wave: 3072 q/k/v rows are 768 workgroups, enough requests in flight to cover every
-// CU (48-layer q/k/v + o: 4 rows a wave 11.1 us a layer, 2 rows 9.1 us, 1 row 8.4 us).
+// CU (48-layer q/k/v + o: 4 rows a wave 11.1 us a layer, 2 rows 9.1 us, 1 row 8.4 us; 2-wave
+// workgroups 9.1 us, x read by every wave from L2 instead of once into LDS 8.59 against 8.56 us;
+// the weights' nontemporal loads 8.44-8.45 against 8.55-8.56 us).
 int launch_gemv_q4(const GemvArgs& a, int epi, hipStream_t st) { return launch_gemv_q4_rw<1>(a, epi, st); }
 
 }  // namespace embla
