@@ -138,6 +138,31 @@ def test_sparse_layer_selection_ties(torch_gpu, orc, c4):
     np.testing.assert_array_equal(got, ref)
 
 
+def test_sparse_layer_selection_many_candidates(torch_gpu, orc, c4):
+    """600 copies of one index key whose score ranks ~900th: the topk-th value is a tie among
+    them, so the first digit's candidates (> 256, > 32 in one classify region) take the
+    workgroup-wide ranking path of the attention's select."""
+    from embla_attn import ops
+    torch = torch_gpu
+    S = 32768
+    ki = c4["ki"].copy()
+    sc = orc.index_scores(c4["qi"], c4["w"], ki[:S - 128])
+    x = int(np.argsort(-sc.astype(np.float64), kind="stable")[900])
+    ki[:600] = ki[x]
+    ws = ops.SparseWorkspace(32768, 16)
+    say("sparse layer selection many candidates")
+    o = ops.sparse_layer_decode(dev(c4["q"], torch.float16), dev(c4["qi"], torch.float16), dev(c4["w"]),
+                                dev(ki, torch.float16), dev(c4["K"], torch.float16), dev(c4["V"], torch.float16),
+                                S, 32768, 4, ws)
+    got = ws.selection().cpu().numpy().astype(np.uint32)
+    sc = orc.index_scores(c4["qi"], c4["w"], ki[:S - 128])
+    ref = orc.select_keys(np.concatenate([sc, np.zeros(128, np.float32)]), S)
+    np.testing.assert_array_equal(got, ref)
+    assert len(np.nonzero(ref[:1024] < 600)[0]) > 0   # some of the copies are taken
+    out = orc.decode_rows(synth.f16_val(c4["q"]), synth.f16_val(c4["K"]), synth.f16_val(c4["V"]), ref.astype(np.int32))
+    assert_close(f16_host(o), out, what="many candidates")
+
+
 def test_select_topk_many_sets_unaligned(torch_gpu, orc):
     """Several sets at an odd stride (rows not 16-byte aligned), ragged n, a small topk."""
     from embla_attn import ops
