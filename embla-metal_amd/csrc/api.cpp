@@ -561,7 +561,7 @@ int embla_sparse_layer_decode(const void* q, const void* qi, const float* w, con
     // (its last step runs inside the attention's workgroups, each ranking the rows it attends;
     // the selection still lands in idx)
     const int rc = launch_wide_select((const uint16_t*)qi, w, (const uint16_t*)ki, scores, S, n_ih, kTopK, kRecent,
-                                      sel_ws, nullptr, stream);
+                                      sel_ws, stream);
     if (rc) return rc;
     SparseArgs fs;
     fs.sel_ws = sel_ws; fs.sel_n = S - kRecent; fs.sel_topk = kTopK; fs.sel_out = idx;

@@ -172,11 +172,13 @@ int launch_index_scores(const uint16_t* qi, const float* w, const uint16_t* ki, 
 #endif
 constexpr size_t kWideSelectWords = 2 * WSEL_NCP * (256 + 4096) + 64 + 32768 / 1024 + 32768 / 32 + 2 * 32768;
 constexpr size_t kWideSelectEpoch = 2 * WSEL_NCP * (256 + 4096) + 3;   // the epoch word's index
-/// Index scores of keys [0, S - recent), then their exact top-k + recent into idx, on many
-/// workgroups (one set). sw: kWideSelectWords words, zero before the first call. idx null: the
-/// last step is left to the consumer (SparseArgs::sel_ws), which also advances the epoch.
+/// Index scores of keys [0, S - recent) and the first steps of their exact top-k on many
+/// workgroups (one set): the scores' histogram, then the first digit of the topk-th value, the
+/// bitmap of keys above it and the candidates in it. The last step is the consumer's
+/// (SparseArgs::sel_ws, wsel_slice), which also advances the epoch. sw: kWideSelectWords words,
+/// zero before the first call.
 int launch_wide_select(const uint16_t* qi, const float* w, const uint16_t* ki, float* scores, int S, int n_ih,
-                       int topk, int recent, uint32_t* sw, uint32_t* idx, hipStream_t st);
+                       int topk, int recent, uint32_t* sw, hipStream_t st);
 
 struct KVQuantArgs {
     const uint16_t* k;   // [T] rows of k, row stride `stride` elements, kv head h at h * 128

@@ -363,25 +363,13 @@ __global__ __launch_bounds__(256) void wsel_classify_kernel(const float* __restr
     if (tid == 0) cnts[blockIdx.x] = lcnt;
 }
 
-/// The wide select's last step over the whole output (one 1024-thread workgroup), then the
-/// recent keys, and the epoch advanced (the next call's histogram buffer): wsel_slice over every
-/// rank. The sparse-layer decode runs the same step inside its own workgroups instead.
-__global__ __launch_bounds__(1024) void wsel_final_kernel(int n, int topk, int recent, uint32_t* __restrict__ sw,
-                                                          uint32_t* __restrict__ out) {
-    __shared__ __attribute__((aligned(16))) uint32_t L[WSL_FIXED + 2 * SEL_MAXN / 4];
-    wsel_slice<1024>(n, topk, sw, L, WSL_FIXED + 2 * SEL_MAXN / 4, 0, (uint32_t)topk, nullptr, out);
-    for (int j = threadIdx.x; j < recent; j += 1024) out[topk + j] = (uint32_t)(n + j);
-    if (threadIdx.x == 0) sw[2 * HWORDS + 3] += 1;
-}
-
 int launch_wide_select(const uint16_t* qi, const float* w, const uint16_t* ki, float* scores, int S, int n_ih,
-                       int topk, int recent, uint32_t* sw, uint32_t* idx, hipStream_t st) {
+                       int topk, int recent, uint32_t* sw, hipStream_t st) {
     const int n = S - recent;
     if (n > SEL_MAXN || n <= topk) return EMBLA_ERR_UNSUPPORTED;
     int rc = launch_index_scores(qi, w, ki, scores, n, n_ih, st, sw);
     if (rc) return rc;
     hipLaunchKernelGGL(wsel_classify_kernel, dim3((n + 1023) / 1024), dim3(256), 0, st, scores, n, topk, sw);
-    if (idx) hipLaunchKernelGGL(wsel_final_kernel, dim3(1), dim3(1024), 0, st, n, topk, recent, sw, idx);
     return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
 }
 
