@@ -447,7 +447,7 @@ int embla_sliding_decode(const void* q, const void* k_new, const void* v_new, vo
     if (chunk < 0 || chunk % 32) return EMBLA_ERR_INVALID;
     const int lo = pos - window + 1 > 0 ? pos - window + 1 : 0;
     const int span = pos - (lo & ~31);   // ring keys from the first tile on (the current key is extra)
-    const int ch = chunk ? chunk : env_int("EMBLA_SLIDING_CH", 192);   // C2 step: 8.61 us at 192, 8.74 at 256, 8.82 at 160, 9.48 at 224
+    const int ch = chunk ? chunk : env_int("EMBLA_SLIDING_CH", 192);   // C2 step: 8.61 us at 192, 8.74 at 256, 8.67-8.82 at 160, 9.48 at 224, 8.77 at 96
     int C = (span + ch - 1) / ch;
     if (C < 1) C = 1;
     if (C > kMaxChunks) return EMBLA_ERR_INVALID;
