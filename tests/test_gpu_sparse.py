@@ -102,6 +102,28 @@ def test_sparse_layer_end_to_end(torch_gpu, orc, c4, S):
     assert_close(f16_host(o), ref, what=f"S={S}")
 
 
+def test_sparse_layer_gq8_bf16(torch_gpu, orc, c4):
+    """16 query heads over 2 kv heads (GQ = 8) and bf16 activations and caches: the attention's
+    own select in its GQ = 8, bf16 instance."""
+    from embla_attn import ops
+    torch = torch_gpu
+    S = 30001
+    say("sparse layer GQ 8 bf16")
+    K = synth.bf16_bits(synth.f16_val(c4["K"][:2]))
+    V = synth.bf16_bits(synth.f16_val(c4["V"][:2]))
+    q = synth.bf16_bits(synth.f16_val(c4["q"]))
+    ws = ops.SparseWorkspace(32768, 16)
+    o = ops.sparse_layer_decode(dev(q.view(np.int16), torch.bfloat16), dev(c4["qi"], torch.float16), dev(c4["w"]),
+                                dev(c4["ki"], torch.float16), dev(K.view(np.int16), torch.bfloat16),
+                                dev(V.view(np.int16), torch.bfloat16), S, 32768, 2, ws, dtype=ops.BF16)
+    got = ws.selection().cpu().numpy().astype(np.uint32)
+    sc = orc.index_scores(c4["qi"], c4["w"], c4["ki"][:S - 128])
+    sel = orc.select_keys(np.concatenate([sc, np.zeros(128, np.float32)]), S)
+    np.testing.assert_array_equal(got, sel)
+    ref = orc.decode_rows(synth.bf16_val(q), synth.bf16_val(K), synth.bf16_val(V), sel.astype(np.int32))
+    assert_close(o.float().cpu().numpy(), ref, what="GQ 8 bf16")
+
+
 def test_sparse_layer_selection_bit_exact(torch_gpu, orc, c4):
     """The layer's selection (scorer histogram, wide classify, final select on the candidates) is
     select_keys' output bit for bit, over consecutive calls of one workspace at different S (each
