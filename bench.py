@@ -580,7 +580,9 @@ def profile_case(torch, name, calls=5):
     """Only dispatches one workload's calls, eagerly, for rocprofv3 --pmc runs (the last dispatch
     is read): 'c5_full' = C5's full-layer attention (embla_prefill_int8, 2048 rows after 30720
     int8 positions); 'gemm_prefill' = the q/k/v projection GEMM of C5's chunk (T 2048, O 3072,
-    K 2048). Prints nothing."""
+    K 2048); 'c5_sparse' = C5's sparse layer (embla_prefill_sparse: indexer, band select,
+    gathered attention); 'c4' = C4 sparse-layer decode steps at context 32768 (scorer, classify,
+    the attention with the select's last step, merge). Prints nothing."""
     from embla_attn import ops
     g = torch.Generator(device="cuda")
     g.manual_seed(4)
@@ -607,6 +609,37 @@ def profile_case(torch, name, calls=5):
         y = torch.empty(T, O, dtype=torch.bfloat16, device="cuda")
         for _ in range(calls):
             ops.gemm_q4(W, (0, wb, wb + sb), x, y, T, O, K, ops.EPI_BF16)
+    elif name == "c5_sparse":
+        p0, T, n_kv = 30720, 2048, 4
+        max_s = p0 + T
+        nrow = n_kv * max_s * 128
+        kr = torch.empty(nrow + n_kv * max_s * 2, dtype=torch.uint8, device="cuda")
+        vr = torch.empty_like(kr)
+        for t in (kr, vr):
+            t[:nrow].random_(0, 256, generator=g)
+            t[nrow:].view(torch.float16).uniform_(0.005, 0.02, generator=g)
+        q = torch.randn(T, 16, 128, generator=g, device="cuda").bfloat16()
+        kn = torch.randn(T, n_kv, 128, generator=g, device="cuda").bfloat16()
+        vn = torch.randn(T, n_kv, 128, generator=g, device="cuda").bfloat16()
+        qi = torch.randn(T, 4, 64, generator=g, device="cuda").half()
+        wi = torch.rand(T, 4, generator=g, device="cuda")
+        ki = torch.randn(p0 + T, 64, generator=g, device="cuda").half()
+        out = torch.empty(T, 16, 128, dtype=torch.bfloat16, device="cuda")
+        sws = ops.SparsePrefillWorkspace(T, p0)
+        for _ in range(calls):
+            ops.prefill_sparse(q, kn, vn, qi, wi, ki, kr, vr, T, p0, max_s, n_kv, sws, out=out)
+    elif name == "c4":
+        from embla_attn import synth
+        c = synth.sparse_case(seed=3, ctx=32768)
+        dev = lambda a, dt=None: (torch.from_numpy(a).cuda().view(dt) if dt is not None else torch.from_numpy(a).cuda())
+        q, qi, w, ki = dev(c["q"], torch.float16), dev(c["qi"], torch.float16), dev(c["w"]), dev(c["ki"], torch.float16)
+        K, V = dev(c["K"], torch.float16), dev(c["V"], torch.float16)
+        ws = ops.SparseWorkspace(32768, 16)
+        out = torch.empty(16, 128, dtype=torch.float16, device="cuda")
+        kis = [ki] + [torch.roll(ki, 2048 * l, 0).contiguous() for l in range(1, 16)]
+        for _ in range(calls):
+            for l in range(16):
+                ops.sparse_layer_decode(q, qi, w, kis[l], K, V, 32768, 32768, 4, ws, out=out)
     else:
         raise SystemExit(f"unknown profile case {name}")
     torch.cuda.synchronize()
@@ -624,7 +657,7 @@ def main():
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only dispatch C3 decode layers and a 64 MB copy (each after a cache-evicting "
                          "fill) for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs; prints nothing else")
-    ap.add_argument("--profile-case", choices=["c5_full", "gemm_prefill"],
+    ap.add_argument("--profile-case", choices=["c5_full", "gemm_prefill", "c5_sparse", "c4"],
                     help="only dispatch one workload's calls (for rocprofv3 --pmc runs); prints nothing")
     args = ap.parse_args()
     if args.gpus != 1:
