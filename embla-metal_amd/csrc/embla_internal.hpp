@@ -164,14 +164,18 @@ int launch_prefill_ring(const PrefillArgs& a, hipStream_t st);
 
 int launch_index_scores(const uint16_t* qi, const float* w, const uint16_t* ki, float* scores, int n, int n_ih,
                         hipStream_t st, uint32_t* sw = nullptr);
-/// Words (4 bytes) of the wide select's workspace: two histogram buffers (8 copies of 256 coarse
-/// and 4096 fine bins), counters (first digit, keys above it, epoch), the candidate counts of the
-/// classify workgroups, the bitmap and their candidate regions (1024 pairs each).
+/// Words (4 bytes) of the wide select's workspace: two histogram buffers (WSEL_NCP copies of 256
+/// coarse bins), counters (first digit, keys above it, epoch), the candidate counts of the
+/// classify workgroups, the bitmap and their candidate regions (1024 pairs each), then the scorer
+/// workgroups' fine-bin rows.
 #ifndef WSEL_NCP
 #define WSEL_NCP 16   // histogram copies of the wide select (C4 step: 8 -> 32.1 us, 16 -> 29.5, 32 -> 29.6, 64 -> 31.4)
 #endif
-constexpr size_t kWideSelectWords = 2 * WSEL_NCP * (256 + 4096) + 64 + 32768 / 1024 + 32768 / 32 + 2 * 32768;
-constexpr size_t kWideSelectEpoch = 2 * WSEL_NCP * (256 + 4096) + 3;   // the epoch word's index
+constexpr size_t kWideSelectFine = 2 * WSEL_NCP * 256 + 64 + 32768 / 1024 + 32768 / 32 + 2 * 32768;
+constexpr int kWideSelectScorers = 128;   // scorer workgroups at most (32768 keys, 256 a workgroup)
+/// + the scorer workgroups' own fine-bin rows (uint16 [kWideSelectScorers][4096])
+constexpr size_t kWideSelectWords = kWideSelectFine + (size_t)kWideSelectScorers * 4096 / 2;
+constexpr size_t kWideSelectEpoch = 2 * WSEL_NCP * 256 + 3;   // the epoch word's index
 /// Index scores of keys [0, S - recent) and the first steps of their exact top-k on many
 /// workgroups (one set): the scores' histogram, then the first digit of the topk-th value, the
 /// bitmap of keys above it and the candidates in it. The last step is the consumer's

@@ -18,6 +18,7 @@
 #include "embla_internal.hpp"
 #include "wsel.hpp"
 
+
 #pragma clang fp contract(off)
 
 namespace embla {
@@ -294,7 +295,7 @@ int launch_select_topk(const float* scores, int score_stride, uint32_t* idx, int
 /// (slots from an LDS counter), whose count it stores for the last step.
 __global__ __launch_bounds__(256) void wsel_classify_kernel(const float* __restrict__ scores, int n, int topk,
                                                             uint32_t* __restrict__ sw) {
-    __shared__ uint32_t ch[CB], fh[NCP][16], sel[2], lcnt;
+    __shared__ uint32_t ch[CB], sel[2], lcnt;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     uint32_t* meta = sw + 2 * HWORDS;
     uint32_t* cnts = meta + 64;
@@ -310,21 +311,42 @@ __global__ __launch_bounds__(256) void wsel_classify_kernel(const float* __restr
     }
     uint32_t c = 0;
 #pragma unroll
-    for (int cp = 0; cp < NCP; cp++) c += H[cp * HCOPY + tid];
+    for (int cp = 0; cp < NCP; cp++) c += H[cp * CB + tid];
     ch[tid] = c;
     if (tid == 0) { sel[0] = 0; sel[1] = 0; lcnt = 0; }
+    __shared__ uint32_t fp[8];   // the fine bins of cd, two a word
+    if (tid < 8) fp[tid] = 0;
     __syncthreads();
     if (w == 0) pick256(ch, (uint32_t)topk, sel);
     __syncthreads();
     const uint32_t cd = sel[0] & (CB - 1), above_c = sel[1];
-    for (int i = tid; i < NCP * 16; i += 256) fh[i >> 4][i & 15] = H[(i >> 4) * HCOPY + CB + 16 * cd + (i & 15)];
+    {   // the fine bins of cd: the sum of the scorer workgroups' rows (their number from n, as
+        // launch_index_scores sizes its grid)
+        const int nsc = min(max(((n + 63) / 64 + 3) / 4, 1), kWideSelectScorers);
+        // (a row a thread, two bins a word; summed as packed 16-bit pairs across the wave by
+        // shuffles, no bin's total exceeding 32768, then one LDS atomic a word a wave: LDS atomics
+        // of every lane on the same 16 words cost ~19 us)
+        const uint32_t* F = sw + kWideSelectFine;
+        uint32_t x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (tid < nsc) {
+            const u4_t x0 = *(const u4_t*)(F + (size_t)tid * 2048 + 8 * cd), x1 = *(const u4_t*)(F + (size_t)tid * 2048 + 8 * cd + 4);
+#pragma unroll
+            for (int i = 0; i < 4; i++) { x[i] = x0[i]; x[4 + i] = x1[i]; }
+        }
+        if (tid < ((nsc + 63) & ~63)) {   // uniform a wave
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1)
+#pragma unroll
+                for (int i = 0; i < 8; i++) x[i] += (uint32_t)__shfl_xor((int)x[i], o, 64);
+            if (lane == 0)
+#pragma unroll
+                for (int i = 0; i < 8; i++) atomicAdd(&fp[i], x[i]);
+        }
+    }
     if (tid == 0) sel[0] = 16 * cd;
     __syncthreads();
     if (w == 0) {   // lanes < 16: fine bins 16 cd + 15 - lane, from the top
-        uint32_t v = 0;
-        if (lane < 16)
-#pragma unroll
-            for (int cp = 0; cp < NCP; cp++) v += fh[cp][15 - lane];
+        const uint32_t v = lane < 16 ? (fp[(15 - lane) >> 1] >> (16 * ((15 - lane) & 1))) & 0xFFFF : 0u;
         uint32_t incl = v;
 #pragma unroll
         for (int o = 1; o < 16; o <<= 1) {
@@ -443,13 +465,22 @@ __global__ __launch_bounds__(256) void index_scores_kernel(const uint16_t* __res
     if (sw) {
         __syncthreads();
         const int t = threadIdx.x;
-        uint32_t* H = sw + (epoch & 1) * HWORDS + (blockIdx.x % NCP) * HCOPY;
+        uint32_t* H = sw + (epoch & 1) * HWORDS + (blockIdx.x % NCP) * CB;
         uint32_t cs = 0;
+        // the coarse bins by device atomics (few distinct a workgroup); the fine bins as this
+        // workgroup's own uint16 row of the fine table, by plain stores (classify sums the rows
+        // for the one coarse digit it picks: device atomics on ~100 fine bins a workgroup cost
+        // ~2 us a call)
+        uint32_t pk[8];
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const uint32_t c = lh[16 * t + i];
-            if (c) { atomicAdd(&H[CB + 16 * t + i], c); cs += c; }
+        for (int i = 0; i < 8; i++) {
+            const uint32_t c0 = lh[16 * t + 2 * i], c1 = lh[16 * t + 2 * i + 1];   // <= 256 each
+            cs += c0 + c1;
+            pk[i] = c0 | (c1 << 16);
         }
+        uint32_t* F = sw + kWideSelectFine + (size_t)blockIdx.x * 2048 + 8 * t;
+        *(u4_t*)F = (u4_t){pk[0], pk[1], pk[2], pk[3]};
+        *(u4_t*)(F + 4) = (u4_t){pk[4], pk[5], pk[6], pk[7]};
         if (cs) atomicAdd(&H[t], cs);
         uint32_t* Z = sw + ((epoch + 1) & 1) * HWORDS;
         for (int q = blockIdx.x * 256 + t; q < HWORDS; q += gridDim.x * 256) Z[q] = 0;

@@ -14,12 +14,13 @@ constexpr int SEL_MAXN = 32768;             // candidates a set
 constexpr int DB = 4096;                    // the wide select's 12-bit digits: bits 31..20, 19..8
 constexpr int CB = 256;                     // its coarse first digit: bits 31..24
 constexpr int NCP = WSEL_NCP;               // histogram copies (scorer workgroup % NCP)
-constexpr int HCOPY = CB + DB;              // words a copy: coarse bins, then fine bins
-constexpr int HWORDS = NCP * HCOPY;         // words a histogram buffer (two, by call parity)
-// The workspace sw, in words: two histogram buffers [2][HWORDS]; meta[64] (1: the first digit d1
-// of the topk-th largest, 2: keys in digits above d1, 3: the epoch picking the buffer); the
-// classify workgroups' candidate counts [SEL_MAXN / 1024]; the bitmap of keys above d1
-// [SEL_MAXN / 32]; each classify workgroup's candidate region (order bits, index) x 1024.
+constexpr int HWORDS = NCP * CB;            // words a histogram buffer (two, by call parity)
+// The workspace sw, in words: two coarse histogram buffers [2][HWORDS] (NCP copies of the
+// scores' top-8-bit counts); meta[64] (1: the first digit d1 of the topk-th largest, 2: keys in
+// digits above d1, 3: the epoch picking the buffer); the classify workgroups' candidate counts
+// [SEL_MAXN / 1024]; the bitmap of keys above d1 [SEL_MAXN / 32]; each classify workgroup's
+// candidate region (order bits, index) x 1024 (from kWideSelectFine on: the scorer workgroups'
+// own rows of top-12-bit counts, uint16 [kWideSelectScorers][4096]).
 __device__ __forceinline__ const uint32_t* wsel_meta(const uint32_t* sw) { return sw + 2 * HWORDS; }
 static_assert(kWideSelectEpoch == 2 * HWORDS + 3, "the epoch word is meta[3]");
 
