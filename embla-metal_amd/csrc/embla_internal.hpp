@@ -173,6 +173,11 @@ int launch_index_scores(const uint16_t* qi, const float* w, const uint16_t* ki, 
 #endif
 constexpr size_t kWideSelectFine = 2 * WSEL_NCP * 256 + 64 + 32768 / 1024 + 32768 / 32 + 2 * 32768;
 constexpr int kWideSelectScorers = 128;   // scorer workgroups at most (32768 keys, 256 a workgroup)
+/// Workgroups of index_scores_kernel for n keys (256 keys a workgroup, at most 1024): the scorer's
+/// grid, and with the wide select the number of fine-bin rows it leaves.
+__host__ __device__ constexpr int index_score_blocks(int n) {
+    return ((n + 63) / 64 + 3) / 4 < 1 ? 1 : (((n + 63) / 64 + 3) / 4 > 1024 ? 1024 : ((n + 63) / 64 + 3) / 4);
+}
 /// + the scorer workgroups' own fine-bin rows (uint16 [kWideSelectScorers][4096])
 constexpr size_t kWideSelectWords = kWideSelectFine + (size_t)kWideSelectScorers * 4096 / 2;
 constexpr size_t kWideSelectEpoch = 2 * WSEL_NCP * 256 + 3;   // the epoch word's index

@@ -320,9 +320,8 @@ __global__ __launch_bounds__(256) void wsel_classify_kernel(const float* __restr
     if (w == 0) pick256(ch, (uint32_t)topk, sel);
     __syncthreads();
     const uint32_t cd = sel[0] & (CB - 1), above_c = sel[1];
-    {   // the fine bins of cd: the sum of the scorer workgroups' rows (their number from n, as
-        // launch_index_scores sizes its grid)
-        const int nsc = min(max(((n + 63) / 64 + 3) / 4, 1), kWideSelectScorers);
+    {   // the fine bins of cd: the sum of the scorer workgroups' rows (one a scorer workgroup)
+        const int nsc = min(index_score_blocks(n), kWideSelectScorers);
         // (a row a thread, two bins a word; summed as packed 16-bit pairs across the wave by
         // shuffles, no bin's total exceeding 32768, then one LDS atomic a word a wave: LDS atomics
         // of every lane on the same 16 words cost ~19 us)
@@ -489,10 +488,7 @@ __global__ __launch_bounds__(256) void index_scores_kernel(const uint16_t* __res
 
 int launch_index_scores(const uint16_t* qi, const float* w, const uint16_t* ki, float* scores, int n, int n_ih,
                         hipStream_t st, uint32_t* sw) {
-    const int waves = (n + 63) / 64;
-    int blocks = (waves + 3) / 4;
-    if (blocks > 1024) blocks = 1024;
-    if (blocks < 1) blocks = 1;
+    const int blocks = index_score_blocks(n);
     switch (n_ih) {
         case 1: hipLaunchKernelGGL(index_scores_kernel<1>, dim3(blocks), dim3(256), 0, st, qi, w, ki, scores, n, sw); break;
         case 2: hipLaunchKernelGGL(index_scores_kernel<2>, dim3(blocks), dim3(256), 0, st, qi, w, ki, scores, n, sw); break;
