@@ -399,9 +399,10 @@ int launch_wide_select(const uint16_t* qi, const float* w, const uint16_t* ki, f
 /// A wave takes 64 keys a round: load j (16 bytes a lane) covers keys 8j .. 8j + 7, lane l holding
 /// key 8j + l / 8, dims 8 (l % 8) .. + 7, so every load of the wave reads 1 KB contiguous.
 /// With the wide select's workspace `sw`, each workgroup also counts its scores' top 12 order bits
-/// in LDS and adds them to histogram copy blockIdx % NCP of this call's buffer (sw's epoch word
-/// picks one of two): fine bins (12 bits) and coarse bins (top 8), thread t adding the 16 fine
-/// bins of coarse bin t. It also clears its slice of the other buffer for the next call.
+/// in LDS, then thread t adds the total of coarse bin t (the top 8 bits) to histogram copy
+/// blockIdx % NCP of this call's buffer (sw's epoch word picks one of two) and stores its 16 fine
+/// bins (12 bits) as uint16 into the workgroup's own fine-bin row. It also clears its slice of the
+/// other coarse buffer for the next call.
 template <int NIH>
 __global__ __launch_bounds__(256) void index_scores_kernel(const uint16_t* __restrict__ qi, const float* __restrict__ wt,
                                                            const uint16_t* __restrict__ ki, float* __restrict__ scores,
