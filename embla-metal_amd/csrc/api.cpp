@@ -501,21 +501,29 @@ int embla_select_keys(const float* scores, uint32_t* idx, int S, int maxS, hipSt
 }
 
 namespace {
-/// embla_sparse_decode, optionally with the wide select's last step fused (fs: its fields of
-/// SparseArgs, sel_* set).
-int sparse_decode_impl(const void* q, const void* kc, const void* vc, const uint32_t* idx, int idx_stride, int nsel,
-                       void* o, int max_s, int n_q, int n_kv, int dtype, int chunk, void* ws, size_t ws_bytes,
-                       const SparseArgs* fs, hipStream_t stream) {
+/// Checks embla_sparse_decode's arguments and fills its launch (fs: the wide select's fields of
+/// SparseArgs, sel_* set, for the select's last step fused into the attention). Launches nothing,
+/// so a caller can check every argument before it starts any kernel of a multi-kernel step.
+int sparse_decode_prepare(const void* q, const void* kc, const void* vc, const uint32_t* idx, int idx_stride,
+                          int nsel, void* o, int max_s, int n_q, int n_kv, int dtype, int chunk, void* ws,
+                          size_t ws_bytes, const SparseArgs* fs, SparseArgs& a) {
     if (!q || !kc || !vc || !o || nsel <= 0 || max_s <= 0 || idx_stride < 0) return EMBLA_ERR_INVALID;
     if (!idx && nsel > max_s) return EMBLA_ERR_INVALID;
     if (n_kv <= 0 || n_q % n_kv || n_kv > kMaxKV || !valid_act(dtype)) return EMBLA_ERR_INVALID;
     if (n_q / n_kv != 4 && n_q / n_kv != 8) return EMBLA_ERR_UNSUPPORTED;
     if (chunk < 0 || chunk % 32) return EMBLA_ERR_INVALID;
-    const int ch = chunk ? chunk : env_int("EMBLA_SPARSE_CH", 64);   // C4 step: 32.0 us at 64, 32.4 at 128, 36.4 at 256
+    int ch = chunk ? chunk : env_int("EMBLA_SPARSE_CH", 64);   // C4 step: 32.0 us at 64, 32.4 at 128, 36.4 at 256
+    if (ch <= 0 || ch % 32) return EMBLA_ERR_INVALID;
+    if (fs) {   // the fused select ranks a chunk's rows in LDS: at most kSparseFusedMaxCh of them
+        if (ch > kSparseFusedMaxCh) ch = kSparseFusedMaxCh;
+        if (!fs->sel_ws || !fs->sel_epoch || fs->sel_topk <= 0 || fs->sel_n <= fs->sel_topk ||
+            fs->sel_n > kWideSelectMaxN || nsel < fs->sel_topk)
+            return EMBLA_ERR_INVALID;
+    }
     const int C = (nsel + ch - 1) / ch;
     if (C > kMaxChunks) return EMBLA_ERR_INVALID;
     if (C > 1 && (!ws || ws_bytes < embla_workspace_bytes(32 * C, n_q))) return EMBLA_ERR_WORKSPACE;
-    SparseArgs a;
+    a = SparseArgs{};
     a.q = (const uint16_t*)q; a.kc = (const uint16_t*)kc; a.vc = (const uint16_t*)vc;
     a.idx = idx; a.idx_stride = idx_stride; a.nsel = nsel;
     a.part = ws ? carve(ws, 32 * C, n_q).part : nullptr;
@@ -525,21 +533,29 @@ int sparse_decode_impl(const void* q, const void* kc, const void* vc, const uint
         a.sel_ws = fs->sel_ws; a.sel_n = fs->sel_n; a.sel_topk = fs->sel_topk;
         a.sel_out = fs->sel_out; a.sel_epoch = fs->sel_epoch;
     }
-    return launch_sparse_decode(a, stream);
+    return EMBLA_OK;
 }
 }  // namespace
 
 int embla_sparse_decode(const void* q, const void* kc, const void* vc, const uint32_t* idx, int idx_stride,
                         int nsel, void* o, int max_s, int n_q, int n_kv, int dtype, int chunk, void* ws,
                         size_t ws_bytes, hipStream_t stream) {
-    return sparse_decode_impl(q, kc, vc, idx, idx_stride, nsel, o, max_s, n_q, n_kv, dtype, chunk, ws, ws_bytes,
-                              nullptr, stream);
+    SparseArgs a;
+    const int rc = sparse_decode_prepare(q, kc, vc, idx, idx_stride, nsel, o, max_s, n_q, n_kv, dtype, chunk, ws,
+                                         ws_bytes, nullptr, a);
+    return rc ? rc : launch_sparse_decode(a, stream);
 }
 
 size_t embla_sparse_workspace_bytes(int max_s, int n_q) {
     if (max_s <= 0 || n_q <= 0) return 0;
     return round_up((size_t)max_s * 4, 256) + round_up((size_t)(kTopK + kRecent) * 4, 256) +
            round_up(embla_workspace_bytes(kTopK + kRecent, n_q), 256) + kWideSelectWords * 4;
+}
+
+size_t embla_sparse_workspace_recount_offset(int max_s, int n_q) {
+    if (max_s <= 0 || n_q <= 0) return 0;
+    return round_up((size_t)max_s * 4, 256) + round_up((size_t)(kTopK + kRecent) * 4, 256) +
+           round_up(embla_workspace_bytes(kTopK + kRecent, n_q), 256) + kWideSelectRecounts * 4;
 }
 
 int embla_sparse_layer_decode(const void* q, const void* qi, const float* w, const void* ki, const void* kc,
@@ -556,18 +572,22 @@ int embla_sparse_layer_decode(const void* q, const void* qi, const float* w, con
         return embla_sparse_decode(q, kc, vc, nullptr, 0, S, o, max_s, n_q, n_kv, dtype, 0, aws, abytes, stream);
     if (n_ih != 1 && n_ih != 2 && n_ih != 4) return EMBLA_ERR_UNSUPPORTED;
     // index scores, then the exact top-k on many workgroups (the select's workspace follows the
-    // decode's; it is zero before the first call and every call leaves it zero)
+    // decode's). Its last step runs inside the attention's workgroups, each ranking the rows it
+    // attends; the selection still lands in idx. Every argument of both launches is checked
+    // before the first: a call rejected after the scorer had counted into the histogram buffer
+    // would leave that buffer stale for the next call.
     uint32_t* sel_ws = (uint32_t*)((char*)aws + round_up(abytes, 256));
-    // (its last step runs inside the attention's workgroups, each ranking the rows it attends;
-    // the selection still lands in idx)
-    const int rc = launch_wide_select((const uint16_t*)qi, w, (const uint16_t*)ki, scores, S, n_ih, kTopK, kRecent,
-                                      sel_ws, stream);
-    if (rc) return rc;
     SparseArgs fs;
     fs.sel_ws = sel_ws; fs.sel_n = S - kRecent; fs.sel_topk = kTopK; fs.sel_out = idx;
     fs.sel_epoch = sel_ws + kWideSelectEpoch;
-    return sparse_decode_impl(q, kc, vc, nullptr, 0, kTopK + kRecent, o, max_s, n_q, n_kv, dtype, 0, aws, abytes, &fs,
-                              stream);
+    SparseArgs a;
+    int rc = sparse_decode_prepare(q, kc, vc, nullptr, 0, kTopK + kRecent, o, max_s, n_q, n_kv, dtype, 0, aws, abytes,
+                                   &fs, a);
+    if (rc) return rc;
+    rc = launch_wide_select((const uint16_t*)qi, w, (const uint16_t*)ki, scores, S, n_ih, kTopK, kRecent, sel_ws,
+                            stream);
+    if (rc) return rc;
+    return launch_sparse_decode(a, stream);
 }
 
 size_t embla_prefill_workspace_bytes(int T, int n_q) {

@@ -151,6 +151,11 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
 
     i4_t qb[2], ql[2];
     float qsc = 0.0f;   // the fixed point's step, per head
+    // SCORES (the reference's full layer, whose scores feed select_keys): q stays a 16-bit float
+    // and S^T runs on v_mfma_f32_16x16x32_f16 with K widened exactly to fp16, so every product is
+    // exact and the sums are fp32 (the fixed point's 2^-16 relative error would move near-ties in
+    // or out of the top 1024). MFMA j: lane (n, g) dims 32g + 8j .. + 7, column n = head n.
+    h8_t qh[SCORES ? 4 : 1];
     // q as a 15-bit fixed point split into int8 halves, hi in qb and lo in ql: column n < GQ holds
     // head n (other columns 0); lane (n, g), MFMA b: dims 32g + 16b .. + 15 (the K slice's dims).
     // Separate operands put both halves' products in the lane that uses them (no cross-lane step).
@@ -188,6 +193,13 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
                 if (ng >= 2) gf = gf * (1.0f + bf2f((uint16_t)(d & 1 ? wb >> 16 : wb & 0xFFFF)));
                 qf[d] = bf2f(f2bf(qf[d] * gf));
             }
+        }
+        if constexpr (SCORES) {   // bf16 / fp16 q as fp16 (bf16 exact down to 2^-17)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) qh[j][e] = live ? (_Float16)qf[8 * j + e] : (_Float16)0.0f;
+            return;
         }
 #pragma unroll
         for (int d = 0; d < 32; d++) am = fmaxf(am, fabsf(qf[d]));
@@ -236,7 +248,19 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
         // S^T (int32) of the two 16-key halves: lane (n, g) item i of half t = key t0 + 16t + 4g + i
         float x[8];
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
+        for (int t = 0; t < 2 && SCORES; t++) {
+            f4_t sf = {0, 0, 0, 0};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const u4_t r = T.k[2 * t + j / 2];
+                const h8_t a = (j & 1) ? i8x8_to_h8(r[2], r[3]) : i8x8_to_h8(r[0], r[1]);
+                sf = mfma16(a, qh[j], sf);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) x[4 * t + i] = sf[i] * ks[4 * t + i];
+        }
+#pragma unroll
+        for (int t = 0; t < 2 && !SCORES; t++) {
             i4_t st = {0, 0, 0, 0}, sl = {0, 0, 0, 0};
             st = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i4_t, T.k[2 * t]), qb[0], st, 0, 0, 0);
             st = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i4_t, T.k[2 * t + 1]), qb[1], st, 0, 0, 0);

@@ -37,7 +37,7 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-constexpr int SPD_FS_MAXCH = 256;   // keys a workgroup with the select's last step fused
+constexpr int SPD_FS_MAXCH = kSparseFusedMaxCh;
 
 template <int GQ, bool BF, bool FS>
 __global__ __launch_bounds__(256) void sparse_decode_kernel(SparseArgs a) {
@@ -82,10 +82,13 @@ __global__ __launch_bounds__(256) void sparse_decode_kernel(SparseArgs a) {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int p = t0 + 4 * j + (lane >> 4);
-            int r = p;
-            if constexpr (FS) r = p < a.sel_topk ? (int)srows[p - j0] : a.sel_n + p - a.sel_topk;
-            else if (rows) r = (int)rows[p];
-            const size_t row = p < j1 ? (size_t)min(r, a.max_s - 1) : 0;   // rows clamped in range
+            // keys past the chunk's last (p >= j1) read row 0 and nothing of the index lists
+            int r = 0;
+            if (p < j1) {
+                if constexpr (FS) r = p < a.sel_topk ? (int)srows[p - j0] : a.sel_n + p - a.sel_topk;
+                else r = rows ? (int)rows[p] : p;
+            }
+            const size_t row = (size_t)min(r, a.max_s - 1);   // rows clamped in range
             kr[j] = ld16(kb + row * HD + 8 * n);
             vr[j] = ld16(vb + row * HD + 8 * n);
         }

@@ -87,6 +87,8 @@ struct SparseArgs {
     uint32_t* sel_epoch = nullptr;
 };
 int launch_sparse_decode(const SparseArgs& a, hipStream_t st);
+constexpr int kSparseFusedMaxCh = 256;    // keys a workgroup with the select's last step fused
+constexpr int kWideSelectMaxN = 32768;    // candidates a set of the wide select
 
 /// Gathered softmax attention over an int8 cache: query row r (position p0 + r) attends the keys
 /// idx[r][0 .. nsel) (at idx + r * idx_row_stride + kv head * idx_kv_stride) when p0 + r + 1 > nsel,
@@ -181,6 +183,7 @@ __host__ __device__ constexpr int index_score_blocks(int n) {
 /// + the scorer workgroups' own fine-bin rows (uint16 [kWideSelectScorers][4096])
 constexpr size_t kWideSelectWords = kWideSelectFine + (size_t)kWideSelectScorers * 4096 / 2;
 constexpr size_t kWideSelectEpoch = 2 * WSEL_NCP * 256 + 3;   // the epoch word's index
+constexpr size_t kWideSelectRecounts = 2 * WSEL_NCP * 256 + 4;   // calls that found a stale histogram
 /// Index scores of keys [0, S - recent) and the first steps of their exact top-k on many
 /// workgroups (one set): the scores' histogram, then the first digit of the topk-th value, the
 /// bitmap of keys above it and the candidates in it. The last step is the consumer's

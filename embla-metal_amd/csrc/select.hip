@@ -295,7 +295,7 @@ int launch_select_topk(const float* scores, int score_stride, uint32_t* idx, int
 /// (slots from an LDS counter), whose count it stores for the last step.
 __global__ __launch_bounds__(256) void wsel_classify_kernel(const float* __restrict__ scores, int n, int topk,
                                                             uint32_t* __restrict__ sw) {
-    __shared__ uint32_t ch[CB], sel[2], lcnt;
+    __shared__ uint32_t ch[CB], sel[2], lcnt, total;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     uint32_t* meta = sw + 2 * HWORDS;
     uint32_t* cnts = meta + 64;
@@ -317,8 +317,23 @@ __global__ __launch_bounds__(256) void wsel_classify_kernel(const float* __restr
     __shared__ uint32_t fp[8];   // the fine bins of cd, two a word
     if (tid < 8) fp[tid] = 0;
     __syncthreads();
-    if (w == 0) pick256(ch, (uint32_t)topk, sel);
+    if (w == 0) pick256(ch, (uint32_t)topk, sel, &total);
     __syncthreads();
+    if (total != (uint32_t)n) {
+        // (uniform) The buffer held counts from before this call's scorer: a workspace that was
+        // not zeroed, was overwritten, or saw a call stop between its scorer and its attention.
+        // Its bins cannot be trusted, so this workgroup counts the coarse digits of all n scores
+        // itself (exact, ~n / 256 loads a thread); the next call's buffer is clean again, as this
+        // call's scorer cleared it. meta[4] counts such calls.
+        ch[tid] = 0;
+        if (tid == 0) { sel[0] = 0; sel[1] = 0; }
+        __syncthreads();
+        for (int j = tid; j < n; j += 256) atomicAdd(&ch[order_bits(scores[j]) >> 24], 1u);
+        __syncthreads();
+        if (w == 0) pick256(ch, (uint32_t)topk, sel);
+        if (blockIdx.x == 0 && tid == 0) atomicAdd(&meta[4], 1u);
+        __syncthreads();
+    }
     const uint32_t cd = sel[0] & (CB - 1), above_c = sel[1];
     {   // the fine bins of cd: the sum of the scorer workgroups' rows (one a scorer workgroup)
         const int nsc = min(index_score_blocks(n), kWideSelectScorers);

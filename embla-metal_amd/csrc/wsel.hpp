@@ -10,14 +10,15 @@
 
 namespace embla {
 
-constexpr int SEL_MAXN = 32768;             // candidates a set
+constexpr int SEL_MAXN = kWideSelectMaxN;   // candidates a set
 constexpr int DB = 4096;                    // the wide select's 12-bit digits: bits 31..20, 19..8
 constexpr int CB = 256;                     // its coarse first digit: bits 31..24
 constexpr int NCP = WSEL_NCP;               // histogram copies (scorer workgroup % NCP)
 constexpr int HWORDS = NCP * CB;            // words a histogram buffer (two, by call parity)
 // The workspace sw, in words: two coarse histogram buffers [2][HWORDS] (NCP copies of the
 // scores' top-8-bit counts); meta[64] (1: the first digit d1 of the topk-th largest, 2: keys in
-// digits above d1, 3: the epoch picking the buffer); the classify workgroups' candidate counts
+// digits above d1, 3: the epoch picking the buffer, 4: calls that found their histogram buffer
+// not clean and recounted, kWideSelectRecounts); the classify workgroups' candidate counts
 // [SEL_MAXN / 1024]; the bitmap of keys above d1 [SEL_MAXN / 32]; each classify workgroup's
 // candidate region (order bits, index) x 1024 (from kWideSelectFine on: the scorer workgroups'
 // own rows of top-12-bit counts, uint16 [kWideSelectScorers][4096]).
@@ -56,8 +57,9 @@ __device__ __forceinline__ void pick4096(const uint32_t* h, uint32_t k, uint32_t
     if (base + incl - c < k && base + incl >= k) { sel[0] = (uint32_t)d; sel[1] = base + incl - c; }
 }
 
-/// Digit (of 256) holding the k-th largest: wave 0, 4 digits a lane from the top.
-__device__ __forceinline__ void pick256(const uint32_t* h, uint32_t k, uint32_t* sel) {
+/// Digit (of 256) holding the k-th largest: wave 0, 4 digits a lane from the top. total (if set)
+/// receives the sum of all 256 counts.
+__device__ __forceinline__ void pick256(const uint32_t* h, uint32_t k, uint32_t* sel, uint32_t* total = nullptr) {
     const int lane = threadIdx.x & 63;
     uint32_t cc[4], s = 0;
 #pragma unroll
@@ -68,6 +70,7 @@ __device__ __forceinline__ void pick256(const uint32_t* h, uint32_t k, uint32_t*
         const uint32_t x = __shfl_up(above, o, 64);
         if (lane >= o) above += x;
     }
+    if (total && lane == 63) *total = above;
     above -= s;
 #pragma unroll
     for (int i = 0; i < 4; i++) {

@@ -244,10 +244,16 @@ class SparseWorkspace:
         self.max_s = max_s
         self.nbytes = int(lib().embla_sparse_workspace_bytes(max_s, n_q))
         self.buf = torch.zeros(self.nbytes, dtype=torch.uint8, device=device)
+        self.recount_off = int(lib().embla_sparse_workspace_recount_offset(max_s, n_q))
 
     @property
     def ptr(self):
         return _p(self.buf)
+
+    def recounts(self) -> int:
+        """Calls that found the select's histogram buffer not clean and recounted it (a device word
+        of the workspace; reading it synchronises)."""
+        return int(self.buf[self.recount_off:self.recount_off + 4].view(torch.int32).item())
 
     def selection(self):
         """The last sparse_layer_decode call's selected rows (top 1024 + latest 128), int32 [1152]:

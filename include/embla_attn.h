@@ -165,9 +165,16 @@ int embla_sparse_decode(const void* q, const void* kc, const void* vc, const uin
                         int nsel, void* o, int max_s, int n_q, int n_kv, int dtype, int chunk, void* ws,
                         size_t ws_bytes, hipStream_t stream);
 
-/* Bytes of workspace for embla_sparse_layer_decode: zero-filled before its first use (every call
- * leaves its counters zero again). */
+/* Bytes of workspace for embla_sparse_layer_decode: zero-fill it before its first use (every call
+ * leaves its counters clean for the next). A workspace that is not clean (never zeroed,
+ * overwritten, or left by a call stopped between its kernels) never yields a wrong selection: the
+ * select checks that its histogram counts exactly this call's keys and otherwise recounts them
+ * from the scores (that call is slower; the next is clean again). The 32-bit word at
+ * embla_sparse_workspace_recount_offset(max_s, n_q) counts such calls. */
 size_t embla_sparse_workspace_bytes(int max_s, int n_q);
+/* Byte offset, in embla_sparse_layer_decode's workspace, of its count of recounted calls (no
+ * counterpart in the reference: it lets a caller audit the workspace's state). */
+size_t embla_sparse_workspace_recount_offset(int max_s, int n_q);
 
 /* One sparse-layer decode step (config C4): with S > 1152 keys, index scores of keys
  * [0, S - 128), the top 1024 plus the latest 128, then attention over those 1152 rows; with

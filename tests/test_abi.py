@@ -153,3 +153,26 @@ def test_bf16_cache_entry_points_reject_bad_arguments():
     assert L.embla_kv_append_bf16(d, d, jobs, 1, 1000, 1024, 30, None) == _lib.EMBLA_ERR_INVALID   # past maxS
     pb = _lib.AttnB(1000, 0, 0, 1024)
     assert L.embla_attn_full_b(d, d, d, d, d, d, d, d, C.byref(pb), 30, None) == _lib.EMBLA_ERR_INVALID
+
+
+@pytest.mark.parametrize("n_q,n_kv,n_ih,dtype,rc", [(16, 3, 4, 0, _lib.EMBLA_ERR_INVALID),
+                                                     (16, 4, 4, 9, _lib.EMBLA_ERR_INVALID),
+                                                     (16, 16, 4, 0, _lib.EMBLA_ERR_UNSUPPORTED),
+                                                     (16, 4, 3, 0, _lib.EMBLA_ERR_UNSUPPORTED)])
+def test_sparse_layer_rejects_before_any_launch(n_q, n_kv, n_ih, dtype, rc):
+    """Every argument of the sparse layer's kernels (scorer, classify, attention) is checked before
+    the first launch: a call rejected after its scorer had counted would leave the select's
+    histogram stale. (Fake pointers: a launch here, with no GPU, could not return these codes.)"""
+    L = _lib.lib()
+    d = C.c_void_p(256)
+    nb = L.embla_sparse_workspace_bytes(32768, n_q)
+    got = L.embla_sparse_layer_decode(d, d, d, d, d, d, d, 32768, 32768, n_q, n_kv, n_ih, dtype, d, nb, None)
+    assert got == rc
+
+
+def test_sparse_workspace_recount_word_inside():
+    L = _lib.lib()
+    for max_s, n_q in [(32768, 16), (4096, 32), (1153, 8)]:
+        nb, off = L.embla_sparse_workspace_bytes(max_s, n_q), L.embla_sparse_workspace_recount_offset(max_s, n_q)
+        assert off % 4 == 0 and 0 < off < nb - 4
+    assert L.embla_sparse_workspace_recount_offset(0, 16) == 0

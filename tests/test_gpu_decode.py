@@ -147,9 +147,67 @@ def test_full8_reference_mode(torch_gpu, orc):
                    for h in range(16)])
     ref, ref_sc = orc.decode_int8(qn, K, ks, V, vs, weights=1, want_scores=True)
     assert_close(bf16_host(o), ref, what="full8 o")
-    # scores carry q's 15-bit fixed point (|q error| <= absmax(q)/64000): 1e-3 of their scale
-    assert_close(scores.cpu().numpy()[:, :S], ref_sc, atol=1e-3 * np.abs(ref_sc).max(), rtol=0, what="full8 scores")
+    # scores are fp32 sums of exact products: within 2^-16 of sum_d |q_d k_d| ks (128 roundings of
+    # 2^-24 each, with a 2x margin), the max over the kv head's query heads
+    got_sc = scores.cpu().numpy()[:, :S]
+    bound = np.stack([(np.abs(qn[8 * h:8 * h + 8]) @ np.abs(K[h].astype(np.float64)).T).max(0) * ks[h]
+                      for h in range(2)])
+    assert (np.abs(got_sc - ref_sc) <= bound * 2.0 ** -16).all(), np.abs(got_sc - ref_sc).max()
     assert not counter.cpu().numpy().any()
+
+
+def test_full8_scores_select_sparse8_chain_near_ties(torch_gpu, orc):
+    """The reference's full -> select_keys -> sparse chain (Engine.swift:796-827): attn_full8's
+    SCORES feed embla_select_keys, whose rows feed attn_sparse8 (SEL). The scales put 1000 keys a kv
+    head clearly above the threshold and 60 in a cluster around it whose scores are 2e-6 apart
+    (~30 fp32 steps): the selection must be the oracle's bit for bit, which a q rounded to a
+    16-bit fixed point (relative error ~1e-4) cannot give."""
+    import torch
+    from embla_attn import ops, _lib
+    say("full8 -> select_keys -> sparse8 near ties")
+    S, max_s = 3000, 4096
+    g = synth.SplitMix64(43)
+    qraw = synth.bf16_bits(g.normal(16 * 128) * 2)
+    g1 = synth.bf16_bits(g.normal(128) * 0.2)
+    g2 = synth.bf16_bits(g.normal(128) * 0.2)
+    K = g.int8(2 * S * 128).reshape(2, S, 128)
+    V = g.int8(2 * S * 128).reshape(2, S, 128)
+    vs = (0.02 + 0.01 * g.uniform(2 * S)).astype(np.float32).reshape(2, S)
+    qn = np.stack([orc.head_norm(synth.bf16_val(qraw.reshape(16, 128)[h]), synth.bf16_val(g1), synth.bf16_val(g2), 2)
+                   for h in range(16)])
+    ks = (0.02 + 0.01 * g.uniform(2 * S)).astype(np.float32).reshape(2, S)
+    near_sets = []
+    for h in range(2):
+        d = (qn[8 * h:8 * h + 8].astype(np.float64) @ K[h].astype(np.float64).T).max(0)   # [S]
+        T = 1.25 * np.abs(d).max() * 0.03   # above every other key's score
+        order = np.argsort(-d[:S - 128], kind="stable")   # the largest dots (all > 0)
+        top, near = order[:1000], order[1000:1060]
+        assert d[near].min() > 0.2 * d[order[0]]
+        ks[h, top] = (1.5 * T / d[top]).astype(np.float32)
+        r = np.argsort(g.uniform(60)) - 30   # a shuffled cluster: index order is not score order
+        near_sets.append(near)
+        ks[h, near] = (T * (1.0 + 2e-6 * r) / d[near]).astype(np.float32)
+    kc = dev(layout.pack_region(K, ks, max_s, "k"))
+    vc = dev(layout.pack_region(V, vs, max_s, "v"))
+    part = torch.zeros(_lib.lib().embla_workspace_bytes(max_s, 16), dtype=torch.uint8, device="cuda")
+    counter = torch.zeros(2, dtype=torch.int32, device="cuda")
+    scores = torch.full((2, max_s), -1.0, dtype=torch.float32, device="cuda")
+    o = torch.empty((16, 128), dtype=torch.bfloat16, device="cuda")
+    qd, g1d, g2d = dev(qraw, torch.bfloat16), dev(g1, torch.bfloat16), dev(g2, torch.bfloat16)
+    ops.attn_full8(qd, g1d, g2d, kc, vc, part, scores, counter, o, S, max_s, ng=2)
+    idx = ops.select_keys(scores, S, max_s)
+    o2 = torch.empty((16, 128), dtype=torch.bfloat16, device="cuda")
+    ops.attn_sparse8(qd, g1d, g2d, kc, vc, part, idx, counter, o2, 1152, max_s)
+    torch.cuda.synchronize()
+    ref_o, ref_sc = orc.decode_int8(qn, K, ks, V, vs, weights=1, want_scores=True)
+    assert_close(bf16_host(o), ref_o, what="chain full8 o")
+    ref_rows = np.stack([orc.select_keys(np.ascontiguousarray(ref_sc[h]), S) for h in range(2)])
+    got_rows = idx.cpu().numpy().astype(np.uint32).reshape(2, 1152)
+    for h in range(2):   # the cluster straddles the threshold: 24 of its 60 keys are in
+        assert np.isin(near_sets[h], ref_rows[h, :1024]).sum() == 24
+    np.testing.assert_array_equal(got_rows, ref_rows)
+    ref2 = orc.decode_int8(qn, K, ks, V, vs, weights=0, rows=ref_rows, n_sel=1152)
+    assert_close(bf16_host(o2), ref2, what="chain sparse8 o")
 
 
 @pytest.mark.parametrize("sel", [True, False])

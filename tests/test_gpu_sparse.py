@@ -199,3 +199,71 @@ def test_select_topk_many_sets_unaligned(torch_gpu, orc):
         row = np.concatenate([sc[s, :S - recent], np.zeros(recent, np.float32)])
         ref = orc.select_keys(row, S, topk=topk, recent=recent)
         np.testing.assert_array_equal(got[s], ref, err_msg=f"set {s}")
+
+
+def _c4_args(torch, c4):
+    return [dev(c4["q"], torch.float16), dev(c4["qi"], torch.float16), dev(c4["w"]), dev(c4["ki"], torch.float16),
+            dev(c4["K"], torch.float16), dev(c4["V"], torch.float16)]
+
+
+def _c4_ref_selection(orc, c4, S):
+    sc = orc.index_scores(c4["qi"], c4["w"], c4["ki"][:S - 128])
+    return orc.select_keys(np.concatenate([sc, np.zeros(128, np.float32)]), S)
+
+
+def test_sparse_layer_dirty_workspace_recounts(torch_gpu, orc, c4):
+    """A workspace full of random bytes (never zeroed) still gives select_keys' selection bit for
+    bit: the select finds that its histogram does not count exactly this call's keys and recounts
+    them (the workspace's recount word says so once); the next call finds a clean buffer."""
+    from embla_attn import ops
+    torch = torch_gpu
+    ws = ops.SparseWorkspace(32768, 16)
+    gen = torch.Generator(device="cpu").manual_seed(7)
+    ws.buf.copy_(torch.randint(0, 256, (ws.nbytes,), dtype=torch.uint8, generator=gen))
+    ws.buf[ws.recount_off:ws.recount_off + 4].zero_()
+    args = _c4_args(torch, c4)
+    for i, S in enumerate([32768, 20011, 32768]):
+        say(f"sparse layer dirty workspace call {i} S={S}")
+        o = ops.sparse_layer_decode(*args, S, 32768, 4, ws)
+        got = ws.selection().cpu().numpy().astype(np.uint32)
+        ref = _c4_ref_selection(orc, c4, S)
+        np.testing.assert_array_equal(got, ref, err_msg=f"call {i} S={S}")
+        assert ws.recounts() == 1, f"call {i}: recounts {ws.recounts()}"
+    out = orc.decode_rows(synth.f16_val(c4["q"]), synth.f16_val(c4["K"]), synth.f16_val(c4["V"]), ref.astype(np.int32))
+    assert_close(f16_host(o), out, what="dirty workspace")
+
+
+def test_sparse_layer_rejected_call_leaves_no_state(torch_gpu, orc, c4):
+    """A call the library rejects (bad n_q / n_kv ratio, bad dtype) launches nothing, so the next
+    valid call's selection is select_keys' bit for bit with no recount; an overwritten histogram
+    buffer between calls is recounted."""
+    from embla_attn import ops
+    from embla_attn._lib import EmblaError, lib
+    from embla_attn.ops import _p
+    torch = torch_gpu
+    ws = ops.SparseWorkspace(32768, 16)
+    args = _c4_args(torch, c4)
+    S = 32768
+    ops.sparse_layer_decode(*args, S, 32768, 4, ws)
+    out = torch.empty((16, 128), dtype=torch.float16, device="cuda")
+    ptrs = [_p(a) for a in args]
+    say("sparse layer rejected calls")
+    # n_q 16 over n_kv 2 (GQ 8) with fp16 is fine, n_kv 3 is not a divisor; dtype 9 is no dtype
+    rc1 = lib().embla_sparse_layer_decode(*ptrs, _p(out), S, 32768, 16, 3, 4, 0, ws.ptr, ws.nbytes, None)
+    rc2 = lib().embla_sparse_layer_decode(*ptrs, _p(out), S, 32768, 16, 4, 4, 9, ws.ptr, ws.nbytes, None)
+    assert rc1 != 0 and rc2 != 0
+    torch.cuda.synchronize()
+    for S2 in [32768, 9001]:
+        ops.sparse_layer_decode(*args, S2, 32768, 4, ws)
+        np.testing.assert_array_equal(ws.selection().cpu().numpy().astype(np.uint32), _c4_ref_selection(orc, c4, S2))
+    assert ws.recounts() == 0
+    # stale counts in both histogram buffers (as if a call had stopped after its scorer)
+    # the select's region starts with the two histogram buffers [2][16 copies][256] and then its
+    # meta words, the recount word being meta[4]
+    base = ws.recount_off - (2 * 16 * 256 + 4) * 4
+    ws.buf[base:base + 2 * 16 * 256 * 4].view(torch.int32).add_(3)
+    ops.sparse_layer_decode(*args, S, 32768, 4, ws)
+    np.testing.assert_array_equal(ws.selection().cpu().numpy().astype(np.uint32), _c4_ref_selection(orc, c4, S))
+    assert ws.recounts() == 1
+    with pytest.raises(EmblaError):
+        ops.sparse_layer_decode(*args, S, 32768, 3, ws)
