@@ -51,9 +51,12 @@ struct __attribute__((aligned(16))) PrefillSmem {
     _Float16 vt[2][NSUB * VTILE];
 };
 
-// a split's partial record (floats): O / l as 128 fp16 (a convex combination of V rows, which the
-// P·V products already take in fp16), then m and l in fp32, padded to 16 bytes: half the bytes of
-// an fp32 O for the split pass to write and the merge to read
+// a split's partial record (floats): O / l as 128 fp16, then m and l in fp32, padded to 16 bytes:
+// half the bytes of an fp32 O for the split pass to write and the merge to read. O / l is a convex
+// combination of V rows (l is the split's own weight sum, the sink is added by the merge), and
+// every instance's P·V product already takes V as fp16: int8 V exactly, 16-bit ring V as a copy
+// (fp16 rings) or widened to fp16 in staging (bf16 rings, bf8_to_h8: exact for |v| in
+// [2^-14, 65504]). So the fp16 record loses no range that the product keeps.
 constexpr int PPH = 68;
 constexpr int PF_WAVES = 8;        // waves a workgroup: GQ query heads x (8 / GQ) 32-row blocks
 #ifndef PF_XCD
