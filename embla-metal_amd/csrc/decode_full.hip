@@ -32,7 +32,11 @@ typedef int i4_t __attribute__((ext_vector_type(4)));
 constexpr float WSCALE = 64.0f;   // prescale of W into fp16's normal range; divided out at the end
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float QFIX = 32000.0f;  // q's fixed-point range: |q_int| <= 32000, so |hi| <= 125
-constexpr int PS = HD + 4;        // floats a (chunk, query head) partial: acc[128], m, l, pad
+// A (chunk, query head) partial record, PH floats: O / (l · WSCALE) as 128 fp16 (a convex
+// combination of the dequantised V rows: fp16 holds it to |v| <= 65504, the range the P·V operand
+// gives V anyway), then m and l in fp32, padded to 16 bytes. Half the bytes of an fp32 O, for the
+// merge to read (it multiplies each record by its l and the softmax correction).
+constexpr int PH = HD / 2 + 4;
 
 /// One 32-key tile's raw bytes for a lane.
 struct Tile8 {
@@ -107,10 +111,10 @@ __device__ __forceinline__ void decode_append(const DecodeAppend& app, const uin
         x1 = h2f((uint16_t)(qr >> 16));
     }
     const float dot = wave_sum_bfly(x0 * (float)nk[2 * lane] + x1 * (float)nk[2 * lane + 1]);
-    float* pp = part + ((size_t)C * n_kv * GQ + hq) * PS;
-    pp[2 * lane] = nsc[1] * (float)nv[2 * lane] * WSCALE;
-    pp[2 * lane + 1] = nsc[1] * (float)nv[2 * lane + 1] * WSCALE;
-    if (lane == 0) { pp[HD] = dot * nsc[0] * sc; pp[HD + 1] = 1.0f; }
+    float* pp = part + ((size_t)C * n_kv * GQ + hq) * PH;   // weight 1: O / l is the dequantised row
+    *(uint32_t*)((uint16_t*)pp + 2 * lane) =
+        (uint32_t)f2h(nsc[1] * (float)nv[2 * lane]) | ((uint32_t)f2h(nsc[1] * (float)nv[2 * lane + 1]) << 16);
+    if (lane == 0) { pp[HD / 2] = dot * nsc[0] * sc; pp[HD / 2 + 1] = 1.0f; }
 }
 
 template <int GQ, bool RELU2, bool SCALE32, bool OBF, bool SCORES, bool QR, bool APP>
@@ -450,10 +454,12 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
         for (int e = 0; e < PER; e++) o[(size_t)hq * HD + od + e] = f2a<OBF>(acc[e] * rr);
         return;
     }
-    float* pp = part + ((size_t)c * n_kv * GQ + hq) * PS;
-#pragma unroll
-    for (int e = 0; e < PER; e++) pp[od + e] = acc[e];
-    if (od == 0) { pp[HD] = M; pp[HD + 1] = L; }
+    float* pp = part + ((size_t)c * n_kv * GQ + hq) * PH;
+    const float il = L > 0.0f ? 1.0f / (WSCALE * L) : 0.0f;   // ReLU²: every weight of a chunk may be 0
+    uint16_t* p16 = (uint16_t*)pp + od;
+    if constexpr (PER == 2) *(uint32_t*)p16 = (uint32_t)f2h(acc[0] * il) | ((uint32_t)f2h(acc[1] * il) << 16);
+    else p16[0] = f2h(acc[0] * il);
+    if (od == 0) { pp[HD / 2] = M; pp[HD / 2 + 1] = L; }
 }
 
 /// Merges the C chunk partials of query head blockIdx.x, dims 32 * blockIdx.y .. + 31: thread
@@ -463,9 +469,12 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
 #endif
 constexpr int MDPW = MERGE_DPW;   // dims a merge workgroup
 
-template <bool RELU2, bool OBF>
+/// Records: fp32 (H16 false: acc[128], m, l, pad: the sparse, ring and 16-bit cache decodes) or
+/// the int8 decode's PH-float records (O / l as fp16, then m, l).
+template <bool RELU2, bool OBF, bool H16>
 __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ part, uint16_t* __restrict__ o,
                                                            int C, int n_q, float sink, float oscale) {
+    constexpr int RS = H16 ? PH : HD + 4;   // floats a record
     // thread (slice sl of 4 dims, chunk group r); the chunk groups of a wave reduce by shuffles, the
     // 4 waves through LDS
     constexpr int SLC = MDPW / 4, NR = 256 / SLC, MAXK = 256 / NR;   // C <= 256
@@ -478,9 +487,14 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
     for (int k = 0; k < MAXK; k++) {
         const int cc = r + NR * k;
         if (cc < C) {
-            const float* p = part + ((size_t)cc * n_q + h) * PS;
-            v[k] = ld16(p + d);
-            const u2_t ml = ld8(p + HD);
+            const float* p = part + ((size_t)cc * n_q + h) * RS;
+            if constexpr (H16) {
+                const u2_t x = ld8((const uint16_t*)p + d);
+                v[k] = (u4_t){x[0], x[1], 0, 0};
+            } else {
+                v[k] = ld16(p + d);
+            }
+            const u2_t ml = ld8(p + (H16 ? HD / 2 : HD));
             mk[k] = __uint_as_float(ml[0]);
             lk[k] = __uint_as_float(ml[1]);
         }
@@ -505,8 +519,14 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
         if (r + NR * k < C) {
             const float f = RELU2 ? 1.0f : (mk[k] == NEG_INF ? 0.0f : exp2f(mk[k] - M));
             Lr += lk[k] * f;
+            if constexpr (H16) {   // O / l: the record's share is its l times the correction
+                const float fl = f * lk[k];
 #pragma unroll
-            for (int i = 0; i < 4; i++) A[i] += __uint_as_float(v[k][i]) * f;
+                for (int i = 0; i < 4; i++) A[i] += h2f((uint16_t)(v[k][i / 2] >> (16 * (i & 1)))) * fl;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++) A[i] += __uint_as_float(v[k][i]) * f;
+            }
         }
     }
 #pragma unroll
@@ -543,7 +563,7 @@ int launch_full_decode(const FullDecodeArgs& a, hipStream_t st) {
         hipLaunchKernelGGL((full_decode_kernel<4, false, false, true, false, true, true>), dim3((a.C + 1) * a.n_kv),
                            block, 0, st, a.q, a.kc,
                            a.vc, a.part, a.scores, a.o, a.S, a.CH, a.C, a.max_s, a.n_kv, qs, sink, a.g1, a.g2, a.ng, app);
-        return launch_decode_merge(a.part, a.o, a.C + 1, a.n_q, false, true, WSCALE, st);
+        return launch_decode_merge(a.part, a.o, a.C + 1, a.n_q, false, true, 1.0f, st, true);
     }
     if (a.ng >= 0) {   // raw queries: the reference's full and sparse layers, and the decode step
         if (gq == 8 && a.relu2 && a.scale32 && a.out_bf16 && !a.scores) EMBLA_FDR(8, true, true, true, false);
@@ -561,22 +581,28 @@ int launch_full_decode(const FullDecodeArgs& a, hipStream_t st) {
     else return EMBLA_ERR_UNSUPPORTED;
 #undef EMBLA_FD
 #undef EMBLA_FDR
-    if (a.C > 1 && a.merge) return launch_decode_merge(a.part, a.o, a.C, a.n_q, a.relu2, a.out_bf16, WSCALE, st);
+    if (a.C > 1 && a.merge) return launch_decode_merge(a.part, a.o, a.C, a.n_q, a.relu2, a.out_bf16, 1.0f, st, true);
     return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
 }
 
 int launch_full_decode_merge(const FullDecodeArgs& a, hipStream_t st) {
-    return launch_decode_merge(a.part, a.o, a.C, a.n_q, a.relu2, a.out_bf16, WSCALE, st);
+    return launch_decode_merge(a.part, a.o, a.C, a.n_q, a.relu2, a.out_bf16, 1.0f, st, true);
 }
 
 int launch_decode_merge(const float* part, uint16_t* o, int C, int n_q, bool relu2, bool out_bf16, float oscale,
-                        hipStream_t st) {
+                        hipStream_t st, bool h16) {
     const dim3 mg(n_q, HD / MDPW), block(256);
     const float sink = 11.313708498984761f;   // sqrt(128)
-    if (relu2 && out_bf16) hipLaunchKernelGGL((decode_merge_kernel<true, true>), mg, block, 0, st, part, o, C, n_q, sink, oscale);
-    else if (!relu2 && out_bf16) hipLaunchKernelGGL((decode_merge_kernel<false, true>), mg, block, 0, st, part, o, C, n_q, sink, oscale);
-    else if (!relu2) hipLaunchKernelGGL((decode_merge_kernel<false, false>), mg, block, 0, st, part, o, C, n_q, sink, oscale);
+#define EMBLA_MG(R, B)                                                                                               \
+    do {                                                                                                             \
+        if (h16) hipLaunchKernelGGL((decode_merge_kernel<R, B, true>), mg, block, 0, st, part, o, C, n_q, sink, oscale); \
+        else hipLaunchKernelGGL((decode_merge_kernel<R, B, false>), mg, block, 0, st, part, o, C, n_q, sink, oscale);    \
+    } while (0)
+    if (relu2 && out_bf16) EMBLA_MG(true, true);
+    else if (!relu2 && out_bf16) EMBLA_MG(false, true);
+    else if (!relu2) EMBLA_MG(false, false);
     else return EMBLA_ERR_UNSUPPORTED;
+#undef EMBLA_MG
     return hipGetLastError() == hipSuccess ? EMBLA_OK : EMBLA_ERR_HIP;
 }
 

@@ -47,9 +47,10 @@ struct DecodeAppend {
 };
 /// The merge launch_full_decode ends with, on its own (a.C > 1, partials in a.part).
 int launch_full_decode_merge(const FullDecodeArgs& a, hipStream_t st);
-/// Merges C chunk partials [C][n_q][132] into o [n_q][128]; the partials' sums carry a factor oscale.
+/// Merges C chunk partials into o [n_q][128]: fp32 records [C][n_q][132] whose sums carry a factor
+/// oscale, or (h16) the int8 decode's records [C][n_q][68] (O / l as fp16, then m and l).
 int launch_decode_merge(const float* part, uint16_t* o, int C, int n_q, bool relu2, bool out_bf16, float oscale,
-                        hipStream_t st);
+                        hipStream_t st, bool h16 = false);
 
 struct RingArgs {
     const uint16_t* q;       // head h's row at q + h * q_stride
