@@ -618,7 +618,22 @@ int embla_prefill_int8(const void* q, int q_dtype, long q_tok_stride, long q_hea
     a.kring = nullptr; a.vring = nullptr; a.R = 0; a.qg = nullptr;
     a.relu2 = weights == EMBLA_RELU2_SINK; a.scale32 = scale_dtype == EMBLA_F32;
     a.q_bf16 = q_dtype == EMBLA_BF16; a.out_bf16 = o_dtype == EMBLA_BF16;
+    // a workspace large enough for the staged copy: the region's keys are converted to fp16 once
+    // (prestage_kernel) instead of once a workgroup, for the instances that have a staged form
+    const size_t staged = embla_prefill_staged_workspace_bytes(T, p0, n_q, n_kv);
+    if (ws && staged && ws_bytes >= staged && window == 0 && !a.relu2 && !a.scale32 && a.q_bf16 && a.out_bf16 &&
+        n_q == 4 * n_kv) {
+        const int R = (p0 + T + 127) / 128 * 128;
+        uint16_t* k16 = (uint16_t*)((char*)ws + round_up(embla_prefill_workspace_bytes(T, n_q), 256));
+        return launch_prefill_prestaged(a, k16, k16 + (size_t)n_kv * R * 128, R, stream);
+    }
     return launch_prefill_int8(a, stream);
+}
+
+size_t embla_prefill_staged_workspace_bytes(int T, int p0, int n_q, int n_kv) {
+    if (T <= 0 || p0 < 0 || n_q <= 0 || n_kv <= 0) return 0;
+    const size_t R = (size_t)(p0 + T + 127) / 128 * 128;
+    return round_up(embla_prefill_workspace_bytes(T, n_q), 256) + 2 * (size_t)n_kv * R * 128 * 2;
 }
 
 int embla_prefill_full(const void* q, const void* k, const void* v, void* kc, void* vc, void* o, int T, int p0,

@@ -164,6 +164,9 @@ struct PrefillArgs {
 };
 int launch_prefill_int8(const PrefillArgs& a, hipStream_t st);
 int launch_prefill_ring(const PrefillArgs& a, hipStream_t st);
+/// Prefill over the int8 region a.kc / a.vc through its staged fp16 copy k16, v16 ([n_kv][R] tiles
+/// of 16-bit elements, R a multiple of 128 >= p0 + T): the staging pass, then the attention.
+int launch_prefill_prestaged(const PrefillArgs& a, uint16_t* k16, uint16_t* v16, int R, hipStream_t st);
 
 int launch_index_scores(const uint16_t* qi, const float* w, const uint16_t* ki, float* scores, int n, int n_ih,
                         hipStream_t st, uint32_t* sw = nullptr);

@@ -58,6 +58,12 @@ struct __attribute__((aligned(16))) PrefillSmem {
 // (fp16 rings) or widened to fp16 in staging (bf16 rings, bf8_to_h8: exact for |v| in
 // [2^-14, 65504]). So the fp16 record loses no range that the product keeps.
 constexpr int PPH = 68;
+#ifndef PF_PRIO
+// wave priority raised over the score chains (1), the P·V products (2): with two waves a SIMD
+// entering each tile together, the raised one issues its chain first and the two drift into
+// alternating MFMA and softmax phases (C5 full: 0.561 -> 0.555 ms with 1, 0.580 with 2, 0.570 with 3)
+#define PF_PRIO 1
+#endif
 constexpr int PF_WAVES = 8;        // waves a workgroup: GQ query heads x (8 / GQ) 32-row blocks
 #ifndef PF_XCD
 #define PF_XCD 1                   // workgroups of one (kv head, split) spread over one XCD
@@ -93,8 +99,11 @@ __device__ __forceinline__ h8_t i8x8_scaled(uint32_t a, uint32_t b, h2_t s01, h2
 // RING: K/V from a 16-bit ring (no scales; S = K·Q^T on the MFMA in the ring's type, BF = bf16;
 // V staged as fp16); else from an int8 region (fp16 MFMA), each key's K scale (with 1/√128, and
 // log2 e for softmax) and V scale multiplied into its staged fp16 row. PRE: q normed with gains,
-// rotated, bf16-rounded in-kernel.
-template <int GQ, bool RELU2, bool SCALE32, bool QBF, bool OBF, bool RING = false, bool BF = false, bool PRE = false>
+// rotated, bf16-rounded in-kernel. LIN (with RING): the "ring" is an int8 region staged to fp16 by
+// prestage_kernel (slots = positions, no wrap; K rows already carry their scale and the score
+// scale, V rows their scale), which the int8 path would otherwise convert in every workgroup.
+template <int GQ, bool RELU2, bool SCALE32, bool QBF, bool OBF, bool RING = false, bool BF = false, bool PRE = false,
+          bool LIN = false>
 __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillArgs a) {
     constexpr int NT = 64 * PF_WAVES;
     constexpr int RB = PF_WAVES / GQ;                       // 32-row blocks a workgroup
@@ -103,7 +112,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
     // picks the (kv head, split), so that each XCD streams as few key ranges as possible and its L2
     // holds them (C5 full: -2%); a ring's windows differ from row block to row block (no gain)
     int tb = blockIdx.x, kvh = blockIdx.y, zz = blockIdx.z;
-    if constexpr (PF_XCD && !RING) {
+    if constexpr (PF_XCD && (!RING || LIN)) {
         const int nc = gridDim.y * gridDim.z;
         const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
         const int combo = lin % nc;
@@ -131,6 +140,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
 
     // score scale: folded into the staged K rows for int8, applied to S for a ring
     const float c = RELU2 ? 0.08838834764831845f : 0.08838834764831845f * 1.4426950408889634f;
+    const float cr = LIN ? 1.0f : c;   // the scale a ring's scores still need
     const size_t nrow = (size_t)a.n_kv * a.max_s * HD;
     const char* ksb = (const char*)(a.kc + nrow);
     const char* vsb = (const char*)(a.vc + nrow);
@@ -161,7 +171,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
         for (int i = 0; i < PER; i++) {
             const int qw = 64 * w + NT * i, gt = qw / (256 * EB), jl = qw % (256 * EB) + lane;
             if constexpr (RING) {
-                const size_t off = tile_base(kvh, a.R, (k0 + 32 * gt) % a.R, 2) + (size_t)jl * 16;
+                const size_t off = tile_base(kvh, a.R, LIN ? k0 + 32 * gt : (k0 + 32 * gt) % a.R, 2) + (size_t)jl * 16;
                 kr[i] = ld16((const char*)a.kring + off);
                 vr[i] = ld16((const char*)a.vring + off);
                 // V piece (row jl / 64, slot l = jl % 64): keys 16 (e / 4) + 4 (l / 16) + e % 4 of
@@ -308,7 +318,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
 #pragma unroll
                 for (int i = 0; i < 4; i++)
                     qb[s][i] = (uint32_t)f2bf(x[8 * s + 2 * i]) | ((uint32_t)f2bf(x[8 * s + 2 * i + 1]) << 16);
-        } else if constexpr (!RING && QBF) {
+        } else if constexpr ((!RING || LIN) && QBF) {
 #pragma unroll
             for (int s = 0; s < 8; s++) qb[s] = __builtin_bit_cast(u4_t, bf8_to_h8(qb[s]));
         }
@@ -355,6 +365,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
         // {8s + 4h + i, 16 + 8s + 4h + i} are the P^T items b = s and b = 2 + s
         auto pv = [&](int kb, const u4_t* pb) {
             const u4_t* vt = (const u4_t*)(sm.vt[b] + kb * VTILE);
+            if (PF_PRIO & 2) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int s = 0; s < 2; s++)
 #pragma unroll
@@ -362,11 +373,13 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
                     const int dim = 32 * i + r;
                     O[i] = mfma32x<false>(vt[(dim & 7) * (VUROW / 8) + (dim >> 3) + 16 * (2 * s + h)], pb[s], O[i]);
                 }
+            if (PF_PRIO & 2) __builtin_amdgcn_s_setprio(0);
         };
         // two 32-key blocks kb0, kb0 + 1 of the staged tile: one max and rescale decision
         auto pair = [&](int kb0) {
             // the two blocks' score chains interleaved (one chain's MFMA under the other's latency)
             f16_t s0, s1;
+            if (PF_PRIO & 1) __builtin_amdgcn_s_setprio(1);
             {
                 const u4_t* k0r = (const u4_t*)(sm.k[b] + (32 * kb0 + r) * KROW) + h;
                 const u4_t* k1r = k0r + 32 * KROW / 8;
@@ -378,13 +391,14 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
                     s1 = mfma32x<BF>(k1r[2 * s], qb[s], s1);
                 }
             }
+            if (PF_PRIO & 1) __builtin_amdgcn_s_setprio(0);
             // scores of the tile's 64 keys: item e of block kb is x[16 kb + e]
             float x[32];
             // a ring's scores are unscaled (x c): ReLU² scales them here, softmax in the exponent
 #pragma unroll
             for (int e = 0; e < 16; e++) {
-                x[e] = RING && RELU2 ? s0[e] * c : s0[e];
-                x[16 + e] = RING && RELU2 ? s1[e] * c : s1[e];
+                x[e] = RING && RELU2 ? s0[e] * cr : s0[e];
+                x[16 + e] = RING && RELU2 ? s1[e] * cr : s1[e];
             }
             if (!full_tile) {   // uniform: only the diagonal (and window-edge) tiles
 #pragma unroll
@@ -402,7 +416,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
                     ma = vmax3(ma, x[e], x[e + 1]);
                     mb = vmax3(mb, x[16 + e], x[17 + e]);
                 }
-                const float mt = max_xor32(vmax3(vmax3(ma, mb, x[15]), x[31], x[31])) * (RING ? c : 1.0f);
+                const float mt = max_xor32(vmax3(vmax3(ma, mb, x[15]), x[31], x[31])) * (RING ? cr : 1.0f);
                 // the running maximum moves only when a row's grows by more than 2^8: weights stay
                 // <= 256 (fp16-safe), O and l share the stale m
                 if (__any(mt > m + 8.0f)) {
@@ -424,7 +438,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
                     const float t = fmaxf(v, 0.0f);
                     return t * t;
                 } else {
-                    return __builtin_amdgcn_exp2f(RING ? __builtin_fmaf(v, c, -msub) : v - msub);
+                    return __builtin_amdgcn_exp2f(RING && !LIN ? __builtin_fmaf(v, c, -msub) : v - msub);
                 }
             };
             float pw[16];
@@ -596,6 +610,69 @@ int launch_prefill_ring(const PrefillArgs& a, hipStream_t st) {
     else if (!a.q_bf16 && !a.out_bf16 && !a.qg) EMBLA_PR(false, false);
     else return EMBLA_ERR_UNSUPPORTED;
 #undef EMBLA_PR
+    return launch_prefill_tail(a, st);
+}
+
+/// Stages an int8 layer region's keys [0, n) as the 16-bit lane-order tiles the LIN instances
+/// read (R slots a kv head, R a multiple of 128 >= n): a thread a 16-byte int8 piece, written as
+/// two 16-byte fp16 pieces with exactly the products prefill_int8_kernel's own staging forms (K
+/// rows times fp16(scale · c), V rows times their fp16 scales, both in fp16). Keys n .. R - 1 are
+/// staged as zeros (their cache bytes and scales may never have been written).
+template <bool SCALE32>
+__global__ __launch_bounds__(256) void prestage_kernel(const int8_t* __restrict__ kc, const int8_t* __restrict__ vc,
+                                                       uint16_t* __restrict__ k16, uint16_t* __restrict__ v16, int n,
+                                                       int R, int max_s, float c) {
+    const int tile = blockIdx.x, kvh = blockIdx.y, is_v = blockIdx.z;
+    const int t0 = 32 * tile, j = threadIdx.x >> 6, l = threadIdx.x & 63;   // int8 piece (j, l)
+    const int8_t* src = (is_v ? vc : kc);
+    const char* sb = (const char*)(src + (size_t)max_s * HD * gridDim.y) + ((size_t)kvh * max_s + t0) * (SCALE32 ? 4 : 2);
+    const bool live = t0 < n;   // uniform
+    const u4_t r = live ? ld16(src + tile_base(kvh, max_s, t0, 1) + (size_t)(64 * j + l) * 16) : (u4_t){0, 0, 0, 0};
+    auto sc = [&](int k) -> float {   // key t0 + k's scale, 0 past the keys staged
+        if (t0 + k >= n) return 0.0f;
+        return SCALE32 ? ((const float*)sb)[k] : h2f(((const uint16_t*)sb)[k]);
+    };
+    uint16_t* dst = (is_v ? v16 : k16) + tile_base(kvh, R, t0, 2) / 2;
+    h8_t a, b;
+    if (!is_v) {   // K piece: key 16 (j / 2) + l % 16, dims 32 (l / 16) + 16 (j % 2) .. + 15
+        const _Float16 sk = (_Float16)(sc(16 * (j >> 1) + (l & 15)) * c);
+        const h2_t s2 = {sk, sk};
+        a = i8x8_scaled(r[0], r[1], s2, s2, s2, s2);
+        b = i8x8_scaled(r[2], r[3], s2, s2, s2, s2);
+        // 16-bit tile: K load j16 = 4t + p / 16 with p = 2 (d % 32): pieces 2j and 2j + 1
+        *(h8_t*)(dst + (size_t)(64 * (2 * j) + l) * 8) = a;
+        *(h8_t*)(dst + (size_t)(64 * (2 * j + 1) + l) * 8) = b;
+    } else {       // V piece: rows u = 2j, 2j + 1 of slot l, keys {16t + 4 (l / 16) + i}
+        const int g = l >> 4;
+        _Float16 v[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float f = sc(16 * (e >> 2) + 4 * g + (e & 3));
+            v[e] = SCALE32 ? (_Float16)f : (_Float16)f;   // fp16 scales are exact; fp32 ones rounded as the staging does
+        }
+        const h2_t v01 = {v[0], v[1]}, v23 = {v[2], v[3]}, v45 = {v[4], v[5]}, v67 = {v[6], v[7]};
+        a = i8x8_scaled(r[0], r[1], v01, v23, v45, v67);
+        b = i8x8_scaled(r[2], r[3], v01, v23, v45, v67);
+        // 16-bit tile: V load j16 = u
+        *(h8_t*)(dst + (size_t)(64 * (2 * j) + l) * 8) = a;
+        *(h8_t*)(dst + (size_t)(64 * (2 * j + 1) + l) * 8) = b;
+    }
+}
+
+/// Prefill over an int8 region through a staged fp16 copy (workspace k16, v16: n_kv * R * 128
+/// elements each): the staging pass, then the LIN instance.
+int launch_prefill_prestaged(const PrefillArgs& a0, uint16_t* k16, uint16_t* v16, int R, hipStream_t st) {
+    const int gq = a0.n_q / a0.n_kv;
+    const int n = a0.p0 + a0.T;
+    if (!(gq == 4 && !a0.relu2 && !a0.scale32 && a0.q_bf16 && a0.out_bf16) || R % 128 || R < n) return EMBLA_ERR_UNSUPPORTED;
+    const float c = 0.08838834764831845f * 1.4426950408889634f;
+    hipLaunchKernelGGL((prestage_kernel<false>), dim3(R / 32, a0.n_kv, 2), dim3(256), 0, st, a0.kc, a0.vc, k16, v16, n, R,
+                       a0.max_s, c);
+    PrefillArgs a = a0;
+    a.kring = k16; a.vring = v16; a.R = R;
+    const dim3 grid((a.T + 32 * (PF_WAVES / gq) - 1) / (32 * (PF_WAVES / gq)), a.n_kv, a.nsplit);
+    hipLaunchKernelGGL((prefill_int8_kernel<4, false, false, true, true, true, false, false, true>), grid,
+                       dim3(64 * PF_WAVES), 0, st, a);
     return launch_prefill_tail(a, st);
 }
 

@@ -63,6 +63,7 @@ SIGNATURES = {
     "embla_prefill_int8": (i32, [vp, i32, C.c_long, C.c_long, vp, vp, vp, i32, C.c_long, C.c_long, i32, i32, i32, i32,
                                  i32, i32, i32, i32, vp, sz, vp]),
     "embla_prefill_workspace_bytes": (sz, [i32, i32]),
+    "embla_prefill_staged_workspace_bytes": (sz, [i32, i32, i32, i32]),
     "embla_prefill_full": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp, sz, vp]),
     "embla_relu2_prefill": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
     "embla_attn_sparse8": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]),

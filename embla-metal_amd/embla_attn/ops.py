@@ -273,8 +273,12 @@ def sparse_layer_decode(q, qi, w, ki, kc, vc, S, max_s, n_kv, ws: SparseWorkspac
 
 
 class PrefillWorkspace:
-    def __init__(self, T: int, n_q: int = 16, device="cuda"):
-        self.nbytes = int(lib().embla_prefill_workspace_bytes(T, n_q))
+    def __init__(self, T: int, n_q: int = 16, device="cuda", staged_p0=None, n_kv: int = 4):
+        """staged_p0: also room for the staged fp16 copy of keys 0 .. staged_p0 + T - 1."""
+        if staged_p0 is None:
+            self.nbytes = int(lib().embla_prefill_workspace_bytes(T, n_q))
+        else:
+            self.nbytes = int(lib().embla_prefill_staged_workspace_bytes(T, staged_p0, n_q, n_kv))
         self.buf = torch.empty(self.nbytes, dtype=torch.uint8, device=device)
 
     @property

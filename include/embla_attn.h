@@ -199,6 +199,13 @@ int embla_prefill_int8(const void* q, int q_dtype, long q_tok_stride, long q_hea
 /* Bytes of the optional prefill workspace for T tokens and n_q query heads. */
 size_t embla_prefill_workspace_bytes(int T, int n_q);
 
+/* Bytes of a prefill workspace that also holds an fp16 copy of the layer's keys 0 .. p0+T-1 (no
+ * counterpart in the reference, whose threadgroups each widen the int8 rows they stage,
+ * attn_nax.metal:26-56): embla_prefill_int8 / embla_prefill_full given at least this much convert
+ * the region once into it, bit-identical products, and attend over the copy (softmax, fp16
+ * scales, bf16 q and out, n_q = 4 n_kv, no window; other calls ignore the extra bytes). */
+size_t embla_prefill_staged_workspace_bytes(int T, int p0, int n_q, int n_kv);
+
 /* Full-layer prefill chunk (config C5 full): the chunk's bf16 K and V [T][n_kv][128] quantised into
  * the int8 cache (fp16 per-token absmax scales) at p0 .., then causal softmax attention of the bf16
  * queries [T][n_q][128] over keys 0 .. p0 + t; o bf16 [T][n_q][128]; ws as embla_prefill_int8. */

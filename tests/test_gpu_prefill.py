@@ -162,3 +162,33 @@ def test_q_prep_b_head_major(torch_gpu, orc):
         for h in range(16):
             want = orc.head_norm(synth.bf16_val(qkv[t, h * 128:(h + 1) * 128]), synth.bf16_val(g1), synth.bf16_val(g2), 2)
             np.testing.assert_array_equal(got[h, t], want, err_msg=f"t={t} h={h}")
+
+
+@pytest.mark.parametrize("p0,T", [(0, 100), (1000, 96), (2100, 64), (2500, 1), (30720, 2048)])
+def test_prefill_staged_copy_bit_identical(torch_gpu, orc, p0, T):
+    """With a workspace that holds the staged fp16 copy, the region is converted once
+    (prestage_kernel) and attended through the 16-bit tile path: the products are the ones each
+    workgroup's own staging forms, so the output is bit for bit the unstaged path's; positions
+    past p0 + T (never written: NaN scales) stay out of it."""
+    from embla_attn import ops
+    torch = torch_gpu
+    say(f"prefill staged copy p0={p0} T={T}")
+    c = synth.prefill_case(seed=5, p0=p0, T=T)
+    max_s = ((p0 + T + 127) // 128) * 128 + 32
+    kc, vc = upload_prefix(c, max_s)
+    nrow = 4 * max_s * 128
+    for t in (kc, vc):   # the positions after the chunk: random bytes, NaN scales
+        t.view(torch.uint8)[nrow:].view(torch.float16)[torch.arange(4, device="cuda")[:, None] * max_s +
+                                                         torch.arange(p0 + T, max_s, device="cuda")] = float("nan")
+    q = dev(c["q"], torch.bfloat16)
+    ops.kv_quant_append(dev(c["kn"], torch.bfloat16), dev(c["vn"], torch.bfloat16), T, p0, 4, kc, vc, max_s)
+    plain = ops.prefill_int8(q, kc, vc, T, p0, max_s, 4, ws=ops.PrefillWorkspace(T, 16))
+    wss = ops.PrefillWorkspace(T, 16, staged_p0=p0)
+    wss.buf.fill_(0xFF)   # NaN fp16 everywhere the staging does not write
+    staged = ops.prefill_int8(q, kc, vc, T, p0, max_s, 4, ws=wss)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(staged.view(torch.int16).cpu().numpy(), plain.view(torch.int16).cpu().numpy())
+    if T <= 100:
+        K, ks, V, vs = cache_after_chunk(orc, c)
+        ref = orc.prefill_int8(synth.bf16_val(c["q"]), K, ks, V, vs, p0, weights=0)
+        assert_close(bf16_host(staged), ref, what=f"staged p0={p0} T={T}")
