@@ -130,6 +130,36 @@ def bench_c3(torch, steps, warmup, n_layers=16, contexts=(4096, 16384, 32768)):
     return res, case, outs[0], regions, main_us
 
 
+def bench_c3_single(torch, regions, case, L=32768, reps=30):
+    """One C3 layer call alone (split-K pass + merge, captured as a one-layer graph), each replay
+    after a 512 MB fill that evicts the L2s and the MALL, so its 34 MB come from HBM with nothing
+    before or after it in the graph: the isolated cold-cache layer time (median of `reps`)."""
+    from embla_attn import ops
+    q = torch.from_numpy(case["q"]).cuda().view(torch.float16)
+    ws = ops.Workspace(L, 16)
+    out = torch.empty((16, 128), dtype=torch.float16, device="cuda")
+    big = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+    kc, vc = regions[0]
+    ops.decode_int8(q, kc, vc, L, L, 4, ws=ws, out=out)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.decode_int8(q, kc, vc, L, L, 4, ws=ws, out=out)
+    times = []
+    for _ in range(reps):
+        big.zero_()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) * 1000)
+    times.sort()
+    us = times[len(times) // 2]
+    return dict(us_cold_median=us, us_cold_min=times[0], gbs=layer_bytes(L) / (us * 1e-6) / 1e9,
+                tokens_per_s=1e6 / us, reps=reps)
+
+
 def bench_read_floor(torch, n_layers=16, max_s=32768, n_kv=4, reps=20):
     """The practical floor of one decode layer's split-K pass: a plain streaming read of the same
     bytes (K and V rows + fp16 scales of 32768 keys, 34,078,720 B) in one launch, 16 distinct
@@ -488,9 +518,10 @@ def cpu_baseline(case, L, budget_s=6.0):
     """The oracle's C restatement of the reference's math (oracle/oracle.c) built at -O3
     -march=native with OpenMP (liborc_omp.so: threads over query heads, prefill rows and index
     keys; the same results as the checker build), timed on this host's cores: C3 whole layers at
-    context L (GB/s, the headline's unit), plus C4 (one sparse-layer step: index scores, top-k,
-    attention over the 1152 rows) and C5 full (a 64-row sample of the 2048-row chunk, scaled to
-    TFLOP/s). The reference itself has no CPU attention path (all of it is Metal)."""
+    context L (GB/s, the headline's unit), plus C2 (decode steps over the 1024-position window),
+    C4 (one sparse-layer step: index scores, top-k, attention over the 1152 rows) and C5 full,
+    sliding and sparse (samples of the 2048-row chunk, scaled to TFLOP/s). The reference itself
+    has no CPU attention path (all of it is Metal)."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import numpy as np
     import orc
@@ -527,6 +558,38 @@ def cpu_baseline(case, L, budget_s=6.0):
     def c5_rows():
         return orc.prefill_int8(qf, Kc, ksc, Vc, vsc, p0 + r0)
     dt5, n5, _ = _timed(c5_rows, budget_s / 2, min_n=1, max_n=5)
+    # C2: decode steps over a window of 1024 positions of an fp16 ring (the values of an N(0,1)
+    # fp16 history; the oracle attends positions pos - 1023 .. pos)
+    g = np.random.default_rng(1)
+    Kr = g.standard_normal((4, 8192, 128)).astype(np.float16).astype(np.float32)
+    Vr = g.standard_normal((4, 8192, 128)).astype(np.float16).astype(np.float32)
+    q2 = g.standard_normal((16, 128)).astype(np.float16).astype(np.float32)
+    win = np.arange(8192 - 1024, 8192, dtype=np.int32)
+    dt2, n2, _ = _timed(lambda: orc.decode_rows(q2, Kr, Vr, win), budget_s / 4)
+    # C5 sliding: a 64-row sample of the chunk, each row over its 1024-position window (scaled
+    # to TFLOP/s by the rows' pair count)
+    qs5 = g.standard_normal((nr, 16, 128)).astype(np.float16).astype(np.float32)
+
+    def c5_sliding_rows():
+        for i in range(nr):
+            orc.decode_rows(qs5[i], Kr, Vr, win)
+    dt6, n6, _ = _timed(c5_sliding_rows, budget_s / 4, min_n=1, max_n=400)
+    sl_flops = float(nr * 1024 * 16 * 512)
+    # C5 sparse: 4 rows of the chunk at positions near its end, each its own index scores over
+    # ~32K keys, select_keys, attention over its 1152 rows (int8 cache, fp16 scales)
+    ki5 = g.standard_normal((p0 + T, 64)).astype(np.float16).view(np.uint16)
+    qi5 = g.standard_normal((4, 4, 64)).astype(np.float16).view(np.uint16)
+    wi5 = g.random((4, 4)).astype(np.float32)
+    q5s = synth.bf16_val(c5["q"][T - 4:T])
+
+    def c5_sparse_rows():
+        for i in range(4):
+            S = p0 + T - 4 + i + 1
+            sc = orc.index_scores(qi5[i], wi5[i], ki5[:S - 128])
+            sel = orc.select_keys(np.concatenate([sc, np.zeros(128, np.float32)]), S)
+            orc.prefill_int8(q5s[i:i + 1], Kc, ksc, Vc, vsc, S - 1, rows_sel=sel[None])
+    dt7, n7, _ = _timed(c5_sparse_rows, budget_s / 4, min_n=1, max_n=400)
+    sp_flops = float(sum(4 * 128 * (p0 + T - 4 + i + 1 - 128) + 4 * 128 * 16 * 1152 for i in range(4)))
     orc.use_openmp(False)
     cores = os.cpu_count()
     base = dict(cores=threads, host_cpus=cores, kind="port", build="oracle/oracle.c, gcc -O3 -march=native -fopenmp")
@@ -539,6 +602,15 @@ def cpu_baseline(case, L, budget_s=6.0):
         "c5_prefill_full": dict(value=flops_rows / dt5 / 1e12, unit="TFLOP/s",
                                 sample=f"{n5} passes over rows {r0}..{r0 + nr - 1} of the C5 chunk "
                                        f"({flops_rows / 1e9:.2f} GFLOP a pass, {dt5 * 1e3:.0f} ms), threads over rows"),
+        "c2_sliding": dict(value=dt2 * 1e6, unit="us/step", tokens_per_s=1.0 / dt2,
+                           sample=f"{n2} C2 decode steps (16 q / 4 kv heads, window 1024 of an fp16 ring of 8192)"),
+        "c5_prefill_sliding": dict(value=sl_flops / dt6 / 1e12, unit="TFLOP/s", tokens_per_s=nr / dt6,
+                                   sample=f"{n6} passes over {nr} rows of the C5 chunk, each over its 1024-position "
+                                          f"window ({sl_flops / 1e9:.2f} GFLOP a pass, {dt6 * 1e3:.0f} ms)"),
+        "c5_prefill_sparse": dict(value=sp_flops / dt7 / 1e12, unit="TFLOP/s", tokens_per_s=4 / dt7,
+                                  sample=f"{n7} passes over 4 rows at the end of the C5 chunk: index scores over "
+                                         f"their ~32K keys, select_keys, attention over the 1152 rows "
+                                         f"({sp_flops / 1e9:.3f} GFLOP a pass, {dt7 * 1e3:.0f} ms)"),
     }
     c3["more"] = more
     return c3, out
@@ -687,6 +759,7 @@ def main():
                           "steps": args.steps}))
         return
     res, case, out0, regions, main_us = bench_c3(torch, args.steps, args.warmup)
+    single = bench_c3_single(torch, regions, case)
     floor = bench_read_floor(torch)
     step = bench_step(torch, regions)
     step["us_per_layer_append_own_launch"] = bench_step(torch, regions, fused=False)["us_per_layer"]
@@ -717,6 +790,10 @@ def main():
                    "context": L, "layers": 16, "q_heads": 16, "kv_heads": 4, "head_dim": 128,
                    "kv": "int8 + fp16 scales", "graph": True},
         "us_per_layer": round(head["us_per_layer"], 3),
+        # decode throughput of one token: through the 16-layer stack, and through one layer
+        "tokens_per_s": round(1e6 / (16 * head["us_per_layer"]), 1),
+        "tokens_per_s_one_layer": round(1e6 / head["us_per_layer"], 1),
+        "c3_single_layer_cold": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in single.items()},
         # the dominant kernel (the split-K pass over the cache, 16 launches a graph timed by events
         # on the launching stream); the whole layer call (with the merge and the launch gaps) is
         # value / layer_roofline
