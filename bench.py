@@ -668,7 +668,7 @@ def profile_case(torch, name, calls=5):
             t[nrow:].view(torch.float16).uniform_(0.005, 0.02, generator=g)
         q = torch.randn(T, 16, 128, generator=g, device="cuda").bfloat16()
         out = torch.empty(T, 16, 128, dtype=torch.bfloat16, device="cuda")
-        ws = ops.PrefillWorkspace(T, 16)
+        ws = ops.PrefillWorkspace(T, 16, staged_p0=p0)
         for _ in range(calls):
             ops.prefill_int8(q, kc, vc, T, p0, max_s, n_kv, out=out, ws=ws)
     elif name == "gemm_prefill":
