@@ -717,6 +717,66 @@ def profile_case(torch, name, calls=5):
     torch.cuda.synchronize()
 
 
+def render_table(d):
+    """The current-numbers table (markdown) of a bench line: each config's time, throughput and
+    roofline fraction, the floors measured beside them, and the CPU baselines."""
+    r = lambda x, n=2: f"{x:,.{n}f}"
+    c5, sl, sp = d["c5_prefill_full"], d["c5_prefill_sliding"], d["c5_prefill_sparse"]
+    rows = [
+        ("C3 decode, 32K, 16-layer stack (`value`)", f"{r(d['us_per_layer'], 2)} µs/layer",
+         f"{r(d['value'], 0)} GB/s; {r(d['tokens_per_s'], 0)} tokens/s through 16 layers, {r(d['tokens_per_s_one_layer'], 0)} through one",
+         f"{d['layer_roofline']['frac']:.3f} of HBM"),
+        ("C3 split-K kernel (`roofline`)", f"{r(d['roofline']['launch_us'], 2)} µs/launch",
+         f"{r(d['roofline']['achieved'], 0)} GB/s; traffic {d['roofline']['traffic'] / d['roofline']['per_launch_bytes']:.3f}x algorithmic",
+         f"{d['roofline']['frac']:.3f} of HBM"),
+        ("C3 one layer alone, cold caches", f"{r(d['c3_single_layer_cold']['us_cold_median'], 2)} µs",
+         f"{r(d['c3_single_layer_cold']['gbs'], 0)} GB/s", f"{d['c3_single_layer_cold']['gbs'] / HBM_PEAK_GBS:.3f} of HBM"),
+        ("C3 sweep 4K / 16K", f"{r(d['c3_sweep_us_per_layer']['4096'])} / {r(d['c3_sweep_us_per_layer']['16384'])} µs/layer",
+         f"{r(d['c3_sweep_gbs']['4096'], 0)} / {r(d['c3_sweep_gbs']['16384'], 0)} GB/s", "launch-bound at 4K"),
+        ("HBM read floor (probe, one 34 MB launch)", f"{r(d['hbm_read_floor']['us_per_launch'])} µs",
+         f"{r(d['hbm_read_floor']['gbs'], 0)} GB/s; split-K = {d['hbm_read_floor']['split_k_launch_over_floor']:.2f}x it",
+         f"{d['hbm_read_floor']['frac_of_peak']:.3f} of HBM"),
+        ("C2 sliding decode (512 steps, one graph)", f"{r(d['c2_sliding']['us_per_step'])} µs/step",
+         f"{r(d['c2_sliding']['tokens_per_s'], 0)} tokens/s", "latency (2 MB cache-resident)"),
+        ("C4 sparse-layer decode, 32K", f"{r(d['c4_sparse']['us_per_layer'])} µs/layer",
+         f"{r(d['c4_sparse']['tokens_per_s'], 0)} tokens/s", f"{d['c4_sparse']['gbs'] / HBM_PEAK_GBS:.3f} of HBM (latency)"),
+        ("C5 full prefill attention", f"{r(c5['ms_attention'], 3)} ms", f"{r(c5['tflops_attention'], 0)} TFLOP/s; "
+         f"fused with the append {r(c5['ms_fused'], 3)} ms, {r(c5['tokens_per_s'], 0)} tokens/s",
+         f"{c5['mfma_util_attention']:.3f} of bf16 MFMA ({c5['frac_of_sustained_mfma']:.2f} of the MFMA-only probe)"),
+        ("C5 sliding prefill attention", f"{r(sl['ms_attention'], 4)} ms", f"{r(sl['tflops_attention'], 0)} TFLOP/s",
+         f"{sl['mfma_util_attention']:.3f} of bf16 MFMA"),
+        ("C5 sparse prefill layer", f"{r(sp['ms_layer'], 3)} ms", f"{r(sp['tflops_layer'], 0)} TFLOP/s (indexer + attention)",
+         f"{sp['mfma_util_layer']:.3f} of bf16 MFMA (gather-bound)"),
+        ("MFMA-only probe", f"{r(d['mfma_ceiling']['ms'], 3)} ms", f"{r(d['mfma_ceiling']['tflops'], 0)} TFLOP/s",
+         f"{d['mfma_ceiling']['frac_of_peak']:.3f} of bf16 MFMA"),
+        ("decode sub-layer step (q/k/v GEMV, decode with append, o GEMV)",
+         f"{r(d['decode_sublayer_step_graph']['us_per_layer'])} µs/layer", f"{r(d['decode_sublayer_step_graph']['gbs'], 0)} GB/s",
+         f"{d['decode_sublayer_step_graph']['frac_hbm']:.3f} of HBM"),
+        ("4-bit projections, decode (GEMV)", f"{r(d['qkv_o_projections_decode']['us_per_layer'])} µs/layer",
+         f"{r(d['qkv_o_projections_decode']['gbs'], 0)} GB/s", f"{d['qkv_o_projections_decode']['frac_hbm']:.3f} of HBM (launch-bound)"),
+        ("4-bit projections, prefill (GEMM)", f"{r(d['qkv_o_projections_prefill']['ms'], 4)} ms",
+         f"{r(d['qkv_o_projections_prefill']['tflops'], 0)} TFLOP/s", f"{d['qkv_o_projections_prefill']['mfma_util']:.3f} of bf16 MFMA"),
+        ("sampling tail, V = 65536", f"{r(d['sampling_tail']['greedy_us'])} / {r(d['sampling_tail']['draw_candidates_us'])} / "
+         f"{r(d['sampling_tail']['draw_all_tokens_us'])} µs", "greedy / draw (few candidates) / draw (all tokens)", "latency"),
+        ("KV block save + restore (2.13 MB)", f"{r(d['kv_block_save_restore']['us_save_restore'])} µs",
+         f"{r(d['kv_block_save_restore']['gbs'], 0)} GB/s", "launch-bound"),
+    ]
+    out = ["| workload | time | throughput | bound, fraction |", "|---|---:|---|---|"]
+    out += [f"| {a} | {b} | {c} | {e} |" for a, b, c, e in rows]
+    cb = d.get("cpu_baseline")
+    if cb:
+        out += ["", f"CPU baseline (`cpu_baseline`, the C oracle on {cb['cores']} host threads, kind \"{cb['kind']}\"):", "",
+                "| workload | CPU | GPU / CPU |", "|---|---:|---:|",
+                f"| C3 layer | {r(cb['value'], 2)} GB/s | {d['value'] / cb['value']:,.0f}x |"]
+        more, gpu = cb["more"], {"c4_sparse": d["c4_sparse"]["us_per_layer"], "c2_sliding": d["c2_sliding"]["us_per_step"],
+                                 "c5_prefill_full": c5["tflops_attention"], "c5_prefill_sliding": sl["tflops_attention"],
+                                 "c5_prefill_sparse": sp["tflops_layer"]}
+        for k, v in more.items():
+            ratio = v["value"] / gpu[k] if v["unit"].startswith("us") else gpu[k] / v["value"]
+            out.append(f"| {k} | {r(v['value'], 4 if v['unit'] == 'TFLOP/s' else 1)} {v['unit']} | {ratio:,.0f}x |")
+    return "\n".join(out)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -729,9 +789,14 @@ def main():
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only dispatch C3 decode layers and a 64 MB copy (each after a cache-evicting "
                          "fill) for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs; prints nothing else")
+    ap.add_argument("--table", metavar="JSON",
+                    help="print the current-numbers table (markdown) of a saved bench line and exit (no GPU)")
     ap.add_argument("--profile-case", choices=["c5_full", "gemm_prefill", "c5_sparse", "c4"],
                     help="only dispatch one workload's calls (for rocprofv3 --pmc runs); prints nothing")
     args = ap.parse_args()
+    if args.table:
+        print(render_table(json.loads(Path(args.table).read_text().strip().splitlines()[-1])))
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the attention hot path runs on a "
                                    "single MI355X (multi-GPU sharding is design only); run with --gpus 1"}))
