@@ -613,25 +613,21 @@ int launch_prefill_ring(const PrefillArgs& a, hipStream_t st) {
     return launch_prefill_tail(a, st);
 }
 
-/// Stages an int8 layer region's keys [0, n) as the 16-bit lane-order tiles the LIN instances
-/// read (R slots a kv head, R a multiple of 128 >= n): a thread a 16-byte int8 piece, written as
-/// two 16-byte fp16 pieces with exactly the products prefill_int8_kernel's own staging forms (K
-/// rows times fp16(scale · c), V rows times their fp16 scales, both in fp16). Keys n .. R - 1 are
-/// staged as zeros (their cache bytes and scales may never have been written).
-template <bool SCALE32>
+/// Stages an int8 layer region's keys [0, n) (fp16 scales) as the 16-bit lane-order tiles the LIN
+/// instance reads (R slots a kv head, R a multiple of 128 >= n): a thread a 16-byte int8 piece,
+/// written as two 16-byte fp16 pieces with exactly the products prefill_int8_kernel's own staging
+/// forms (K rows times fp16(scale · c), V rows times their fp16 scales, both in fp16). Keys
+/// n .. R - 1 are staged as zeros (their cache bytes and scales may never have been written).
 __global__ __launch_bounds__(256) void prestage_kernel(const int8_t* __restrict__ kc, const int8_t* __restrict__ vc,
                                                        uint16_t* __restrict__ k16, uint16_t* __restrict__ v16, int n,
                                                        int R, int max_s, float c) {
     const int tile = blockIdx.x, kvh = blockIdx.y, is_v = blockIdx.z;
     const int t0 = 32 * tile, j = threadIdx.x >> 6, l = threadIdx.x & 63;   // int8 piece (j, l)
     const int8_t* src = (is_v ? vc : kc);
-    const char* sb = (const char*)(src + (size_t)max_s * HD * gridDim.y) + ((size_t)kvh * max_s + t0) * (SCALE32 ? 4 : 2);
+    const uint16_t* sb = (const uint16_t*)(src + (size_t)max_s * HD * gridDim.y) + (size_t)kvh * max_s + t0;
     const bool live = t0 < n;   // uniform
     const u4_t r = live ? ld16(src + tile_base(kvh, max_s, t0, 1) + (size_t)(64 * j + l) * 16) : (u4_t){0, 0, 0, 0};
-    auto sc = [&](int k) -> float {   // key t0 + k's scale, 0 past the keys staged
-        if (t0 + k >= n) return 0.0f;
-        return SCALE32 ? ((const float*)sb)[k] : h2f(((const uint16_t*)sb)[k]);
-    };
+    auto sc = [&](int k) -> float { return t0 + k < n ? h2f(sb[k]) : 0.0f; };   // 0 past the keys staged
     uint16_t* dst = (is_v ? v16 : k16) + tile_base(kvh, R, t0, 2) / 2;
     h8_t a, b;
     if (!is_v) {   // K piece: key 16 (j / 2) + l % 16, dims 32 (l / 16) + 16 (j % 2) .. + 15
@@ -647,8 +643,7 @@ __global__ __launch_bounds__(256) void prestage_kernel(const int8_t* __restrict_
         _Float16 v[8];
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            const float f = sc(16 * (e >> 2) + 4 * g + (e & 3));
-            v[e] = SCALE32 ? (_Float16)f : (_Float16)f;   // fp16 scales are exact; fp32 ones rounded as the staging does
+            v[e] = (_Float16)sc(16 * (e >> 2) + 4 * g + (e & 3));   // an fp16 scale, exact
         }
         const h2_t v01 = {v[0], v[1]}, v23 = {v[2], v[3]}, v45 = {v[4], v[5]}, v67 = {v[6], v[7]};
         a = i8x8_scaled(r[0], r[1], v01, v23, v45, v67);
@@ -666,7 +661,7 @@ int launch_prefill_prestaged(const PrefillArgs& a0, uint16_t* k16, uint16_t* v16
     const int n = a0.p0 + a0.T;
     if (!(gq == 4 && !a0.relu2 && !a0.scale32 && a0.q_bf16 && a0.out_bf16) || R % 128 || R < n) return EMBLA_ERR_UNSUPPORTED;
     const float c = 0.08838834764831845f * 1.4426950408889634f;
-    hipLaunchKernelGGL((prestage_kernel<false>), dim3(R / 32, a0.n_kv, 2), dim3(256), 0, st, a0.kc, a0.vc, k16, v16, n, R,
+    hipLaunchKernelGGL(prestage_kernel, dim3(R / 32, a0.n_kv, 2), dim3(256), 0, st, a0.kc, a0.vc, k16, v16, n, R,
                        a0.max_s, c);
     PrefillArgs a = a0;
     a.kring = k16; a.vring = v16; a.R = R;
