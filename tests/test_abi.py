@@ -176,3 +176,15 @@ def test_sparse_workspace_recount_word_inside():
         nb, off = L.embla_sparse_workspace_bytes(max_s, n_q), L.embla_sparse_workspace_recount_offset(max_s, n_q)
         assert off % 4 == 0 and 0 < off < nb - 4
     assert L.embla_sparse_workspace_recount_offset(0, 16) == 0
+
+
+def test_prefill_staged_workspace_bytes():
+    """The staged workspace holds the split partials and then fp16 K and V for keys 0 .. p0 + T - 1
+    (rounded up to 128 positions) of every kv head; invalid sizes give 0."""
+    L = _lib.lib()
+    base = L.embla_prefill_workspace_bytes(2048, 16)
+    st = L.embla_prefill_staged_workspace_bytes(2048, 30720, 16, 4)
+    assert st >= base + 2 * 4 * 32768 * 128 * 2
+    assert L.embla_prefill_staged_workspace_bytes(100, 5, 16, 4) >= base
+    assert L.embla_prefill_staged_workspace_bytes(0, 5, 16, 4) == 0
+    assert L.embla_prefill_staged_workspace_bytes(10, -1, 16, 4) == 0
