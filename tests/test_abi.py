@@ -185,6 +185,6 @@ def test_prefill_staged_workspace_bytes():
     base = L.embla_prefill_workspace_bytes(2048, 16)
     st = L.embla_prefill_staged_workspace_bytes(2048, 30720, 16, 4)
     assert st >= base + 2 * 4 * 32768 * 128 * 2
-    assert L.embla_prefill_staged_workspace_bytes(100, 5, 16, 4) >= base
+    assert L.embla_prefill_staged_workspace_bytes(100, 5, 16, 4) >= L.embla_prefill_workspace_bytes(100, 16) + 2 * 4 * 128 * 256
     assert L.embla_prefill_staged_workspace_bytes(0, 5, 16, 4) == 0
     assert L.embla_prefill_staged_workspace_bytes(10, -1, 16, 4) == 0
