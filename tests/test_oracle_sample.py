@@ -105,3 +105,27 @@ def test_mix32_bijective_on_sample(orc):
     xs = np.random.default_rng(1).integers(0, 2**32, 20000, dtype=np.uint64)
     ys = {f(int(x)) for x in xs}
     assert len(ys) == len(set(int(x) for x in xs))
+
+
+def _lowbias32_inverse(y):
+    """The inverse of Wellons' lowbias32 (hash-prospector, 2018), written from its published
+    inverse: undo the xorshifts (x ^= x >> 16 is an involution; x ^= x >> 15 is undone by
+    x ^= x >> 15 ^ x >> 30) and multiply by the published inverses of the two odd constants
+    (0x43021123 = 0x846ca68b^-1, 0x1d69e2a5 = 0x7feb352d^-1 mod 2^32)."""
+    M = 0xFFFFFFFF
+    y ^= y >> 16
+    y = (y * 0x43021123) & M
+    y ^= (y >> 15) ^ (y >> 30)
+    y = (y * 0x1d69e2a5) & M
+    y ^= y >> 16
+    return y
+
+
+def test_mix32_is_lowbias32(orc):
+    """The sampler's hash (misc.metal:186-191) is Wellons' lowbias32; the oracle's restatement
+    inverts exactly under that hash's published inverse, which pins both multipliers (a changed
+    or transposed constant fails) independently of the oracle's own text."""
+    f = orc.lib().orc_mix32
+    xs = np.random.default_rng(2).integers(0, 2**32, 5000, dtype=np.uint64)
+    for x in [0, 1, 2, 0x80000000, 0xFFFFFFFF] + [int(v) for v in xs]:
+        assert _lowbias32_inverse(f(x)) == x, hex(x)
