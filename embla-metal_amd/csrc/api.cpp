@@ -57,6 +57,8 @@ Workspace carve(void* ws, int max_s, int n_q) {
     return w;
 }
 
+/// A tuning override from the environment, or dflt. Call sites keep the value in a static, so the
+/// environment is read once a process, not on every launch.
 int env_int(const char* name, int dflt) {
     const char* s = getenv(name);
     if (!s || !*s) return dflt;
@@ -68,7 +70,7 @@ int env_int(const char* name, int dflt) {
 /// tile for 4 of the 8 waves: short contexts gain from more workgroups), a multiple of 32. The reference's chunks8 makes the same choice for its GPU
 /// (Engine.swift:736-739).
 int decode_chunk(int S, int n_kv) {
-    const int target = env_int("EMBLA_DECODE_WG", 256);
+    static const int target = env_int("EMBLA_DECODE_WG", 256);
     int per_head = target / n_kv > 0 ? target / n_kv : 1;
     if (per_head > kMaxChunks) per_head = kMaxChunks;
     int ch = (S + per_head - 1) / per_head;
@@ -447,7 +449,9 @@ int embla_sliding_decode(const void* q, const void* k_new, const void* v_new, vo
     if (chunk < 0 || chunk % 32) return EMBLA_ERR_INVALID;
     const int lo = pos - window + 1 > 0 ? pos - window + 1 : 0;
     const int span = pos - (lo & ~31);   // ring keys from the first tile on (the current key is extra)
-    const int ch = chunk ? chunk : env_int("EMBLA_SLIDING_CH", 192);   // C2 step: 8.61 us at 192, 8.74 at 256, 8.67-8.82 at 160, 9.48 at 224, 8.77 at 96
+    static const int ch_env = env_int("EMBLA_SLIDING_CH", 192);
+    const int ch = chunk ? chunk : ch_env;   // C2 step: 8.61 us at 192, 8.74 at 256, 8.67-8.82 at 160, 9.48 at 224, 8.77 at 96
+    if (ch <= 0 || ch % 32) return EMBLA_ERR_INVALID;   // (a bad EMBLA_SLIDING_CH)
     int C = (span + ch - 1) / ch;
     if (C < 1) C = 1;
     if (C > kMaxChunks) return EMBLA_ERR_INVALID;
@@ -512,7 +516,8 @@ int sparse_decode_prepare(const void* q, const void* kc, const void* vc, const u
     if (n_kv <= 0 || n_q % n_kv || n_kv > kMaxKV || !valid_act(dtype)) return EMBLA_ERR_INVALID;
     if (n_q / n_kv != 4 && n_q / n_kv != 8) return EMBLA_ERR_UNSUPPORTED;
     if (chunk < 0 || chunk % 32) return EMBLA_ERR_INVALID;
-    int ch = chunk ? chunk : env_int("EMBLA_SPARSE_CH", 64);   // C4 step: 32.0 us at 64, 32.4 at 128, 36.4 at 256
+    static const int ch_env = env_int("EMBLA_SPARSE_CH", 64);
+    int ch = chunk ? chunk : ch_env;   // C4 step: 32.0 us at 64, 32.4 at 128, 36.4 at 256
     if (ch <= 0 || ch % 32) return EMBLA_ERR_INVALID;
     if (fs) {   // the fused select ranks a chunk's rows in LDS: at most kSparseFusedMaxCh of them
         if (ch > kSparseFusedMaxCh) ch = kSparseFusedMaxCh;

@@ -750,9 +750,10 @@ int launch_sparse_rows8(const SparseRows8Args& a, hipStream_t st) {
     const dim3 grid(a.C, a.n_kv, a.R), block(256);
     const int gq = a.n_q / a.n_kv;
 #define EMBLA_SR(GQ, TL, S32) hipLaunchKernelGGL((sparse_rows8_kernel<GQ, TL, S32>), grid, block, 0, st, a)
-    if (gq == 4 && !a.tiles && !a.scale32 && !getenv("EMBLA_SPR_STAGE"))
+    static const bool staged = getenv("EMBLA_SPR_STAGE") != nullptr;   // the LDS-staged variant (tuning)
+    if (gq == 4 && !a.tiles && !a.scale32 && !staged)
         hipLaunchKernelGGL((sparse_rows8_rm_kernel<4>), grid, block, 0, st, a);
-    else if (gq == 8 && !a.tiles && !a.scale32 && !getenv("EMBLA_SPR_STAGE"))
+    else if (gq == 8 && !a.tiles && !a.scale32 && !staged)
         hipLaunchKernelGGL((sparse_rows8_rm_kernel<8>), grid, block, 0, st, a);
     else if (gq == 4 && !a.tiles && !a.scale32) EMBLA_SR(4, false, false);
     else if (gq == 8 && !a.tiles && !a.scale32) EMBLA_SR(8, false, false);
