@@ -164,17 +164,19 @@ def test_q_prep_b_head_major(torch_gpu, orc):
             np.testing.assert_array_equal(got[h, t], want, err_msg=f"t={t} h={h}")
 
 
-@pytest.mark.parametrize("p0,T", [(0, 100), (1000, 96), (2100, 64), (2500, 1), (30720, 2048)])
-def test_prefill_staged_copy_bit_identical(torch_gpu, orc, p0, T):
+@pytest.mark.parametrize("p0,T,tight", [(0, 100, False), (1000, 96, False), (2100, 64, False), (2500, 1, False),
+                                         (100, 100, True), (30720, 2048, False)])
+def test_prefill_staged_copy_bit_identical(torch_gpu, orc, p0, T, tight):
     """With a workspace that holds the staged fp16 copy, the region is converted once
     (prestage_kernel) and attended through the 16-bit tile path: the products are the ones each
     workgroup's own staging forms, so the output is bit for bit the unstaged path's; positions
     past p0 + T (never written: NaN scales) stay out of it."""
     from embla_attn import ops
     torch = torch_gpu
-    say(f"prefill staged copy p0={p0} T={T}")
+    say(f"prefill staged copy p0={p0} T={T} tight={tight}")
     c = synth.prefill_case(seed=5, p0=p0, T=T)
-    max_s = ((p0 + T + 127) // 128) * 128 + 32
+    # tight: max_s the chunk's end rounded to 32 only, below the staged copy's 128-position rounding
+    max_s = ((p0 + T + 31) // 32) * 32 if tight else ((p0 + T + 127) // 128) * 128 + 32
     kc, vc = upload_prefix(c, max_s)
     nrow = 4 * max_s * 128
     for t in (kc, vc):   # the positions after the chunk: random bytes, NaN scales
