@@ -563,6 +563,19 @@ size_t embla_sparse_workspace_recount_offset(int max_s, int n_q) {
            round_up(embla_workspace_bytes(kTopK + kRecent, n_q), 256) + kWideSelectRecounts * 4;
 }
 
+int embla_sparse_workspace_audit(void* ws, size_t ws_bytes, int max_s, int n_q, hipStream_t stream) {
+    if (!ws || max_s <= 0 || n_q <= 0) return EMBLA_ERR_INVALID;
+    if (ws_bytes < embla_sparse_workspace_bytes(max_s, n_q)) return EMBLA_ERR_WORKSPACE;
+    uint32_t* word = (uint32_t*)((char*)ws + embla_sparse_workspace_recount_offset(max_s, n_q));
+    uint32_t n = 0;
+    if (hipMemcpyAsync(&n, word, 4, hipMemcpyDeviceToHost, stream) != hipSuccess) return EMBLA_ERR_HIP;
+    if (hipStreamSynchronize(stream) != hipSuccess) return EMBLA_ERR_HIP;
+    if (n == 0) return EMBLA_OK;
+    if (hipMemsetAsync(word, 0, 4, stream) != hipSuccess || hipStreamSynchronize(stream) != hipSuccess)
+        return EMBLA_ERR_HIP;
+    return EMBLA_ERR_WORKSPACE;
+}
+
 int embla_sparse_layer_decode(const void* q, const void* qi, const float* w, const void* ki, const void* kc,
                               const void* vc, void* o, int S, int max_s, int n_q, int n_kv, int n_ih, int dtype,
                               void* ws, size_t ws_bytes, hipStream_t stream) {

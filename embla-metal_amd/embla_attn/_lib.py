@@ -60,6 +60,7 @@ SIGNATURES = {
     "embla_sparse_decode": (i32, [vp, vp, vp, vp, i32, i32, vp, i32, i32, i32, i32, i32, vp, sz, vp]),
     "embla_sparse_workspace_bytes": (sz, [i32, i32]),
     "embla_sparse_workspace_recount_offset": (sz, [i32, i32]),
+    "embla_sparse_workspace_audit": (i32, [vp, sz, i32, i32, vp]),
     "embla_prefill_int8": (i32, [vp, i32, C.c_long, C.c_long, vp, vp, vp, i32, C.c_long, C.c_long, i32, i32, i32, i32,
                                  i32, i32, i32, i32, vp, sz, vp]),
     "embla_prefill_workspace_bytes": (sz, [i32, i32]),

@@ -241,7 +241,7 @@ def sparse_decode(q, kc, vc, idx, nsel, max_s, n_kv, idx_stride=0, dtype=F16, ch
 
 class SparseWorkspace:
     def __init__(self, max_s: int, n_q: int = 16, device="cuda"):
-        self.max_s = max_s
+        self.max_s, self.n_q = max_s, n_q
         self.nbytes = int(lib().embla_sparse_workspace_bytes(max_s, n_q))
         self.buf = torch.zeros(self.nbytes, dtype=torch.uint8, device=device)
         self.recount_off = int(lib().embla_sparse_workspace_recount_offset(max_s, n_q))
@@ -249,6 +249,11 @@ class SparseWorkspace:
     @property
     def ptr(self):
         return _p(self.buf)
+
+    def audit(self, stream=None) -> int:
+        """embla_sparse_workspace_audit: EMBLA_ERR_WORKSPACE (-4) if a call since the last audit found
+        the workspace not clean, else 0; clears the count."""
+        return int(lib().embla_sparse_workspace_audit(self.ptr, self.nbytes, self.max_s, self.n_q, stream_handle(stream)))
 
     def recounts(self) -> int:
         """Calls that found the select's histogram buffer not clean and recounted it (a device word

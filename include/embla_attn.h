@@ -175,6 +175,11 @@ size_t embla_sparse_workspace_bytes(int max_s, int n_q);
 /* Byte offset, in embla_sparse_layer_decode's workspace, of its count of recounted calls (no
  * counterpart in the reference: it lets a caller audit the workspace's state). */
 size_t embla_sparse_workspace_recount_offset(int max_s, int n_q);
+/* The workspace's audit (no counterpart in the reference): waits for the stream, returns
+ * EMBLA_ERR_WORKSPACE if any call since the last audit found the workspace not clean (its
+ * selection was still exact: the select recounted), EMBLA_OK if none did, and clears the count.
+ * The only entry point that synchronises the host. */
+int embla_sparse_workspace_audit(void* ws, size_t ws_bytes, int max_s, int n_q, hipStream_t stream);
 
 /* One sparse-layer decode step (config C4): with S > 1152 keys, index scores of keys
  * [0, S - 128), the top 1024 plus the latest 128, then attention over those 1152 rows; with

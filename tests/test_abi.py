@@ -188,3 +188,12 @@ def test_prefill_staged_workspace_bytes():
     assert L.embla_prefill_staged_workspace_bytes(100, 5, 16, 4) >= L.embla_prefill_workspace_bytes(100, 16) + 2 * 4 * 128 * 256
     assert L.embla_prefill_staged_workspace_bytes(0, 5, 16, 4) == 0
     assert L.embla_prefill_staged_workspace_bytes(10, -1, 16, 4) == 0
+
+
+def test_sparse_workspace_audit_rejects_bad_arguments():
+    L = _lib.lib()
+    d = C.c_void_p(256)
+    nb = L.embla_sparse_workspace_bytes(32768, 16)
+    assert L.embla_sparse_workspace_audit(None, nb, 32768, 16, None) == _lib.EMBLA_ERR_INVALID
+    assert L.embla_sparse_workspace_audit(d, nb - 1, 32768, 16, None) == _lib.EMBLA_ERR_WORKSPACE
+    assert L.embla_sparse_workspace_audit(d, nb, 0, 16, None) == _lib.EMBLA_ERR_INVALID

@@ -229,6 +229,8 @@ def test_sparse_layer_dirty_workspace_recounts(torch_gpu, orc, c4):
         ref = _c4_ref_selection(orc, c4, S)
         np.testing.assert_array_equal(got, ref, err_msg=f"call {i} S={S}")
         assert ws.recounts() == 1, f"call {i}: recounts {ws.recounts()}"
+    assert ws.audit() == -4   # EMBLA_ERR_WORKSPACE: a call found it not clean; the count is cleared
+    assert ws.recounts() == 0 and ws.audit() == 0
     out = orc.decode_rows(synth.f16_val(c4["q"]), synth.f16_val(c4["K"]), synth.f16_val(c4["V"]), ref.astype(np.int32))
     assert_close(f16_host(o), out, what="dirty workspace")
 
@@ -256,7 +258,7 @@ def test_sparse_layer_rejected_call_leaves_no_state(torch_gpu, orc, c4):
     for S2 in [32768, 9001]:
         ops.sparse_layer_decode(*args, S2, 32768, 4, ws)
         np.testing.assert_array_equal(ws.selection().cpu().numpy().astype(np.uint32), _c4_ref_selection(orc, c4, S2))
-    assert ws.recounts() == 0
+    assert ws.recounts() == 0 and ws.audit() == 0
     # stale counts in both histogram buffers (as if a call had stopped after its scorer)
     # the select's region starts with the two histogram buffers [2][16 copies][256] and then its
     # meta words, the recount word being meta[4]
