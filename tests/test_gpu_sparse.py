@@ -83,7 +83,7 @@ def test_sparse_decode_gathered(torch_gpu, orc, c4, nsel, chunk):
     assert_close(f16_host(o), ref, what=f"nsel={nsel}")
 
 
-@pytest.mark.parametrize("S", [32768, 1000, 1153])
+@pytest.mark.parametrize("S", [32768, 1000, 1151, 1152, 1153, 1154, 32767])
 def test_sparse_layer_end_to_end(torch_gpu, orc, c4, S):
     from embla_attn import ops
     torch = torch_gpu
