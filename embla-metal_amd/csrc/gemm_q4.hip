@@ -40,11 +40,15 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_kernel(GemmArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int n0 = blockIdx.x * QN, m0 = blockIdx.y * QM;
     const int wm = (wv >> 1) * 64, wn = (wv & 1) * (QN / 2);   // the wave's 64 x QN/2 block
-    const int sr = tid >> 1, sc = 32 * (tid & 1);               // X staging: token row, first column
+    // X staging: chunk 256 i + tid is row 32 i + tid / 8, columns 8 (tid % 8) .. +7, so one
+    // wave load reads 8 whole 128-byte row pieces
+    const int sr = tid >> 3, sc = 8 * (tid & 7);
     const int wr_ = tid / TPR, wc = 8 * WPT * (tid % TPR);      // W staging: row, first column
     const char* W = (const char*)a.W;
     const int wpr = a.K / 8, gpr = a.K / 64;
-    const uint16_t* xrow = a.X + (size_t)min(m0 + sr, a.T - 1) * a.ldx + sc;
+    const uint16_t* xr[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) xr[i] = a.X + (size_t)min(m0 + 32 * i + sr, a.T - 1) * a.ldx + sc;
     const size_t wrow = (size_t)min(n0 + wr_, a.O - 1);
 
     // two register stages of staged data: a step's global loads go out two steps before it is
@@ -53,7 +57,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_kernel(GemmArgs a) {
     Stage R0, R1;
     auto load = [&](int k0, Stage& R) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) R.x[i] = ld16(xrow + k0 + 8 * i);
+        for (int i = 0; i < 4; i++) R.x[i] = ld16(xr[i] + k0);
         const uint32_t* wp = (const uint32_t*)(W + a.wo) + wrow * wpr + k0 / 8 + WPT * (tid % TPR);
         if constexpr (WPT == 4) {
             const u4_t v = ld16(wp);
@@ -70,7 +74,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_kernel(GemmArgs a) {
     auto store = [&](int buf, const Stage& R) {
         uint16_t* xd = sm.x[buf] + sr * QROW + sc;
 #pragma unroll
-        for (int i = 0; i < 4; i++) *(u4_t*)(xd + 8 * i) = R.x[i];
+        for (int i = 0; i < 4; i++) *(u4_t*)(xd + 32 * i * QROW) = R.x[i];
         uint16_t* wd = sm.w[buf] + wr_ * QROW + wc;
 #pragma unroll
         for (int j = 0; j < WPT; j++) {   // word j: columns wc + 8 j + q, q = 0..7
