@@ -11,7 +11,9 @@
 // rows' words, scales and biases are requested before x is read. Two columns go through one v_dot2_f32_bf16:
 // the nibbles of columns 8j + k and 8j + k + 4 of word j sit 16 bits apart, so
 // (word >> 4k) & 0x000F000F | 0x43004300 is the bf16 pair (128 + q, 128 + q') exactly (bf16 holds
-// integers to 256), and x is paired the same way once a wave (v_perm_b32). The 128 folds into the
+// integers to 256), and x is paired the same way once a workgroup (v_perm_b32) as it is staged
+// into LDS, with the sums of its 8-column chunks (8.20 -> 7.80 us for the q/k/v + o rows of a
+// decode layer, against pairing once a wave after the loads land). The 128 folds into the
 // group's bias term: sum (s q + b) x = s sum (128 + q) x + (b - 128 s) sum x. The sums are fp32.
 #include "common.hpp"
 #include "embla_internal.hpp"
@@ -49,36 +51,42 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(GemvArgs a) {
                 sc[u][sp] = bf2f(*(const uint16_t*)(W + sg.s + (r * gpr + 32 * sp + lane / 2) * 2));
                 bi[u][sp] = bf2f(*(const uint16_t*)(W + sg.b + (r * gpr + 32 * sp + lane / 2) * 2));
             }
-    // x: the lane's 32 columns of each span as bf16 pairs (8j + k, 8j + k + 4), and their sum
-    uint32_t xp[MAXS][16];
-    float xs[MAXS];
-    // x is read once a workgroup into LDS (its 4 waves' rows share one segment: segment ends are
-    // multiples of 4 rows), after the weights are requested
+    // x: the lane's 32 columns of each span as bf16 pairs (8j + k, 8j + k + 4), and their sum.
+    // Paired once a workgroup, in staging: thread t pairs the 8 columns 8t .. 8t + 7 of each span
+    // and sums them (its 4 waves' rows share one segment: segment ends are multiples of 4 rows),
+    // after the weights are requested; a lane then reads its 4 chunks' pairs and sums.
     const uint16_t* X = (const uint16_t*)a.X + sg.x;
-    __shared__ u4_t xl[MAXS * 256];
-#pragma unroll
-    for (int sp = 0; sp < MAXS; sp++)
-        if (sp < spans) xl[256 * sp + threadIdx.x] = ld16(X + 2048 * sp + 8 * threadIdx.x);
-    __syncthreads();
+    __shared__ u4_t xq[MAXS * 256];
+    __shared__ float xsl[MAXS * 256];
 #pragma unroll
     for (int sp = 0; sp < MAXS; sp++) {
         if (sp < spans) {
-            u4_t v[4];
-#pragma unroll
-            for (int j = 0; j < 4; j++) v[j] = xl[256 * sp + 4 * lane + j];
+            const u4_t v = ld16(X + 2048 * sp + 8 * threadIdx.x);
+            u4_t pr;
             float s = 0.0f;
 #pragma unroll
+            for (int i = 0; i < 4; i++) s += bf2f((uint16_t)(v[i] & 0xFFFF)) + bf2f((uint16_t)(v[i] >> 16));
+#pragma unroll
+            for (int k = 0; k < 4; k++)   // columns 8t + k (dword k / 2), 8t + k + 4 (dword k / 2 + 2), half k % 2
+                pr[k] = __builtin_amdgcn_perm(v[(k >> 1) + 2], v[k >> 1], (k & 1) ? 0x07060302u : 0x05040100u);
+            xq[256 * sp + threadIdx.x] = pr;
+            xsl[256 * sp + threadIdx.x] = s;
+        }
+    }
+    __syncthreads();
+    uint32_t xp[MAXS][16];
+    float xs[MAXS];
+#pragma unroll
+    for (int sp = 0; sp < MAXS; sp++) {
+        if (sp < spans) {
+#pragma unroll
             for (int j = 0; j < 4; j++) {
+                const u4_t pr = xq[256 * sp + 4 * lane + j];
 #pragma unroll
-                for (int i = 0; i < 4; i++) s += bf2f((uint16_t)(v[j][i] & 0xFFFF)) + bf2f((uint16_t)(v[j][i] >> 16));
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    // columns 8j + k (dword k / 2 of v[j]) and 8j + k + 4 (dword k / 2 + 2), half k % 2
-                    const uint32_t lo = v[j][k >> 1], hi = v[j][(k >> 1) + 2];
-                    xp[sp][4 * j + k] = __builtin_amdgcn_perm(hi, lo, (k & 1) ? 0x07060302u : 0x05040100u);
-                }
+                for (int k = 0; k < 4; k++) xp[sp][4 * j + k] = pr[k];
             }
-            xs[sp] = s;
+            const f4_t s4 = *(const f4_t*)&xsl[256 * sp + 4 * lane];
+            xs[sp] = (s4[0] + s4[1]) + (s4[2] + s4[3]);
         }
     }
     float acc[RW];
