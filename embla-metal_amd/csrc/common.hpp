@@ -118,6 +118,30 @@ __device__ __forceinline__ float max_xor32(float v) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return vmax2(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
+/// v and v of lane xor 16 (r[0], r[1] in some order a lane), on v_permlane16_swap: with both
+/// operands v, rows 0 and 2 keep their own values in one output and take rows 1 and 3 in the
+/// other, and the other way round for rows 1 and 3. A commutative op of the pair gives the
+/// shfl_xor result bit for bit, with no LDS round trip.
+__device__ __forceinline__ float max_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+/// The same over lane xor 32 (v_permlane32_swap); fmaxf, as the shfl_xor reductions it replaces.
+__device__ __forceinline__ float fmax_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+/// max / sum over the four 16-lane rows (xor 16, then xor 32)
+__device__ __forceinline__ float max_rows(float v) { return fmax_xor32(max_xor16(v)); }
+__device__ __forceinline__ float sum_rows(float v) { return sum_xor32(sum_xor16(v)); }
 __device__ __forceinline__ float readlane(float v, int l) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }

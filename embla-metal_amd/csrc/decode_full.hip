@@ -25,6 +25,8 @@
 #include "embla_internal.hpp"
 #include "kv_row.hpp"
 
+#include <type_traits>
+
 namespace embla {
 
 typedef int i4_t __attribute__((ext_vector_type(4)));
@@ -207,8 +209,7 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
         }
 #pragma unroll
         for (int d = 0; d < 32; d++) am = fmaxf(am, fabsf(qf[d]));
-        am = fmaxf(am, shfl_xor(am, 16));
-        am = fmaxf(am, shfl_xor(am, 32));
+        am = max_rows(am);
         const float inv = am > 0.0f ? QFIX / am : 0.0f;
         qsc = am / QFIX;
 #pragma unroll
@@ -320,8 +321,7 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
                 x[e] = valid[e] ? x[e] * sc : NEG_INF;
                 mt = fmaxf(mt, x[e]);
             }
-            mt = fmaxf(mt, shfl_xor(mt, 16));
-            mt = fmaxf(mt, shfl_xor(mt, 32));
+            mt = max_rows(mt);
             const float mn = fmaxf(m, mt);
             // rescale only when some head's maximum grew (rare once the maxima settle); nothing to
             // rescale while m is still -inf
@@ -403,8 +403,7 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
     // ---- merge the waves (LDS)
     __shared__ float om[DW][GQ][HD];
     __shared__ float mm[DW][GQ], ll[DW][GQ];
-    l += shfl_xor(l, 16);
-    l += shfl_xor(l, 32);
+    l = sum_rows(l);
     if (g == 0 && n < GQ) { mm[w][n] = m; ll[w][n] = l; }
 #pragma unroll
     for (int u = 0; u < 8; u++)
@@ -469,6 +468,24 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
 #endif
 constexpr int MDPW = MERGE_DPW;   // dims a merge workgroup
 
+/// op over the lanes of the wave with the same lane % G (G = 1, 2, 4 or 8), in every lane: DPP
+/// within 16-lane rows (quad xor 1, xor 2, then row rotations by 4 and 8, which reach every lane
+/// of the row with the same lane % 4 once the quads agree), then the rows by permlane swaps. No
+/// LDS round trips (a shfl_xor chain waits on LDS at each of its 6 - log2 G steps).
+template <int G, bool MAX>
+__device__ __forceinline__ float group_reduce(float v) {
+    auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+    auto dpp = [](float x, auto ctrl) {
+        const int xi = __builtin_bit_cast(int, x);
+        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(xi, xi, decltype(ctrl)::value, 0xF, 0xF, false));
+    };
+    if constexpr (G < 2) v = op(v, dpp(v, std::integral_constant<int, 0xB1>{}));   // quad_perm [1, 0, 3, 2]
+    if constexpr (G < 4) v = op(v, dpp(v, std::integral_constant<int, 0x4E>{}));   // quad_perm [2, 3, 0, 1]
+    if constexpr (G < 8) v = op(v, dpp(v, std::integral_constant<int, 0x124>{}));  // row_ror:4
+    v = op(v, dpp(v, std::integral_constant<int, 0x128>{}));                        // row_ror:8
+    return MAX ? max_rows(v) : sum_rows(v);
+}
+
 /// Records: fp32 (H16 false: acc[128], m, l, pad: the sparse, ring and 16-bit cache decodes) or
 /// the int8 decode's PH-float records (O / l as fp16, then m, l).
 template <bool RELU2, bool OBF, bool H16>
@@ -506,8 +523,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
 #pragma unroll
         for (int k = 0; k < MAXK; k++)
             if (r + NR * k < C) M = fmaxf(M, mk[k]);
-#pragma unroll
-        for (int m = SLC; m < 64; m <<= 1) M = fmaxf(M, shfl_xor(M, m));
+        M = group_reduce<SLC, true>(M);
         if ((tid & 63) == 0) sm[w] = M;
         __syncthreads();
         M = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
@@ -529,12 +545,9 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
             }
         }
     }
+    Lr = group_reduce<SLC, false>(Lr);
 #pragma unroll
-    for (int m = SLC; m < 64; m <<= 1) {
-        Lr += shfl_xor(Lr, m);
-#pragma unroll
-        for (int i = 0; i < 4; i++) A[i] += shfl_xor(A[i], m);
-    }
+    for (int i = 0; i < 4; i++) A[i] = group_reduce<SLC, false>(A[i]);
     if ((tid & 63) < SLC) { sa[w][sl] = A; sl_[w][sl] = Lr; }
     __syncthreads();
     if (tid >= SLC) return;

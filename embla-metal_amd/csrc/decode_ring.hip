@@ -102,8 +102,7 @@ __global__ __launch_bounds__(256) void ring_decode_kernel(RingArgs a) {
         float mt = NEG_INF;
 #pragma unroll
         for (int e = 0; e < 8; e++) mt = fmaxf(mt, x[e]);
-        mt = fmaxf(mt, shfl_xor(mt, 16));
-        mt = fmaxf(mt, shfl_xor(mt, 32));
+        mt = max_rows(mt);
         const float mn = fmaxf(m, mt);
         if (__any(n < GQ && mn > m)) {
             if (__any(n < GQ && m != NEG_INF)) {
@@ -184,8 +183,7 @@ __global__ __launch_bounds__(256) void ring_decode_kernel(RingArgs a) {
                 dot += a2f<BF>((uint16_t)(qb[u][i] & 0xFFFF)) * kx[8 * u + 2 * i];
                 dot += a2f<BF>((uint16_t)(qb[u][i] >> 16)) * kx[8 * u + 2 * i + 1];
             }
-        dot += shfl_xor(dot, 16);
-        dot += shfl_xor(dot, 32);
+        dot = sum_rows(dot);
         float x[8];
         x[0] = dot * sc;
 #pragma unroll
@@ -225,8 +223,7 @@ __global__ __launch_bounds__(256) void ring_decode_kernel(RingArgs a) {
     // ---- merge the 4 waves (LDS), then this chunk's partial (or o with one chunk)
     __shared__ float om[4][GQ][HD];
     __shared__ float mm[4][GQ], ll[4][GQ];
-    l += shfl_xor(l, 16);
-    l += shfl_xor(l, 32);
+    l = sum_rows(l);
     if (g == 0 && n < GQ) { mm[w][n] = m; ll[w][n] = l; }
 #pragma unroll
     for (int u = 0; u < 8; u++)

@@ -113,8 +113,7 @@ __global__ __launch_bounds__(256) void sparse_decode_kernel(SparseArgs a) {
         float mt = NEG_INF;
 #pragma unroll
         for (int e = 0; e < 8; e++) mt = fmaxf(mt, x[e]);
-        mt = fmaxf(mt, shfl_xor(mt, 16));
-        mt = fmaxf(mt, shfl_xor(mt, 32));
+        mt = max_rows(mt);
         const float mn = fmaxf(m, mt);
         if (__any(n < GQ && mn > m)) {
             if (__any(n < GQ && m != NEG_INF)) {
@@ -162,8 +161,7 @@ __global__ __launch_bounds__(256) void sparse_decode_kernel(SparseArgs a) {
     // ---- merge the 4 waves (LDS), then this chunk's partial (or o with one chunk)
     __shared__ float om[4][GQ][HD];
     __shared__ float mm[4][GQ], ll[4][GQ];
-    l += shfl_xor(l, 16);
-    l += shfl_xor(l, 32);
+    l = sum_rows(l);
     if (g == 0 && n < GQ) { mm[w][n] = m; ll[w][n] = l; }
 #pragma unroll
     for (int u = 0; u < 8; u++)
@@ -385,8 +383,7 @@ __global__ __launch_bounds__(256) void sparse_rows8_kernel(SparseRows8Args a) {
         float mt = NEG_INF;
 #pragma unroll
         for (int e = 0; e < 8; e++) mt = fmaxf(mt, x[e]);
-        mt = fmaxf(mt, shfl_xor(mt, 16));
-        mt = fmaxf(mt, shfl_xor(mt, 32));
+        mt = max_rows(mt);
         const float mn = fmaxf(m, mt);
         if (__any(n < GQ && mn > m)) {
             if (__any(n < GQ && m != NEG_INF)) {
@@ -438,8 +435,7 @@ __global__ __launch_bounds__(256) void sparse_rows8_kernel(SparseRows8Args a) {
     float (*om)[GQ][HD] = (float (*)[GQ][HD])smem;
     float (*mm)[GQ] = (float (*)[GQ])(smem + 4 * GQ * HD * 4);
     float (*ll)[GQ] = (float (*)[GQ])(smem + (4 * GQ * HD + 4 * GQ) * 4);
-    l += shfl_xor(l, 16);
-    l += shfl_xor(l, 32);
+    l = sum_rows(l);
     if (g == 0 && n < GQ) { mm[w][n] = m; ll[w][n] = l; }
 #pragma unroll
     for (int u = 0; u < 8; u++)
@@ -555,8 +551,7 @@ __global__ __launch_bounds__(256, 4) void sparse_rows8_rm_kernel(SparseRows8Args
         float am = 0.0f;
 #pragma unroll
         for (int d = 0; d < 32; d++) am = fmaxf(am, fabsf(qf[d]));
-        am = fmaxf(am, shfl_xor(am, 16));
-        am = fmaxf(am, shfl_xor(am, 32));
+        am = max_rows(am);
         const float inv = am > 0.0f ? QFIX / am : 0.0f;
         // step x 1/sqrt(128) x log2(e), applied in the exponent's fma (> 0, so -inf scores stay -inf)
         qsc = fmaxf(am / QFIX * (0.08838834764831845f * 1.4426950408889634f), 1e-30f);
@@ -643,8 +638,7 @@ __global__ __launch_bounds__(256, 4) void sparse_rows8_rm_kernel(SparseRows8Args
         float mt = NEG_INF;
 #pragma unroll
         for (int e = 0; e < 8; e++) mt = fmaxf(mt, x[e]);
-        mt = fmaxf(mt, shfl_xor(mt, 16));
-        mt = fmaxf(mt, shfl_xor(mt, 32));
+        mt = max_rows(mt);
         const float mn = fmaxf(m, mt * qsc);
         if (__any(n < GQ && mn > m)) {
             if (__any(n < GQ && m != NEG_INF)) {
@@ -702,8 +696,7 @@ __global__ __launch_bounds__(256, 4) void sparse_rows8_rm_kernel(SparseRows8Args
     float (*om)[GQ][HD] = (float (*)[GQ][HD])smem;
     float (*mm)[GQ] = (float (*)[GQ])(smem + 4 * GQ * HD * 4);
     float (*ll)[GQ] = (float (*)[GQ])(smem + (4 * GQ * HD + 4 * GQ) * 4);
-    l += shfl_xor(l, 16);
-    l += shfl_xor(l, 32);
+    l = sum_rows(l);
     if (g == 0 && n < GQ) { mm[w][n] = m; ll[w][n] = l; }
 #pragma unroll
     for (int u = 0; u < 8; u++)

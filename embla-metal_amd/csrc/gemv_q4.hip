@@ -26,6 +26,26 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2v_t, a), __builtin_bit_cast(bf2v_t, b), c, false);
 }
 
+/// The sum over the wave's 64 lanes, in every lane: within 16-lane rows by DPP (quad xor 1, xor 2,
+/// then the half-row and row mirrors), then the 4 rows' totals by readlane. No LDS round trips (a
+/// chain of ds_bpermute shuffles waits on LDS each step).
+__device__ __forceinline__ float wave_total(float v) {
+    auto dpp = [](float x, int ctrl) -> float {
+        const int xi = __builtin_bit_cast(int, x);
+        switch (ctrl) {   // constant after inlining
+            case 0: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(xi, xi, 0xB1, 0xF, 0xF, false));
+            case 1: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(xi, xi, 0x4E, 0xF, 0xF, false));
+            case 2: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(xi, xi, 0x141, 0xF, 0xF, false));
+            default: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(xi, xi, 0x140, 0xF, 0xF, false));
+        }
+    };
+    v += dpp(v, 0);   // quad_perm [1, 0, 3, 2]
+    v += dpp(v, 1);   // quad_perm [2, 3, 0, 1]: every lane of a quad holds its sum
+    v += dpp(v, 2);   // row_half_mirror: the other quad of the 8
+    v += dpp(v, 3);   // row_mirror: the other 8 of the row
+    return (readlane(v, 0) + readlane(v, 16)) + (readlane(v, 32) + readlane(v, 48));
+}
+
 template <int EPI, int RW>
 __global__ __launch_bounds__(256) void gemv_q4_kernel(GemvArgs a) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -105,9 +125,7 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(GemvArgs a) {
                 r += sc[u][sp] * d + (bi[u][sp] - 128.0f * sc[u][sp]) * xs[sp];
             }
         }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) r += shfl_xor(r, o);
-        acc[u] = r;
+        acc[u] = wave_total(r);
     }
     if (lane < RW) {   // lane u writes row u
         float v = acc[0];
