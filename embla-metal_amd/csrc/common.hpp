@@ -142,6 +142,36 @@ __device__ __forceinline__ float sum_xor32(float v) {
 /// max / sum over the four 16-lane rows (xor 16, then xor 32)
 __device__ __forceinline__ float max_rows(float v) { return fmax_xor32(max_xor16(v)); }
 __device__ __forceinline__ float sum_rows(float v) { return sum_xor32(sum_xor16(v)); }
+/// DPP moves (VALU, no LDS round trip); CTRL: quad_perm 0xB1 (lane xor 1), 0x4E (xor 2),
+/// row_half_mirror 0x141 (lane 7 - i of its 8), row_mirror 0x140, row_shr:n 0x110 + n, row_ror:n
+/// 0x120 + n, row_bcast:15 0x142, row_bcast:31 0x143. Lanes with no source (bound_ctrl) and rows
+/// off in ROW_MASK read 0.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xF, true);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+/// Inclusive prefix sums within each 16-lane row (every lane of the wave active).
+__device__ __forceinline__ uint32_t row_scan_incl(uint32_t v) {
+    v += dpp_u32<0x111>(v);
+    v += dpp_u32<0x112>(v);
+    v += dpp_u32<0x114>(v);
+    v += dpp_u32<0x118>(v);
+    return v;
+}
+/// Inclusive prefix sum over the wave's 64 lanes (every lane active): the rows' scans, then row
+/// 0's total into row 1 and row 2's into row 3 (row_bcast:15), then lane 31's into rows 2 and 3
+/// (row_bcast:31). Exact for integers, as the shfl_up ladder it replaces.
+__device__ __forceinline__ uint32_t wave_scan_incl(uint32_t v) {
+    v = row_scan_incl(v);
+    v += dpp_u32<0x142, 0xA>(v);
+    v += dpp_u32<0x143, 0xC>(v);
+    return v;
+}
+__device__ __forceinline__ uint32_t readlane_u32(uint32_t v, int l) { return (uint32_t)__builtin_amdgcn_readlane((int)v, l); }
 __device__ __forceinline__ float readlane(float v, int l) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }

@@ -39,20 +39,12 @@ __device__ __forceinline__ uint32_t order_bits(float f) {
 __device__ __forceinline__ uint32_t block_scan_excl(uint32_t v, uint32_t* buf, uint32_t& total) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     uint32_t incl = v;
-#pragma unroll
-    for (int s = 1; s < 64; s <<= 1) {
-        const uint32_t o = __shfl_up(incl, s, 64);
-        if (lane >= s) incl += o;
-    }
+    incl = wave_scan_incl(incl);
     if (lane == 63) buf[w] = incl;
     __syncthreads();
     if (w == 0) {
         uint32_t x = lane < 16 ? buf[lane] : 0u, xi = x;
-#pragma unroll
-        for (int s = 1; s < 16; s <<= 1) {
-            const uint32_t o = __shfl_up(xi, s, 64);
-            if (lane >= s) xi += o;
-        }
+        xi = row_scan_incl(xi);
         if (lane < 16) buf[lane] = xi - x;
         if (lane == 15) buf[16] = xi;
     }
@@ -235,11 +227,7 @@ __global__ __launch_bounds__(SEL_T) void select_topk_kernel(const float* __restr
         const uint32_t v0 = 2 * lane < m ? t[2 * lane] : 0u, v1 = 2 * lane + 1 < m ? t[2 * lane + 1] : 0u;
         const uint32_t s = v0 + v1;
         uint32_t incl = s;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const uint32_t o = __shfl_up(incl, d, 64);
-            if (lane >= d) incl += o;
-        }
+        incl = wave_scan_incl(incl);
         if (2 * lane < m) t[2 * lane] = incl - s;
         if (2 * lane + 1 < m) t[2 * lane + 1] = incl - s + v0;
         if (lane == 63) sm.sel[w] = incl;   // totals: keys above kth, keys equal to it
@@ -337,9 +325,9 @@ __global__ __launch_bounds__(256) void wsel_classify_kernel(const float* __restr
     const uint32_t cd = sel[0] & (CB - 1), above_c = sel[1];
     {   // the fine bins of cd: the sum of the scorer workgroups' rows (one a scorer workgroup)
         const int nsc = min(index_score_blocks(n), kWideSelectScorers);
-        // (a row a thread, two bins a word; summed as packed 16-bit pairs across the wave by
-        // shuffles, no bin's total exceeding 32768, then one LDS atomic a word a wave: LDS atomics
-        // of every lane on the same 16 words cost ~19 us)
+        // (a row a thread, two bins a word; summed as packed 16-bit pairs across the wave by a
+        // DPP scan, no bin's total or partial sum exceeding 32768, then one LDS atomic a word a
+        // wave: LDS atomics of every lane on the same 16 words cost ~19 us)
         const uint32_t* F = sw + kWideSelectFine;
         uint32_t x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
         if (tid < nsc) {
@@ -349,9 +337,7 @@ __global__ __launch_bounds__(256) void wsel_classify_kernel(const float* __restr
         }
         if (tid < ((nsc + 63) & ~63)) {   // uniform a wave
 #pragma unroll
-            for (int o = 32; o >= 1; o >>= 1)
-#pragma unroll
-                for (int i = 0; i < 8; i++) x[i] += (uint32_t)__shfl_xor((int)x[i], o, 64);
+            for (int i = 0; i < 8; i++) x[i] = readlane_u32(wave_scan_incl(x[i]), 63);   // the wave's totals
             if (lane == 0)
 #pragma unroll
                 for (int i = 0; i < 8; i++) atomicAdd(&fp[i], x[i]);
@@ -362,11 +348,7 @@ __global__ __launch_bounds__(256) void wsel_classify_kernel(const float* __restr
     if (w == 0) {   // lanes < 16: fine bins 16 cd + 15 - lane, from the top
         const uint32_t v = lane < 16 ? (fp[(15 - lane) >> 1] >> (16 * ((15 - lane) & 1))) & 0xFFFF : 0u;
         uint32_t incl = v;
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) {
-            const uint32_t x = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += x;
-        }
+        incl = row_scan_incl(incl);
         const uint32_t k1 = (uint32_t)topk - above_c;
         if (lane < 16 && incl - v < k1 && incl >= k1) { sel[0] = 16 * cd + 15 - lane; sel[1] = above_c + incl - v; }
     }
@@ -387,7 +369,7 @@ __global__ __launch_bounds__(256) void wsel_classify_kernel(const float* __restr
         if (bc) {
             uint32_t p0 = 0;
             if (lane == 0) p0 = atomicAdd(&lcnt, (uint32_t)__popcll(bc));
-            p0 = __shfl(p0, 0, 64);
+            p0 = readlane_u32(p0, 0);
             if (real && dg == d1) {
                 const uint32_t p = p0 + __builtin_amdgcn_mbcnt_hi((uint32_t)(bc >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bc, 0u));
                 cand[2 * p] = key;   // p < 1024: a workgroup has 1024 keys
@@ -463,9 +445,11 @@ __global__ __launch_bounds__(256) void index_scores_kernel(const uint16_t* __res
                 float c = 0.0f;
 #pragma unroll
                 for (int d = 0; d < 8; d++) c = __builtin_fmaf(q[h][d], kf[d], c);
-                c = c + shfl_xor(c, 1);
-                c = c + shfl_xor(c, 2);
-                c = c + shfl_xor(c, 4);
+                // lane xor 1, xor 2 (quad_perm), then the other quad of the 8 (row_half_mirror: its 4
+                // lanes agree by then): the spec's ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7))
+                c = c + dpp_f32<0xB1>(c);
+                c = c + dpp_f32<0x4E>(c);
+                c = c + dpp_f32<0x141>(c);
                 const float r = fmaxf(c, 0.0f);
                 const float r2 = r * r;
                 s = __builtin_fmaf(w[h], r2, s);

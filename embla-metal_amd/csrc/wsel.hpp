@@ -38,22 +38,14 @@ __device__ __forceinline__ void pick4096(const uint32_t* h, uint32_t k, uint32_t
         s += (x[0] + x[1]) + (x[2] + x[3]);
     }
     uint32_t above = s;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t x = __shfl_up(above, o, 64);
-        if (lane >= o) above += x;
-    }
+    above = wave_scan_incl(above);
     above -= s;
     const int L = max(__ffsll((long long)__ballot(above < k && above + s >= k)) - 1, 0);   // 0 if none
-    const uint32_t base = __shfl(above, L, 64);
+    const uint32_t base = readlane_u32(above, L);   // L is uniform
     const int d = DB - 1 - 64 * L - lane;
     const uint32_t c = h[d];
     uint32_t incl = c;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t y = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += y;
-    }
+    incl = wave_scan_incl(incl);
     if (base + incl - c < k && base + incl >= k) { sel[0] = (uint32_t)d; sel[1] = base + incl - c; }
 }
 
@@ -65,11 +57,7 @@ __device__ __forceinline__ void pick256(const uint32_t* h, uint32_t k, uint32_t*
 #pragma unroll
     for (int i = 0; i < 4; i++) { cc[i] = h[255 - 4 * lane - i]; s += cc[i]; }
     uint32_t above = s;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t x = __shfl_up(above, o, 64);
-        if (lane >= o) above += x;
-    }
+    above = wave_scan_incl(above);
     if (total && lane == 63) *total = above;
     above -= s;
 #pragma unroll
@@ -84,11 +72,7 @@ template <int BT>
 __device__ __forceinline__ uint32_t wsel_scan(uint32_t v, uint32_t* wsum, uint32_t& total) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     uint32_t incl = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t x = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += x;
-    }
+    incl = wave_scan_incl(incl);
     if (lane == 63) wsum[w] = incl;
     __syncthreads();
     uint32_t before = 0;
@@ -178,11 +162,7 @@ __device__ __forceinline__ void wsel_slice_block(int n, int topk, const uint32_t
     if (w == 0) {   // offsets of the regions in the list (nb <= NR)
         const uint32_t c = lane < nb ? min(cnts[lane], 1024u) : 0u;
         uint32_t incl = c;
-#pragma unroll
-        for (int o = 1; o < NR; o <<= 1) {
-            const uint32_t x = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += x;
-        }
+        incl = wave_scan_incl(incl);
         if (lane < nb) coff[lane] = incl - c;
         if (lane == nb - 1) coff[nb] = incl;
     }
@@ -273,22 +253,14 @@ __device__ __forceinline__ void pick1024(const uint32_t* h, uint32_t k, uint32_t
         s += (x[0] + x[1]) + (x[2] + x[3]);
     }
     uint32_t above = s;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t x = __shfl_up(above, o, 64);
-        if (lane >= o) above += x;
-    }
+    above = wave_scan_incl(above);
     above -= s;
     const int L = max(__ffsll((long long)__ballot(above < k && above + s >= k)) - 1, 0);   // 0 if none
-    const uint32_t base = __shfl(above, L, 64);
+    const uint32_t base = readlane_u32(above, L);   // L is uniform
     const int d = 1023 - 16 * L - (lane & 15);
     const uint32_t c = lane < 16 ? h[d] : 0u;
     uint32_t incl = c;
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-        const uint32_t y = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += y;
-    }
+    incl = row_scan_incl(incl);
     if (lane < 16 && base + incl - c < k && base + incl >= k) { sel[0] = (uint32_t)d; sel[1] = base + incl - c; }
 }
 
@@ -348,18 +320,12 @@ __device__ __forceinline__ void wsel_slice(int n, int topk, const uint32_t* __re
         for (int i = 0; i < 8; i++) cv[i] = *(const u4_t*)(creg + 2 * (1024 * rb + 16 * rh) + 4 * i);
         const uint32_t cown = lane < nb ? min(cnts[lane], 1024u) : 0u;
         const uint32_t cb = __shfl(cown, rb, 64);   // the lane's region's count (0 past nb)
-        uint32_t tot = cown;
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) tot += __shfl_xor(tot, o, 64);
+        const uint32_t tot = readlane_u32(wave_scan_incl(cown), 63);
         const bool ok = __ballot(cb > WSL_WSPEC) == 0 && tot <= WSL_WMAX && nr <= 64;
         if (ok) {
             const uint32_t nv = (uint32_t)min(max((int)cb - 16 * rh, 0), 16);   // the lane's candidates
             uint32_t incl = nv;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const uint32_t x = __shfl_up(incl, o, 64);
-                if (lane >= o) incl += x;
-            }
+            incl = wave_scan_incl(incl);
             const uint32_t off = incl - nv;
 #pragma unroll
             for (int i = 0; i < 16; i++)
@@ -426,12 +392,9 @@ __device__ __forceinline__ void wsel_slice(int n, int topk, const uint32_t* __re
             }
         }
         uint32_t ig = cg, ie = ce;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t xg = __shfl_up(ig, o, 64), xe = __shfl_up(ie, o, 64);
-            if (lane >= o) { ig += xg; ie += xe; }
-        }
-        const uint32_t ngt = __shfl(ig, 63, 64), kt = wsl_kt;
+        ig = wave_scan_incl(ig);
+        ie = wave_scan_incl(ie);
+        const uint32_t ngt = readlane_u32(ig, 63), kt = wsl_kt;
         uint32_t sg = ig - cg, se = ie - ce;
 #pragma unroll
         for (int i = 0; i < 16; i += 4) {
