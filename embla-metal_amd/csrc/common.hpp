@@ -130,6 +130,12 @@ __device__ __forceinline__ float sum_xor16(float v) {
     const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
+/// v of lane xor 16 (exactly shfl_xor(v, 16)): from the swap's pair, the half that is not the
+/// lane's own (rows 0 and 2 find their partner's in r[1], rows 1 and 3 in r[0]).
+__device__ __forceinline__ float xchg_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+}
 /// The same over lane xor 32 (v_permlane32_swap); fmaxf, as the shfl_xor reductions it replaces.
 __device__ __forceinline__ float fmax_xor32(float v) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
@@ -169,6 +175,27 @@ __device__ __forceinline__ uint32_t wave_scan_incl(uint32_t v) {
     v = row_scan_incl(v);
     v += dpp_u32<0x142, 0xA>(v);
     v += dpp_u32<0x143, 0xC>(v);
+    return v;
+}
+/// op over the wave's 64 lanes, in every lane, bit for bit as the xor butterfly 32, 16, 8, 4, 2, 1
+/// (v = op(v, v of lane xor m)) gives it, for a commutative op: the permlane swaps hand each lane
+/// the pair for xor 32 and 16; row_ror:8 is xor 8 within a 16-lane row; row_ror:4 reads lane
+/// i + 4 mod 16, which is i ^ 4 or i ^ 4 ^ 8, and lanes i and i ^ 8 agree after the xor-8 level;
+/// then quad_perm for xor 2 and xor 1. No LDS round trips.
+template <class Op>
+__device__ __forceinline__ float wave_bfly(float v, Op op) {
+    {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    }
+    {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    }
+    v = op(v, dpp_f32<0x128>(v));
+    v = op(v, dpp_f32<0x124>(v));
+    v = op(v, dpp_f32<0x4E>(v));
+    v = op(v, dpp_f32<0xB1>(v));
     return v;
 }
 __device__ __forceinline__ uint32_t readlane_u32(uint32_t v, int l) { return (uint32_t)__builtin_amdgcn_readlane((int)v, l); }

@@ -153,8 +153,7 @@ __global__ __launch_bounds__(256) void full16_decode_kernel(Full16Args a) {
                 x[e] = valid[e] ? x[e] * (qs * LOG2E16) : NEG_INF;
                 mt = fmaxf(mt, x[e]);
             }
-            mt = fmaxf(mt, shfl_xor(mt, 16));
-            mt = fmaxf(mt, shfl_xor(mt, 32));
+            mt = max_rows(mt);
             const float mn = fmaxf(m, mt);
             if (__any(n < GQ && mn > m)) {
                 if (__any(n < GQ && m != NEG_INF)) {
@@ -224,8 +223,7 @@ __global__ __launch_bounds__(256) void full16_decode_kernel(Full16Args a) {
     // ---- merge the 4 waves (LDS), then this chunk's partial (or o with one chunk)
     __shared__ float om[4][GQ][HD];
     __shared__ float mm[4][GQ], ll[4][GQ];
-    l += shfl_xor(l, 16);
-    l += shfl_xor(l, 32);
+    l = sum_rows(l);
     if (g == 0 && n < GQ) { mm[w][n] = m; ll[w][n] = l; }
 #pragma unroll
     for (int u = 0; u < 8; u++)

@@ -41,7 +41,7 @@ __device__ __forceinline__ void prep_row(const uint16_t* src, const uint16_t* ga
         // rotate dims (d, d + 32), d < 32: lane group 0 holds d, group 1 holds d + 32
 #pragma unroll
         for (int d = 0; d < 32; d++) {
-            const float other = shfl_xor(x[d], 16);
+            const float other = xchg_xor16(x[d]);
             if (g < 2) {
                 float cs, sn;
                 rope_cs(pos, d, cs, sn);

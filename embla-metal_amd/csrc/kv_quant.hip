@@ -81,7 +81,7 @@ __global__ __launch_bounds__(64) void ring_append_kernel(RingAppendArgs a) {
         x0 = x0 * (r * (1.0f + bf2f(a.kg[2 * lane])));
         x1 = x1 * (r * (1.0f + bf2f(a.kg[2 * lane + 1])));
         // RoPE: dims d and d + 32 (d < 32) rotate together; lane l holds 2l, 2l + 1
-        const float o0 = shfl_xor(x0, 16), o1 = shfl_xor(x1, 16);
+        const float o0 = xchg_xor16(x0), o1 = xchg_xor16(x1);
         if (lane < 32) {
             const int d0 = (2 * lane) & 31;
             float s0, c0, s1, c1;

@@ -12,15 +12,12 @@ namespace embla {
 
 constexpr float EPS32 = 1.1920929e-07f;
 
+/// Sum (max) over the wave as the xor butterfly 32 .. 1 (v = v + v of lane xor m) gives it.
 __device__ __forceinline__ float wave_sum_bfly(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = v + shfl_xor(v, m);
-    return v;
+    return wave_bfly(v, [](float a, float b) { return a + b; });
 }
 __device__ __forceinline__ float wave_max_bfly(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor(v, m));
-    return v;
+    return wave_bfly(v, [](float a, float b) { return fmaxf(a, b); });
 }
 
 /// RMS factor of a head held two dims a lane, in the fixed order the oracle restates.
@@ -44,9 +41,9 @@ __device__ __forceinline__ float sumsq_grouped32(const float* x) {
         v[i] = a + b;
     }
 #pragma unroll
-    for (int i = 0; i < 16; i++) v[i] = v[i] + shfl_xor(v[i], 32);
+    for (int i = 0; i < 16; i++) v[i] = sum_xor32(v[i]);
 #pragma unroll
-    for (int i = 0; i < 16; i++) v[i] = v[i] + shfl_xor(v[i], 16);
+    for (int i = 0; i < 16; i++) v[i] = sum_xor16(v[i]);
 #pragma unroll
     for (int m = 8; m >= 1; m >>= 1)
 #pragma unroll

@@ -293,7 +293,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
 #pragma unroll
                 for (int e = 0; e < m; e++) v[e] = v[e] + v[e + m];
 #pragma unroll
-            for (int e = 0; e < 4; e++) v[e] = v[e] + shfl_xor(v[e], 32);
+            for (int e = 0; e < 4; e++) v[e] = sum_xor32(v[e]);
             v[0] = v[0] + v[2];
             v[1] = v[1] + v[3];
             v[0] = v[0] + v[1];
@@ -472,7 +472,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
     // loop) and written coalesced: a token's GQ heads are one contiguous run, GQ partial records
     // (PPH floats each) or GQ output rows. Each lane holding one row, 32 rows 4 KB apart a store
     // instruction, cost 4.2 µs a call on the sliding layer's 8.4 MB output.
-    lsum += shfl_xor(lsum, 32);
+    lsum = sum_xor32(lsum);
     const float inv = RELU2 ? 1.0f / (11.313708498984761f + lsum) : 1.0f / lsum;
     const int tl = 32 * (w / GQ) + r, hl = w % GQ;   // the lane's token and head in the workgroup
     const int ntok = min(32 * RB, a.T - wt0);

@@ -75,10 +75,8 @@ __device__ __forceinline__ void wave_best(float& v, uint32_t& i) {
     }
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+__device__ __forceinline__ float wave_sum(float v) {   // the xor butterfly's sum, bit for bit
+    return wave_bfly(v, [](float a, float b) { return a + b; });
 }
 
 // ------------------------------------------------------------------ block scan
@@ -147,8 +145,7 @@ struct BlockRec { float z, cm; uint32_t nc; float s; uint32_t si; float x; uint3
 __device__ __forceinline__ float global_max(const float* bmax, int G) {
     const int lane = threadIdx.x & 63;
     float m = lane < G ? bmax[lane] : NEG_INF;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    m = wave_bfly(m, [](float a, float b) { return fmaxf(a, b); });
     return m;
 }
 
@@ -180,11 +177,7 @@ __global__ __launch_bounds__(256) void sample_weights_kernel(const uint16_t* __r
     }
     // candidates compacted in the block's list, in token order: exclusive scan of n
     uint32_t incl = n;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t v = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += v;
-    }
+    incl = wave_scan_incl(incl);
     z = wave_sum(z);
     cm = wave_sum(cm);
     wave_best(best, bi);
@@ -260,11 +253,7 @@ __global__ __launch_bounds__(FT) void sample_final_kernel(const uint16_t* __rest
         BlockRec r = {};
         if (lane < G) r = rec[lane];
         uint32_t incl = lane < G ? r.nc : 0;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t v = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += v;
-        }
+        incl = wave_scan_incl(incl);
         off[lane + 1] = incl;
         if (lane == 0) off[0] = 0;
         float s = lane < G ? r.s : NEG_INF;

@@ -94,7 +94,7 @@ __global__ __launch_bounds__(256) void index_mfma_kernel(IndexMfmaArgs a) {
                     ss = __builtin_fmaf(x0, x0, ss);
                     ss = __builtin_fmaf(x1, x1, ss);
                 }
-            ss += shfl_xor(ss, 32);
+            ss = sum_xor32(ss);
             nmax = fmaxf(nmax, ss);
         }
 #pragma unroll
@@ -113,8 +113,7 @@ __global__ __launch_bounds__(256) void index_mfma_kernel(IndexMfmaArgs a) {
             }
     }
     if (norms) {
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) nmax = fmaxf(nmax, shfl_xor(nmax, o));
+        nmax = wave_bfly(nmax, [](float x, float y) { return fmaxf(x, y); });
         // the fp32 sum of 64 exact squares is within 64 units of 2^-24 of the true sum
         if (lane == 0) a.kmax[ch] = sqrtf(nmax * (1.0f + 0x1p-16f)) * (1.0f + 0x1p-16f);
     }
@@ -198,11 +197,7 @@ __device__ void bs_pick(Sm& sm, int nc, uint32_t k) {
             s += t;
         }
         uint32_t above = s;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t x = __shfl_up(above, o, 64);
-            if (lane >= o) above += x;
-        }
+        above = wave_scan_incl(above);
         above -= s;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -230,22 +225,14 @@ __device__ void bs_pick1(BandSmem& sm, uint32_t k) {
                 s += (x[0] + x[1]) + (x[2] + x[3]);
             }
         uint32_t above = s;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t x = __shfl_up(above, o, 64);
-            if (lane >= o) above += x;
-        }
+        above = wave_scan_incl(above);
         above -= s;
-        const int L = __ffsll((long long)__ballot(above < k && above + s >= k)) - 1;
-        const uint32_t base = __shfl(above, L, 64);
+        const int L = max(__ffsll((long long)__ballot(above < k && above + s >= k)) - 1, 0);
+        const uint32_t base = readlane_u32(above, L);   // L is uniform
         const int d = 4095 - 64 * L - lane;   // bins of lane L, from the top
         const uint32_t c = sm.h1[0][d] + sm.h1[1][d];
         uint32_t incl = c;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t y = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += y;
-        }
+        incl = wave_scan_incl(incl);
         if (base + incl - c < k && base + incl >= k) { sm.sel[0] = (uint32_t)d; sm.sel[1] = base + incl - c; }
     }
     __syncthreads();
@@ -260,11 +247,7 @@ __device__ void bs_emit(Sm& sm, uint32_t k, uint32_t* __restrict__ out, int n, i
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     auto block_scan = [&](uint32_t c, uint32_t& total) -> uint32_t {
         uint32_t incl = c;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t x = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += x;
-        }
+        incl = wave_scan_incl(incl);
         if (lane == 63) sm.wsum[w] = incl;
         __syncthreads();
         uint32_t before = 0;
@@ -328,8 +311,7 @@ __global__ __launch_bounds__(BS_T) __attribute__((amdgpu_waves_per_eu(6))) void 
         // row, from the row's query norms, weights and the key norm maximum
         float km = 0.0f;
         for (int c = lane; c < a.nchunks; c += 64) km = fmaxf(km, a.kmax[c]);
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) km = fmaxf(km, shfl_xor(km, o));
+        km = wave_bfly(km, [](float x, float y) { return fmaxf(x, y); });
         double eps = 0.0, mag = 0.0;
 #pragma unroll
         for (int h = 0; h < 4; h++) {
@@ -408,7 +390,7 @@ __global__ __launch_bounds__(BS_T) __attribute__((amdgpu_waves_per_eu(6))) void 
                 if (bm) {   // one LDS atomic a wave (scores massed at the k-th value put every lane here)
                     uint32_t p0 = 0;
                     if (lane == __ffsll((long long)bm) - 1) p0 = atomicAdd(&sm.cnt[0], (uint32_t)__popcll(bm));
-                    p0 = __shfl(p0, __ffsll((long long)bm) - 1, 64);
+                    p0 = readlane_u32(p0, __ffsll((long long)bm) - 1);   // a uniform lane
                     const uint32_t p = p0 + (uint32_t)__popcll(bm & ((1ull << lane) - 1));
                     if (inb && p < BS_LB) sm.bj[p] = (uint32_t)(j + e);
                 }
@@ -598,8 +580,7 @@ __global__ __launch_bounds__(BS_T) void band_overflow_kernel(BandSelectArgs a) {
             for (int i = 0; i < OV_NK; i++)
                 if (ok[i]) sm.xs[jj[i]] = ob32(x[i]);
         }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) nab += (uint32_t)__shfl_xor((int)nab, o, 64);
+        nab = readlane_u32(wave_scan_incl(nab), 63);   // the wave's total
         if (lane == 0 && nab) atomicAdd(&sm.above, nab);
         __syncthreads();
         uint32_t k = (uint32_t)a.topk - sm.above;   // rank of the spec's k-th largest in the band
