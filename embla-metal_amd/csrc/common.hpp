@@ -198,6 +198,19 @@ __device__ __forceinline__ float wave_bfly(float v, Op op) {
     v = op(v, dpp_f32<0xB1>(v));
     return v;
 }
+/// A lane's O^T block of a 16x16 MFMA output (O[u][i]: dim 8n + u, head 4g + i) into LDS rows
+/// om[head][128], for the heads below GQ (a multiple of 4): one branch, two 16-byte stores a head
+/// (a store a value under its own condition compiled to a branch each).
+template <int GQ>
+__device__ __forceinline__ void store_o_rows(float (*om)[128], const f4_t* O, int n, int g) {
+    if (4 * g < GQ) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            *(f4_t*)&om[4 * g + i][8 * n] = (f4_t){O[0][i], O[1][i], O[2][i], O[3][i]};
+            *(f4_t*)&om[4 * g + i][8 * n + 4] = (f4_t){O[4][i], O[5][i], O[6][i], O[7][i]};
+        }
+    }
+}
 __device__ __forceinline__ uint32_t readlane_u32(uint32_t v, int l) { return (uint32_t)__builtin_amdgcn_readlane((int)v, l); }
 __device__ __forceinline__ float readlane(float v, int l) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));

@@ -401,15 +401,11 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
     }
 
     // ---- merge the waves (LDS)
-    __shared__ float om[DW][GQ][HD];
+    __shared__ __attribute__((aligned(16))) float om[DW][GQ][HD];
     __shared__ float mm[DW][GQ], ll[DW][GQ];
     l = sum_rows(l);
     if (g == 0 && n < GQ) { mm[w][n] = m; ll[w][n] = l; }
-#pragma unroll
-    for (int u = 0; u < 8; u++)
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            if (4 * g + i < GQ) om[w][4 * g + i][8 * n + u] = O[u][i];
+    store_o_rows<GQ>(om[w], O, n, g);
     __syncthreads();
 
     constexpr int PER = GQ * HD / (64 * DW);   // outputs a thread: 1 or 2 (one head, consecutive dims)

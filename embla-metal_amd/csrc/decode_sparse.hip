@@ -159,15 +159,11 @@ __global__ __launch_bounds__(256) void sparse_decode_kernel(SparseArgs a) {
     }
 
     // ---- merge the 4 waves (LDS), then this chunk's partial (or o with one chunk)
-    __shared__ float om[4][GQ][HD];
+    __shared__ __attribute__((aligned(16))) float om[4][GQ][HD];
     __shared__ float mm[4][GQ], ll[4][GQ];
     l = sum_rows(l);
     if (g == 0 && n < GQ) { mm[w][n] = m; ll[w][n] = l; }
-#pragma unroll
-    for (int u = 0; u < 8; u++)
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            if (4 * g + i < GQ) om[w][4 * g + i][8 * n + u] = O[u][i];
+    store_o_rows<GQ>(om[w], O, n, g);
     __syncthreads();
     constexpr int PER = GQ * HD / 256;
     const int oh = tid * PER / HD, od = tid * PER % HD;
@@ -437,11 +433,7 @@ __global__ __launch_bounds__(256) void sparse_rows8_kernel(SparseRows8Args a) {
     float (*ll)[GQ] = (float (*)[GQ])(smem + (4 * GQ * HD + 4 * GQ) * 4);
     l = sum_rows(l);
     if (g == 0 && n < GQ) { mm[w][n] = m; ll[w][n] = l; }
-#pragma unroll
-    for (int u = 0; u < 8; u++)
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            if (4 * g + i < GQ) om[w][4 * g + i][8 * n + u] = O[u][i];
+    store_o_rows<GQ>(om[w], O, n, g);
     __syncthreads();
     constexpr int PER = GQ * HD / 256;
     const int oh = tid * PER / HD, od = tid * PER % HD;
@@ -698,11 +690,7 @@ __global__ __launch_bounds__(256, 4) void sparse_rows8_rm_kernel(SparseRows8Args
     float (*ll)[GQ] = (float (*)[GQ])(smem + (4 * GQ * HD + 4 * GQ) * 4);
     l = sum_rows(l);
     if (g == 0 && n < GQ) { mm[w][n] = m; ll[w][n] = l; }
-#pragma unroll
-    for (int u = 0; u < 8; u++)
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            if (4 * g + i < GQ) om[w][4 * g + i][8 * n + u] = O[u][i];
+    store_o_rows<GQ>(om[w], O, n, g);
     __syncthreads();
     constexpr int PER = GQ * HD / 256;
     const int oh = tid * PER / HD, od = tid * PER % HD;
