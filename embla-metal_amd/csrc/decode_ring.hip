@@ -8,8 +8,9 @@
 // MI355X design: the ring holds K and V in the MFMA lane-order 32-key tiles (common.hpp, ES = 2), so
 // S^T = K q^T and O += W V run on v_mfma_f32_16x16x32_{f16,bf16} with no conversion of K or V.
 // Workgroups split the window's ring part (positions lo .. pos-1) into chunks; the current key is
-// one extra row taken from the inputs by the last chunk's workgroup, which also writes it into the
-// ring (no other workgroup reads that slot in this launch, W <= R). Chunk partials are merged by
+// one extra row taken from the inputs by the last chunk's workgroup (its wave with the fewest
+// tiles: C2 7.87 -> 7.18 us a step against its first wave after that wave's tiles), which also
+// writes it into the ring (no other workgroup reads that slot in this launch, W <= R). Chunk partials are merged by
 // decode_merge_kernel (decode_full.hip).
 #include "common.hpp"
 #include "embla_internal.hpp"
@@ -169,8 +170,10 @@ __global__ __launch_bounds__(256) void ring_decode_kernel(RingArgs a) {
         }
     }
 
-    // the current key: one extra row, taken by wave 0 of the last chunk's workgroup
-    if (c == a.C - 1 && w == 0) {
+    // the current key: one extra row, taken by wave 3 of the last chunk's workgroup (tiles are
+    // dealt to waves 0, 1, 2, 3 in turn, so wave 3 has the fewest, none in a chunk of up to 3
+    // tiles, and its loads of the new rows overlap the other waves' tiles)
+    if (c == a.C - 1 && w == 3) {
         float kx[32], vx[32];
         prep_row<BF, PREOPS>(a.k_new + (size_t)kvh * HD, a.kg, g, pos, kx);
         prep_row<BF, false>(a.v_new + (size_t)kvh * HD, nullptr, g, pos, vx);
