@@ -53,6 +53,7 @@ __global__ __launch_bounds__(256) void sparse_decode_kernel(SparseArgs a) {
     uint16_t* Ks = stage[w][0];
     uint16_t* Vs = stage[w][1];
     __shared__ uint32_t srows[FS ? SPD_FS_MAXCH : 1];   // FS: the chunk's selected rows
+    static_assert(sizeof(stage) / 4 >= WSL_FIXED + 2, "the staging LDS holds the select's last step");
     if constexpr (FS) {
         // ranks j0 .. ts - 1 of the selection, from the wide select's last step (its scratch is
         // the staging LDS, free until the first gather); the rows go to the output at the end
@@ -78,17 +79,25 @@ __global__ __launch_bounds__(256) void sparse_decode_kernel(SparseArgs a) {
 
     for (int t0 = j0 + 32 * w; t0 < j1; t0 += 128) {
         // gather: load j covers rows 4j .. 4j + 3, lane l: row 4j + l / 16, dims 8 (l % 16) ..
-        u4_t kr[8], vr[8];
+        // the 8 row indices first, with no branch (an index read a row behind its own wait put 8
+        // round trips before the last load): keys past the chunk's last (p >= j1) take row 0,
+        // their index reads clamped in range and discarded
+        int r[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int p = t0 + 4 * j + (lane >> 4);
-            // keys past the chunk's last (p >= j1) read row 0 and nothing of the index lists
-            int r = 0;
-            if (p < j1) {
-                if constexpr (FS) r = p < a.sel_topk ? (int)srows[p - j0] : a.sel_n + p - a.sel_topk;
-                else r = rows ? (int)rows[p] : p;
+            if constexpr (FS) {
+                const int sr = (int)srows[min(p - j0, SPD_FS_MAXCH - 1)];
+                r[j] = p < j1 ? (p < a.sel_topk ? sr : a.sel_n + p - a.sel_topk) : 0;
+            } else {
+                r[j] = rows ? (int)rows[min(p, j1 - 1)] : p;
+                r[j] = p < j1 ? r[j] : 0;
             }
-            const size_t row = (size_t)min(r, a.max_s - 1);   // rows clamped in range
+        }
+        u4_t kr[8], vr[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const size_t row = (size_t)min(r[j], a.max_s - 1);   // rows clamped in range
             kr[j] = ld16(kb + row * HD + 8 * n);
             vr[j] = ld16(vb + row * HD + 8 * n);
         }

@@ -298,6 +298,7 @@ __device__ __forceinline__ void wsel_slice(int n, int topk, const uint32_t* __re
                                            uint32_t r0, uint32_t nr, uint32_t* rows, uint32_t* __restrict__ out) {
     constexpr int NW = SEL_MAXN / 32, NR = SEL_MAXN / 1024;
     static_assert(NW == 16 * 64 && NR == 32 && 2 * WSL_WSPEC == 64 && BT >= WSL_WMAX, "the fast path's shape");
+    static_assert(4 * NW + 2 * WSL_WMAX + 33 <= WSL_FIXED, "the fast path's words, its junk word included, within L");
     __shared__ uint32_t wsl_ok, wsl_tot, wsl_k, wsl_kt, wsl_sel[2];
     uint32_t* gts = L;                          // NW: keys above E
     uint32_t* eqs = L + NW;                     // NW: keys equal to E
@@ -327,12 +328,15 @@ __device__ __forceinline__ void wsel_slice(int n, int topk, const uint32_t* __re
             uint32_t incl = nv;
             incl = wave_scan_incl(incl);
             const uint32_t off = incl - nv;
+            // a lane's items past its count go to a junk word past the keys' padding, never read
+            // (unconditional stores: a store under a lane's own condition compiled to a branch each)
+            uint32_t* const junk = ck + WSL_WMAX + 32;
 #pragma unroll
-            for (int i = 0; i < 16; i++)
-                if (i < (int)nv) {
-                    ck[off + i] = cv[i >> 1][2 * (i & 1)];
-                    cj[off + i] = cv[i >> 1][2 * (i & 1) + 1] & (SEL_MAXN - 1);
-                }
+            for (int i = 0; i < 16; i++) {
+                const bool live = i < (int)nv;
+                *(live ? ck + off + i : junk) = cv[i >> 1][2 * (i & 1)];
+                *(live ? cj + off + i : junk) = cv[i >> 1][2 * (i & 1) + 1] & (SEL_MAXN - 1);
+            }
             if (lane < 16) ck[tot + lane] = 0;   // zero keys up to a multiple of 4 (and beyond)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
