@@ -627,7 +627,9 @@ __global__ __launch_bounds__(256, 4) void sparse_rows8_rm_kernel(SparseRows8Args
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int lo = __shfl_xor(st[t][i], GQ, 64);
+                // lo from lane n + GQ (DPP row_shl: lane i reads lane i + GQ of its row; only the
+                // lanes n < GQ use x)
+                const int lo = (int)dpp_u32<0x100 + GQ>((uint32_t)st[t][i]);
                 const float kq = t == 0 ? kq0[i] : kq1[i];
                 x[4 * t + i] = (float)(st[t][i] * 256 + lo) * kq;
             }
