@@ -69,8 +69,12 @@ int env_int(const char* name, int dflt) {
 /// (default 256, one a CU on MI355X), at most kMaxChunks a kv head, at least 128 keys (a 32-key
 /// tile for 4 of the 8 waves: short contexts gain from more workgroups), a multiple of 32. The reference's chunks8 makes the same choice for its GPU
 /// (Engine.swift:736-739).
-int decode_chunk(int S, int n_kv) {
-    static const int target = env_int("EMBLA_DECODE_WG", 256);
+int decode_chunk(int S, int n_kv, int extra = 0) {
+    static const int env_target = env_int("EMBLA_DECODE_WG", 256);
+    // extra: workgroups the launch adds (the decode step's appends); the chunks then leave them
+    // CUs with a sixteenth to spare, so that no workgroup waits for a CU (C3 step: 11.83 us a
+    // layer with 64 chunks a kv head + 4 appends, 11.15-11.17 with 57)
+    const int target = extra ? env_target * 15 / 16 - extra : env_target;
     int per_head = target / n_kv > 0 ? target / n_kv : 1;
     if (per_head > kMaxChunks) per_head = kMaxChunks;
     int ch = (S + per_head - 1) / per_head;
@@ -253,7 +257,7 @@ int embla_decode_step_int8(const void* qkv, int q_off, int k_off, int v_off, con
     if (pos < 0 || max_s <= 0 || max_s % 32 || pos >= max_s) return EMBLA_ERR_INVALID;
     if (n_kv <= 0 || n_q % n_kv || n_kv > kMaxKV) return EMBLA_ERR_INVALID;
     if (!valid_scale(scale_dtype) || !valid_act(out_dtype) || chunk < 0 || chunk % 32) return EMBLA_ERR_INVALID;
-    const int ch = pos == 0 ? 32 : chunk ? chunk : decode_chunk(pos, n_kv);
+    const int ch = pos == 0 ? 32 : chunk ? chunk : decode_chunk(pos, n_kv, n_kv);
     const int C = (pos + ch - 1) / ch;   // chunks over the cached keys 0 .. pos - 1
     if (C + 1 > kMaxChunks) return EMBLA_ERR_INVALID;
     if (!ws || ws_bytes < embla_workspace_bytes(max_s, n_q) || (size_t)(C + 1) * n_q * kPartStride * 4 > part_bytes(max_s, n_q))

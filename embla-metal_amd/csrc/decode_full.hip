@@ -165,69 +165,131 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
     // q as a 15-bit fixed point split into int8 halves, hi in qb and lo in ql: column n < GQ holds
     // head n (other columns 0); lane (n, g), MFMA b: dims 32g + 16b .. + 15 (the K slice's dims).
     // Separate operands put both halves' products in the lane that uses them (no cross-lane step).
-    auto setup_q = [&]() {
-        const int hn = n % GQ;
-        const bool live = n < GQ;
-        const uint16_t* qr = q + ((size_t)kvh * GQ + hn) * HD + 32 * g;
-        float qf[32];
-        float am = 0.0f;
+    // q's rows are requested before the first tile (loads complete in order: requested after the
+    // tile, q's wait would also wait for the tile, and the set-up would start only once the tile
+    // had arrived from HBM). The set-up splits the kv head's GQ rows over the wave: lane L takes
+    // head L / LPH, dims d0 .. d0 + VPL - 1 (a quarter of what a lane of the operand layout holds,
+    // where 16 lanes of a row repeat 4 heads), and hands the operands over through the wave's own
+    // slot of the merge LDS (free until its tiles are done).
+    constexpr int VPL = 2 * GQ, LPH = 64 / GQ, NQ = VPL / 8;
+    const int qhd = lane / LPH, d0 = VPL * (lane % LPH);
+    __shared__ __attribute__((aligned(16))) float om[DW][GQ][HD];
+    char* const qa = (char*)&om[w][0][0];
+    u4_t qraw[NQ], ga[QR ? NQ : 1], gb[QR ? NQ : 1];   // (QR: the head norm's gains)
+    auto load_q = [&]() {
+        const uint16_t* qr = q + ((size_t)kvh * GQ + qhd) * HD + d0;
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const u4_t r = ld16(qr + 8 * u);
+        for (int u = 0; u < NQ; u++) qraw[u] = ld16(qr + 8 * u);
+        if constexpr (QR) {   // no branch (a load under one made its join wait for every load)
+            const uint16_t* p1 = ng >= 1 ? g1 + d0 : qr;   // (a gain not given reads q's row, unused)
+            const uint16_t* p2 = ng >= 2 ? g2 + d0 : qr;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                qf[8 * u + 2 * i] = QR ? bf2f((uint16_t)(r[i] & 0xFFFF)) : h2f((uint16_t)(r[i] & 0xFFFF));
-                qf[8 * u + 2 * i + 1] = QR ? bf2f((uint16_t)(r[i] >> 16)) : h2f((uint16_t)(r[i] >> 16));
+            for (int u = 0; u < NQ; u++) {
+                ga[u] = ld16(p1 + 8 * u);
+                gb[u] = ld16(p2 + 8 * u);
             }
         }
+    };
+    // op over the LPH lanes of a head, as the butterfly over the head's dim pairs gives it: the
+    // pair p = GQ k + j of lane k, slot j; levels xor 32 .. GQ cross lanes (k), xor GQ / 2 .. 1 stay
+    // in the lane. The first cross-lane level exchanges exactly (GQ = 4: row_ror:8 is k ^ 8 in a
+    // 16-lane row; GQ = 8: k ^ 4 from row_shl:4 or row_shr:4), after which the lanes a rotation or
+    // quad_perm mixes agree, so every level pairs what the butterfly pairs.
+    auto head_lanes = [&](float v, auto op) -> float {
+        if constexpr (GQ == 4) {
+            v = op(v, dpp_f32<0x128>(v));   // k ^ 8
+            v = op(v, dpp_f32<0x124>(v));   // k ^ 4
+        } else {
+            const float up = dpp_f32<0x104>(v), dn = dpp_f32<0x114>(v);   // lane + 4, lane - 4
+            v = op(v, (lane & 4) ? dn : up);                               // k ^ 4
+        }
+        v = op(v, dpp_f32<0x4E>(v));   // k ^ 2
+        v = op(v, dpp_f32<0xB1>(v));   // k ^ 1
+        return v;
+    };
+    auto setup_q = [&]() {
+        float x[VPL];
+#pragma unroll
+        for (int u = 0; u < NQ; u++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t r = qraw[u][i];
+                x[8 * u + 2 * i] = QR ? bf2f((uint16_t)(r & 0xFFFF)) : h2f((uint16_t)(r & 0xFFFF));
+                x[8 * u + 2 * i + 1] = QR ? bf2f((uint16_t)(r >> 16)) : h2f((uint16_t)(r >> 16));
+            }
         if constexpr (QR) {
             // the head norm of common.metal:13-26 (q_prep's): x * rms * (1 + g1) * (1 + g2),
-            // rounded to bf16; the lane groups g = 0..3 hold dims 32 g .. 32 g + 31
+            // rounded to bf16, Σx² in rms_factor's butterfly over the dim pairs (2p, 2p + 1)
 #pragma clang fp contract(off)
-            const float rf = 1.0f / sqrtf(sumsq_grouped32(qf) / 128.0f + EPS32);
-            u4_t ga[4], gb[4];
+            float sp[GQ];
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                ga[u] = ng >= 1 ? ld16(g1 + 32 * g + 8 * u) : (u4_t){0, 0, 0, 0};
-                gb[u] = ng >= 2 ? ld16(g2 + 32 * g + 8 * u) : (u4_t){0, 0, 0, 0};
+            for (int j = 0; j < GQ; j++) {
+                const float a = x[2 * j] * x[2 * j], b = x[2 * j + 1] * x[2 * j + 1];
+                sp[j] = head_lanes(a + b, [](float u, float v) { return u + v; });
             }
 #pragma unroll
-            for (int d = 0; d < 32; d++) {
+            for (int m = GQ / 2; m >= 1; m >>= 1)
+#pragma unroll
+                for (int j = 0; j < m; j++) sp[j] = sp[j] + sp[j + m];
+            const float rf = 1.0f / sqrtf(sp[0] / 128.0f + EPS32);
+#pragma unroll
+            for (int d = 0; d < VPL; d++) {
                 const uint32_t wa = ga[d / 8][(d % 8) / 2], wb = gb[d / 8][(d % 8) / 2];
                 float gf = rf;
                 if (ng >= 1) gf = gf * (1.0f + bf2f((uint16_t)(d & 1 ? wa >> 16 : wa & 0xFFFF)));
                 if (ng >= 2) gf = gf * (1.0f + bf2f((uint16_t)(d & 1 ? wb >> 16 : wb & 0xFFFF)));
-                qf[d] = bf2f(f2bf(qf[d] * gf));
+                x[d] = bf2f(f2bf(x[d] * gf));
             }
         }
-        if constexpr (SCORES) {   // bf16 / fp16 q as fp16 (bf16 exact down to 2^-17)
+        const bool live = n < GQ;
+        if constexpr (SCORES) {   // bf16 / fp16 q as fp16 (bf16 exact down to 2^-17), [head][dim]
+#pragma unroll
+            for (int u = 0; u < NQ; u++) {
+                h8_t hv;
+#pragma unroll
+                for (int e = 0; e < 8; e++) hv[e] = (_Float16)x[8 * u + e];
+                *(h8_t*)(qa + (qhd * HD + d0 + 8 * u) * 2) = hv;
+            }
+            wave_lds_sync();
 #pragma unroll
             for (int j = 0; j < 4; j++)
-#pragma unroll
-                for (int e = 0; e < 8; e++) qh[j][e] = live ? (_Float16)qf[8 * j + e] : (_Float16)0.0f;
+                qh[j] = live ? *(const h8_t*)(qa + (n * HD + 32 * g + 8 * j) * 2) : (h8_t){};
             return;
         }
+        float am = 0.0f;
 #pragma unroll
-        for (int d = 0; d < 32; d++) am = fmaxf(am, fabsf(qf[d]));
-        am = max_rows(am);
+        for (int d = 0; d < VPL; d++) am = fmaxf(am, fabsf(x[d]));
+        am = head_lanes(am, [](float u, float v) { return fmaxf(u, v); });
         const float inv = am > 0.0f ? QFIX / am : 0.0f;
-        qsc = am / QFIX;
+        // hi bytes [head][dim] at qa, lo bytes after them, then each head's step
+        uint32_t wh[VPL / 4], wl[VPL / 4];
 #pragma unroll
-        for (int b = 0; b < 2; b++) {
+        for (int k = 0; k < VPL / 4; k++) {
+            wh[k] = 0;
+            wl[k] = 0;
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                uint32_t wh = 0, wl = 0;
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int qi = (int)rintf(qf[16 * b + 4 * k + e] * inv);
-                    const int hi = (qi + 128) >> 8, lo = qi - hi * 256;
-                    wh |= (uint32_t)((live ? hi : 0) & 0xFF) << (8 * e);
-                    wl |= (uint32_t)((live ? lo : 0) & 0xFF) << (8 * e);
-                }
-                qb[b][k] = (int)wh;
-                ql[b][k] = (int)wl;
+            for (int e = 0; e < 4; e++) {
+                const int qi = (int)rintf(x[4 * k + e] * inv);
+                const int hi = (qi + 128) >> 8, lo = qi - hi * 256;
+                wh[k] |= (uint32_t)(hi & 0xFF) << (8 * e);
+                wl[k] |= (uint32_t)(lo & 0xFF) << (8 * e);
             }
         }
+#pragma unroll
+        for (int k = 0; k < VPL / 4; k += 2) {
+            *(u2_t*)(qa + qhd * HD + d0 + 4 * k) = (u2_t){wh[k], wh[k + 1]};
+            *(u2_t*)(qa + GQ * HD + qhd * HD + d0 + 4 * k) = (u2_t){wl[k], wl[k + 1]};
+        }
+        float* const qs = (float*)(qa + 2 * GQ * HD);
+        if (lane % LPH == 0) qs[qhd] = am / QFIX;
+        wave_lds_sync();
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            qb[b] = live ? *(const i4_t*)(qa + n * HD + 32 * g + 16 * b) : (i4_t){0, 0, 0, 0};
+            ql[b] = live ? *(const i4_t*)(qa + GQ * HD + n * HD + 32 * g + 16 * b) : (i4_t){0, 0, 0, 0};
+        }
+        qsc = qs[n % GQ];
+        wave_lds_sync();   // (the slot is the merge's again only after every lane's reads)
     };
 
     auto load_k_scales = [&](int t0, Tile8& T) {
@@ -347,9 +409,10 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
                 }
                 m = mn;
             }
+            const float mr = m == NEG_INF ? 0.0f : m;   // no valid key yet (a wave with no tile): every p 0
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                const float p = __builtin_amdgcn_exp2f(x[e] - m);   // x = -inf -> 0; m finite once a key is valid
+                const float p = __builtin_amdgcn_exp2f(x[e] - mr);   // x = -inf -> 0
                 l += p;
                 wa[e] = (_Float16)(p * vs[e] * WSCALE);
             }
@@ -388,20 +451,37 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
         // the first tile: K and the scales, then V only after the q math. A thinner first burst
         // of requests measured faster than issuing the whole tile at once (10.49 against 11.15 µs
         // a launch at 32k)
-        if (t0 < j1) load_k_scales(t0, A);
+        // The first tile's loads take no branch (a wave without a tile reads the chunk's first,
+        // unused): under a branch, the compiler's wait for q at the join also waited for the tile
+        // (loads complete in order), and the q set-up ran only after the tile had arrived.
+        const int tf = t0 < j1 ? t0 : j0;
+        load_q();
+        __builtin_amdgcn_sched_barrier(0);   // q's requests first
+        load_k_scales(tf, A);
+        __builtin_amdgcn_sched_barrier(0);   // the scheduler keeps the tile's requests ahead of the set-up
+        // q's registers pass through an empty statement here, so no part of the set-up is hoisted
+        // above the tile's requests (its wait for q would then come first)
+#pragma unroll
+        for (int u = 0; u < NQ; u++) {
+            asm volatile("" : "+v"(qraw[u]));
+            if constexpr (QR) asm volatile("" : "+v"(ga[u]), "+v"(gb[u]));
+        }
         setup_q();
-        if (t0 < j1) {
-            const int8_t* pv = vc + tile_base(kvh, max_s, t0, 1) + lane * 16;
+        {
+            const int8_t* pv = vc + tile_base(kvh, max_s, tf, 1) + lane * 16;
 #pragma unroll
             for (int j = 0; j < 4; j++) A.v[j] = TLD(pv + 1024 * j);
         }
         // each tile's K (and K scales) for the next tile go out as soon as the score MFMAs have
-        // consumed them, its V (and V scales) after the P·V MFMAs: 10.41 -> 9.92 µs a launch at 32k
-        for (int t = t0; t < j1; t += step) compute_tile(t, A, t + step < j1 ? t + step : -1);
+        // consumed them, its V (and V scales) after the P·V MFMAs: 10.41 -> 9.92 µs a launch at 32k.
+        // The first tile runs outside the loop, whether or not the wave has one (t0 >= j1: every
+        // key masked): inside the loop's guard, the compiler sank the first tile's loads below the
+        // q set-up.
+        compute_tile(t0, A, t0 + step < j1 ? t0 + step : -1);
+        for (int t = t0 + step; t < j1; t += step) compute_tile(t, A, t + step < j1 ? t + step : -1);
     }
 
     // ---- merge the waves (LDS)
-    __shared__ __attribute__((aligned(16))) float om[DW][GQ][HD];
     __shared__ float mm[DW][GQ], ll[DW][GQ];
     l = sum_rows(l);
     if (g == 0 && n < GQ) { mm[w][n] = m; ll[w][n] = l; }
