@@ -24,10 +24,10 @@ constexpr int RPS = HD + 4;   // partial record stride, as decode_full.hip
 /// Prepared row (norm with gains, RoPE, bf16 rounding when PREOPS), dims 32g .. 32g + 31 of a head
 /// held by the 4 lanes n, n+16, n+32, n+48 (lane group g), as fp32 in x[32].
 template <bool BF, bool PREOPS>
-__device__ __forceinline__ void prep_row(const uint16_t* src, const uint16_t* gain, int g, int pos, float* x) {
+__device__ __forceinline__ void prep_row(const u4_t* raw, const uint16_t* gain, int g, int pos, float* x) {
 #pragma unroll
     for (int u = 0; u < 4; u++) {
-        const u4_t r = ld16(src + 32 * g + 8 * u);
+        const u4_t r = raw[u];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             x[8 * u + 2 * i] = a2f<BF>((uint16_t)(r[i] & 0xFFFF));
@@ -75,14 +75,22 @@ __global__ __launch_bounds__(256) void ring_decode_kernel(RingArgs a) {
     };
     constexpr int step = 32 * 4;
     const int tw = j0 + 32 * w;
+    // q's row is requested before the tiles (loads complete in order: after them, its wait would
+    // also wait for the tiles)
+    u4_t qraw[4];
+    {
+        const uint16_t* qr = a.q + (size_t)(kvh * GQ + (n < GQ ? n : 0)) * a.q_stride + 32 * g;
+#pragma unroll
+        for (int u = 0; u < 4; u++) qraw[u] = ld16(qr + 8 * u);
+    }
     if (tw < j1) load(tw, 0);
     if (tw + step < j1) load(tw + step, 1);
 
     // q^T, B operand: lane (head n, group g), MFMA u: dims 32g + 8u .. + 7
     u4_t qb[4];
-    {
+    if constexpr (PREOPS) {
         float x[32];
-        prep_row<BF, PREOPS>(a.q + (size_t)(kvh * GQ + (n < GQ ? n : 0)) * a.q_stride, a.qg, g, pos, x);
+        prep_row<BF, PREOPS>(qraw, a.qg, g, pos, x);
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             u4_t r;
@@ -91,6 +99,11 @@ __global__ __launch_bounds__(256) void ring_decode_kernel(RingArgs a) {
                 r[i] = (uint32_t)f2a<BF>(x[8 * u + 2 * i]) | ((uint32_t)f2a<BF>(x[8 * u + 2 * i + 1]) << 16);
             qb[u] = n < GQ ? r : (u4_t){0, 0, 0, 0};
         }
+    } else {
+        // the row's 16-bit values are the operand as they are; columns n >= GQ repeat head 0
+        // (finite, and no result reads them: heads are the rows below GQ)
+#pragma unroll
+        for (int u = 0; u < 4; u++) qb[u] = qraw[u];
     }
     const float sc = 0.08838834764831845f * RLOG2E;
     float m = NEG_INF, l = 0.0f;
@@ -175,8 +188,14 @@ __global__ __launch_bounds__(256) void ring_decode_kernel(RingArgs a) {
     // tiles, and its loads of the new rows overlap the other waves' tiles)
     if (c == a.C - 1 && w == 3) {
         float kx[32], vx[32];
-        prep_row<BF, PREOPS>(a.k_new + (size_t)kvh * HD, a.kg, g, pos, kx);
-        prep_row<BF, false>(a.v_new + (size_t)kvh * HD, nullptr, g, pos, vx);
+        u4_t kr[4], vr[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            kr[u] = ld16(a.k_new + (size_t)kvh * HD + 32 * g + 8 * u);
+            vr[u] = ld16(a.v_new + (size_t)kvh * HD + 32 * g + 8 * u);
+        }
+        prep_row<BF, PREOPS>(kr, a.kg, g, pos, kx);
+        prep_row<BF, false>(vr, nullptr, g, pos, vx);
         // q·k for head n: this lane's 32 dims, then the 4 lane groups
         float dot = 0.0f;
 #pragma unroll
