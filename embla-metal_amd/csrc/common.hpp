@@ -217,6 +217,20 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
+/// A 32-key tile's per-key scores from lane n = 0 of each row (lane group g): items e = 4t + i are
+/// keys 16t + 4g + i, i.e. at dst[16t + i] (dst: the tile's first key plus 4g). A full tile is two
+/// 16-byte stores; a partial one stores its valid keys one by one.
+__device__ __forceinline__ void store_scores(float* dst, const float* smx, const bool* valid, bool full, int n) {
+    if (n != 0) return;
+    if (full) {
+        *(f4_t*)dst = (f4_t){smx[0], smx[1], smx[2], smx[3]};
+        *(f4_t*)(dst + 16) = (f4_t){smx[4], smx[5], smx[6], smx[7]};
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            if (valid[e]) dst[16 * (e >> 2) + (e & 3)] = smx[e];
+    }
+}
 __device__ __forceinline__ uint32_t readlane_u32(uint32_t v, int l) { return (uint32_t)__builtin_amdgcn_readlane((int)v, l); }
 __device__ __forceinline__ float readlane(float v, int l) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));

@@ -352,20 +352,17 @@ __global__ __launch_bounds__(64 * DW, 2) void full_decode_kernel(
         for (int e = 0; e < 8; e++) valid[e] = full || t0 + 16 * (e >> 2) + 4 * g + (e & 3) < j1;
         if constexpr (SCORES) {
             // max over the kv head's query heads of the dequantised q·k (attention.metal:295-305)
+            // (lane n = 0 of each row takes it: lane xor 1, xor 2 by quad_perm, then lane + 4 by
+            // row_shl, no LDS round trip; heads n >= GQ hold -inf)
             float smx[8];
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 float v = n < GQ ? x[e] : NEG_INF;
-                v = fmaxf(v, shfl_xor(v, 1));
-                v = fmaxf(v, shfl_xor(v, 2));
-                v = fmaxf(v, shfl_xor(v, 4));
-                smx[e] = v;
+                v = fmaxf(v, dpp_f32<0xB1>(v));
+                v = fmaxf(v, dpp_f32<0x4E>(v));
+                smx[e] = fmaxf(v, dpp_f32<0x104>(v));
             }
-            if (n == 0) {
-#pragma unroll
-                for (int e = 0; e < 8; e++)
-                    if (valid[e]) scores[(size_t)kvh * max_s + t0 + 16 * (e >> 2) + 4 * g + (e & 3)] = smx[e];
-            }
+            store_scores(scores + (size_t)kvh * max_s + t0 + 4 * g, smx, valid, full, n);
         }
         h8_t wa;
         if constexpr (RELU2) {

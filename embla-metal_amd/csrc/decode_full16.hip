@@ -124,19 +124,17 @@ __global__ __launch_bounds__(256) void full16_decode_kernel(Full16Args a) {
             }
         }
         if constexpr (SCORES) {   // max over the kv head's query heads of the raw q·k
+            // (lane n = 0 of each row takes it: lane xor 1, xor 2 by quad_perm, then lane + 4 by
+            // row_shl, no LDS round trip; heads n >= GQ hold -inf)
             float smx[8];
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 float v = n < GQ ? x[e] : NEG_INF;
-#pragma unroll
-                for (int msk = 1; msk < GQ; msk <<= 1) v = fmaxf(v, shfl_xor(v, msk));
-                smx[e] = v;
+                v = fmaxf(v, dpp_f32<0xB1>(v));
+                v = fmaxf(v, dpp_f32<0x4E>(v));
+                smx[e] = fmaxf(v, dpp_f32<0x104>(v));
             }
-            if (n == 0) {
-#pragma unroll
-                for (int e = 0; e < 8; e++)
-                    if (valid[e]) a.scores[(size_t)kvh * a.max_s + t0 + 16 * (e >> 2) + 4 * g + (e & 3)] = smx[e];
-            }
+            store_scores(a.scores + (size_t)kvh * a.max_s + t0 + 4 * g, smx, valid, t0 + 32 <= j1, n);
         }
         float p[8];
         if constexpr (RELU2) {
