@@ -405,14 +405,24 @@ __global__ __launch_bounds__(256) void index_scores_kernel(const uint16_t* __res
                                                            const uint16_t* __restrict__ ki, float* __restrict__ scores,
                                                            int n, uint32_t* __restrict__ sw) {
     __shared__ uint32_t lh[DB];
+    const int lane = threadIdx.x & 63, kq = lane & 7;
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6), nwaves = gridDim.x * 4;
+    // a block's keys, load j: keys 8j .. 8j + 7, lane l: key 8j + l / 8, dims 8 (l % 8) ..; keys
+    // past n read key n - 1 (no branch; their scores are neither stored nor counted)
+    u4_t raw[8];
+    auto load_keys = [&](int base) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) raw[j] = ld16(ki + (size_t)min(base + 8 * j + (lane >> 3), n - 1) * 64 + 8 * kq);
+    };
+    // the first block's keys are requested before anything else (a wave has one block at up to
+    // 262144 keys): the histogram clear, its barrier and the queries' loads run under them
+    load_keys(wave * 64);
     uint32_t epoch = 0;
     if (sw) {
         epoch = sw[2 * HWORDS + 3];
         for (int b = threadIdx.x; b < DB; b += 256) lh[b] = 0;
         __syncthreads();
     }
-    const int lane = threadIdx.x & 63, kq = lane & 7;
-    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6), nwaves = gridDim.x * 4;
     float q[NIH][8], w[NIH];
 #pragma unroll
     for (int h = 0; h < NIH; h++) {
@@ -425,12 +435,7 @@ __global__ __launch_bounds__(256) void index_scores_kernel(const uint16_t* __res
         w[h] = wt[h];
     }
     for (int base = wave * 64; base < n; base += nwaves * 64) {
-        u4_t raw[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int key = base + 8 * j + (lane >> 3);
-            raw[j] = key < n ? ld16(ki + (size_t)key * 64 + 8 * kq) : (u4_t){0, 0, 0, 0};
-        }
+        if (base != wave * 64) load_keys(base);
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             float kf[8];
