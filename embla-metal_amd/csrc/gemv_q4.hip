@@ -71,6 +71,10 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(GemvArgs a) {
                 sc[u][sp] = bf2f(*(const uint16_t*)(W + sg.s + (r * gpr + 32 * sp + lane / 2) * 2));
                 bi[u][sp] = bf2f(*(const uint16_t*)(W + sg.b + (r * gpr + 32 * sp + lane / 2) * 2));
             }
+    // EPI 2 (+= into fp32): the residual of the lane's row (lanes >= RW: the wave's first row,
+    // unused) is requested with the weights, not as a round trip after the products
+    float yprev = 0.0f;
+    if constexpr (EPI == 2) yprev = ((const float*)a.Y)[sg.y + (size_t)(r0 + (lane < RW ? lane : 0))];
     // x: the lane's 32 columns of each span as bf16 pairs (8j + k, 8j + k + 4), and their sum.
     // Paired once a workgroup, in staging: thread t pairs the 8 columns 8t .. 8t + 7 of each span
     // and sums them (its 4 waves' rows share one segment: segment ends are multiples of 4 rows),
@@ -136,7 +140,7 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(GemvArgs a) {
         else if constexpr (EPI == 1) {
             const float t = fmaxf(bf2f(f2bf(v)), 0.0f);
             ((uint16_t*)a.Y)[at] = f2bf(t * t);
-        } else if constexpr (EPI == 2) ((float*)a.Y)[at] += bf2f(f2bf(v));
+        } else if constexpr (EPI == 2) ((float*)a.Y)[at] = yprev + bf2f(f2bf(v));
         else if constexpr (EPI == 3) ((float*)a.Y)[at] = bf2f(f2bf(v));
         else ((float*)a.Y)[at] = v;
     }
