@@ -13,7 +13,8 @@
 // words = 16 nibbles, dequantised as s * q + b in fp32, rounded to bf16 by v_cvt_pk_bf16_f32)
 // into double-buffered LDS (rows padded to 144 bytes: the 16-byte operand
 // reads of 32 lanes land in distinct banks). A step's global loads go out two steps ahead (two
-// register stages); one barrier a step.
+// register stages); one barrier a step. The += epilogue's fp32 residual is read before the first
+// step, so those reads overlap the products.
 #include "common.hpp"
 #include "embla_internal.hpp"
 
@@ -120,6 +121,22 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_kernel(GemmArgs a) {
     // loads past the last step repeat it and their stores go to a buffer no one reads again, so a
     // step's products and the next step's dequantisation share one block for the scheduler.
     const int last = QK * (steps - 1);
+    // EPI 2 (+=): the residual's items are requested first, so that their reads overlap the
+    // products instead of following them
+    float yp[EPI == 2 ? 2 : 1][EPI == 2 ? J : 1][16];
+    if constexpr (EPI == 2) {
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < J; j++) {
+                const int n = min(n0 + wn + 32 * j + fr, a.O - 1);
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int m = min(m0 + wm + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3), a.T - 1);
+                    yp[i][j][e] = ((const float*)a.Y)[(size_t)m * a.ldy + n];
+                }
+            }
+    }
     load(0, R0);
     load(min(QK, last), R1);
     store(0, R0);
@@ -154,7 +171,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_kernel(GemmArgs a) {
                 else if constexpr (EPI == 1) {
                     const float t = fmaxf(bf2f(f2bf(v)), 0.0f);
                     ((uint16_t*)a.Y)[at] = f2bf(t * t);
-                } else if constexpr (EPI == 2) ((float*)a.Y)[at] += bf2f(f2bf(v));
+                } else if constexpr (EPI == 2) ((float*)a.Y)[at] = yp[i][j][e] + bf2f(f2bf(v));
                 else if constexpr (EPI == 3) ((float*)a.Y)[at] = bf2f(f2bf(v));
                 else ((float*)a.Y)[at] = v;
             }
