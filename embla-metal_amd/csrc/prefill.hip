@@ -66,6 +66,9 @@ constexpr int PPH = 68;
 #endif
 constexpr int PF_WAVES = 8;        // waves a workgroup: GQ query heads x (8 / GQ) 32-row blocks
 #ifndef PF_XCD
+#ifndef PF_FOLD
+#define PF_FOLD 1
+#endif
 #define PF_XCD 1                   // workgroups of one (kv head, split) spread over one XCD
 #endif
 int launch_prefill_tail(const PrefillArgs& a, hipStream_t st);
@@ -325,6 +328,12 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
     }
 
     float m = NEG_INF, lsum = 0.0f;
+    // FOLD: the score chains subtract the running maximum themselves, by a ninth k-step of a ones
+    // column (A) against -m (B, lane half 0, k 0), so the weights need no v_sub. m is then kept
+    // exactly representable in fp16 (any shift of a row's scores leaves its softmax unchanged).
+    constexpr bool FOLD = PF_FOLD && !RELU2 && !BF && (!RING || LIN);
+    const u4_t kone = {h ? 0u : 0x3C00u, 0u, 0u, 0u};   // fp16 1.0 at k 0
+    u4_t qm = {0u, 0u, 0u, 0u};                          // -m (0 while the row has no key)
     f16_t O[4];
 #pragma unroll
     for (int i = 0; i < 4; i++)
@@ -383,8 +392,15 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
             {
                 const u4_t* k0r = (const u4_t*)(sm.k[b] + (32 * kb0 + r) * KROW) + h;
                 const u4_t* k1r = k0r + 32 * KROW / 8;
-                s0 = mfma32x<BF>(k0r[0], qb[0], (f16_t){});
-                s1 = mfma32x<BF>(k1r[0], qb[0], (f16_t){});
+                if constexpr (FOLD) {
+                    s0 = mfma32x<false>(kone, qm, (f16_t){});
+                    s1 = mfma32x<false>(kone, qm, (f16_t){});
+                    s0 = mfma32x<BF>(k0r[0], qb[0], s0);
+                    s1 = mfma32x<BF>(k1r[0], qb[0], s1);
+                } else {
+                    s0 = mfma32x<BF>(k0r[0], qb[0], (f16_t){});
+                    s1 = mfma32x<BF>(k1r[0], qb[0], (f16_t){});
+                }
 #pragma unroll
                 for (int s = 1; s < 8; s++) {
                     s0 = mfma32x<BF>(k0r[2 * s], qb[s], s0);
@@ -408,7 +424,37 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
                 }
             }
             float msub = 0.0f;
-            if constexpr (!RELU2) {
+            if constexpr (FOLD) {
+                // x = score - m already (m = 0 for a row with no key yet)
+                float ma = vmax3(x[0], x[1], x[2]), mb = vmax3(x[16], x[17], x[18]);
+#pragma unroll
+                for (int e = 3; e < 15; e += 2) {
+                    ma = vmax3(ma, x[e], x[e + 1]);
+                    mb = vmax3(mb, x[16 + e], x[17 + e]);
+                }
+                const float mt = max_xor32(vmax3(vmax3(ma, mb, x[15]), x[31], x[31]));
+                const bool fresh = m == NEG_INF;
+                // a row's first keys set m; later, m moves only when a row's scores exceed it by
+                // more than 2^8: weights stay <= 256 (fp16-safe), O and l share the stale m
+                if (__any(mt > 8.0f || (fresh && mt > NEG_INF))) {
+                    const float meff = fresh ? 0.0f : m;
+                    const float top = meff + mt;   // the row's largest score of the pair
+                    float mn = fresh ? top : fmaxf(m, top);
+                    mn = mn == NEG_INF ? NEG_INF : (float)(_Float16)mn;
+                    const float corr = fresh ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
+                    lsum *= corr;
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+#pragma unroll
+                        for (int e = 0; e < 16; e++) O[i][e] *= corr;
+                    const float d = mn == NEG_INF ? 0.0f : mn - meff;   // re-base this pair's x
+#pragma unroll
+                    for (int e = 0; e < 32; e++) x[e] -= d;
+                    m = mn;
+                    const _Float16 nm = (_Float16)(mn == NEG_INF ? 0.0f : -mn);
+                    qm[0] = h ? 0u : (uint32_t)__builtin_bit_cast(uint16_t, nm);
+                }
+            } else if constexpr (!RELU2) {
                 // two max3 chains over the 32 scores, then across the row's two lanes
                 float ma = vmax3(x[0], x[1], x[2]), mb = vmax3(x[16], x[17], x[18]);
 #pragma unroll
@@ -438,7 +484,8 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
                     const float t = fmaxf(v, 0.0f);
                     return t * t;
                 } else {
-                    return __builtin_amdgcn_exp2f(RING && !LIN ? __builtin_fmaf(v, c, -msub) : v - msub);
+                    if constexpr (FOLD) return __builtin_amdgcn_exp2f(v);
+                    else return __builtin_amdgcn_exp2f(RING && !LIN ? __builtin_fmaf(v, c, -msub) : v - msub);
                 }
             };
             float pw[16];
