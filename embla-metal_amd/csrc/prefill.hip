@@ -332,7 +332,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
     // column (A) against -m (B, lane half 0, k 0), so the weights need no v_sub. m is then kept
     // exactly representable in fp16 (any shift of a row's scores leaves its softmax unchanged).
     // Its range is fp16's: scores up to 65504 in log2 units (about 45,400 before the 1/sqrt(d)
-    // scale), as the operands, already fp16, bound them in practice.
+    // scale); the layers' q and k are RMS-normed a head, which keeps scores far below that.
     constexpr bool FOLD = PF_FOLD && !RELU2 && !BF && (!RING || LIN);
     const u4_t kone = {h ? 0u : 0x3C00u, 0u, 0u, 0u};   // fp16 1.0 at k 0
     u4_t qm = {0u, 0u, 0u, 0u};                          // -m (0 while the row has no key)
