@@ -29,8 +29,9 @@
 namespace embla {
 
 __device__ __forceinline__ uint32_t ob32(float f) {
+    // negative: every bit flipped; otherwise the sign bit set (an arithmetic shift, an or, a xor)
     const uint32_t u = __float_as_uint(f);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
 }
 __device__ __forceinline__ float ob_to_float(uint32_t o) {
     return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
@@ -97,20 +98,32 @@ __global__ __launch_bounds__(256) void index_mfma_kernel(IndexMfmaArgs a) {
             ss = sum_xor32(ss);
             nmax = fmaxf(nmax, ss);
         }
+        auto score = [&](int rt, int b) {
+            float sc = 0.0f;
+            const f4_t wv = wl[8 * IXRT * w + 8 * rt + 2 * b + hh];
 #pragma unroll
-        for (int rt = 0; rt < IXRT; rt++)
-#pragma unroll
-            for (int b = 0; b < 4; b++) {
-                float sc = 0.0f;
-                const f4_t wv = wl[8 * IXRT * w + 8 * rt + 2 * b + hh];
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float r = vmax2(d[rt][4 * b + i], 0.0f);
-                    sc = __builtin_fmaf(wv[i], r * r, sc);
-                }
-                const int row = r0 + 8 * rt + 2 * b + hh;
-                if (row < a.T) a.keys[(size_t)row * a.ld + key] = key < row + a.lim0 ? (uint16_t)(ob32(sc) >> 16) : 0;
+            for (int i = 0; i < 4; i++) {
+                const float r = vmax2(d[rt][4 * b + i], 0.0f);
+                sc = __builtin_fmaf(wv[i], r * r, sc);
             }
+            return (uint16_t)(ob32(sc) >> 16);
+        };
+        // (uniform) every row of the wave exists and sees every key of the block: no per-key tests
+        if (r0 + 8 * IXRT <= a.T && kb + 32 <= r0 + a.lim0) {
+#pragma unroll
+            for (int rt = 0; rt < IXRT; rt++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) a.keys[(size_t)(r0 + 8 * rt + 2 * b + hh) * a.ld + key] = score(rt, b);
+        } else {
+#pragma unroll
+            for (int rt = 0; rt < IXRT; rt++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    const int row = r0 + 8 * rt + 2 * b + hh;
+                    const uint16_t v = score(rt, b);
+                    if (row < a.T) a.keys[(size_t)row * a.ld + key] = key < row + a.lim0 ? v : 0;
+                }
+        }
     }
     if (norms) {
         nmax = wave_bfly(nmax, [](float x, float y) { return fmaxf(x, y); });
