@@ -481,10 +481,17 @@ __global__ __launch_bounds__(256) void sparse_rows8_kernel(SparseRows8Args a) {
 /// scores are exact integers times the fixed point's step. A lane (head n, group g) of the score
 /// tile holds keys {16t + 4g + i}, the A-operand slice of O += W V; it gathers those 8 keys' V
 /// bytes for dims 8n .. 8n + 7 (8 bytes a key, a row's 128 bytes over 16 lanes) and transposes
-/// them into the fp16 B operand in registers. The next step's K gather is in flight during this
-/// step's products, its V gather from the end of this step's.
+/// them into the fp16 B operand in registers. K goes through a per-wave LDS tile, gathered as
+/// whole rows; as soon as a step's K is in the tile, the next step's K and V rows are requested, so
+/// both are in flight through this whole step.
+// three workgroups a CU (<= 168 VGPRs): room for the next step's V rows in flight beside this
+// step's (C5 sparse layer 0.403 ms at four with the V rows requested at a step's end, 0.380 at three,
+// 0.374 with them a step ahead)
+#ifndef SPR_OCC
+#define SPR_OCC 3
+#endif
 template <int GQ>
-__global__ __launch_bounds__(256, 4) void sparse_rows8_rm_kernel(SparseRows8Args a) {
+__global__ __launch_bounds__(256, SPR_OCC) void sparse_rows8_rm_kernel(SparseRows8Args a) {
     typedef int i4_t __attribute__((ext_vector_type(4)));
     constexpr float QFIX = 32000.0f;   // |q_int| <= 32000: |hi| <= 125
     const int c = blockIdx.x, kvh = blockIdx.y, r = blockIdx.z;
@@ -504,6 +511,11 @@ __global__ __launch_bounds__(256, 4) void sparse_rows8_rm_kernel(SparseRows8Args
     __shared__ __attribute__((aligned(16))) char smem[MERGE];
     __shared__ __attribute__((aligned(16))) uint32_t sidx[SPR_MAXSEL];   // the key list, padded with row 0
     __shared__ __attribute__((aligned(16))) float sks[4][2][32];   // per wave: k scales, v scales
+    // a step's K rows, gathered whole (8 lanes a 128-byte row, 8 keys a load: each cache line once,
+    // where the MFMA's A layout would touch each twice, 64 bytes at a time), in a per-wave tile:
+    // 16-byte piece p of key j at slot p ^ ((j >> 1) & 7), so that the A-layout reads (16 lanes,
+    // 16 keys, one piece) fall in distinct bank groups
+    __shared__ __attribute__((aligned(16))) u4_t kt[4][32][8];
 
     // the key list: every load issued before the first store (rows clamped in range)
     const uint32_t* rows = sel ? a.idx + (size_t)r * a.idx_row_stride + (size_t)kvh * a.idx_kv_stride : nullptr;
@@ -586,13 +598,10 @@ __global__ __launch_bounds__(256, 4) void sparse_rows8_rm_kernel(SparseRows8Args
     // 16(e / 4) + 4g + e % 4, dims 8n .. 8n + 7; lanes < 32 hold key t0 + lane's two scales
     struct Raw { u4_t k[4]; u2_t v[8]; uint32_t s; };
     // rows as 32-bit byte offsets from the kv head's base (< 2^31: max_s * 128 a head)
-    auto gather_k = [&](int t0, Raw& R) {
+    auto gather_k = [&](int t0, Raw& R) {   // k[i]: key 8i + lane / 8, bytes 16 (lane % 8) .. + 15
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
-            const uint32_t off = sidx[t0 + 16 * t + n] * (uint32_t)HD + 16 * g;
-#pragma unroll
-            for (int h = 0; h < 2; h++) R.k[2 * t + h] = ld16(kb + off + 64 * h);
-        }
+        for (int i = 0; i < 4; i++)
+            R.k[i] = ld16(kb + sidx[t0 + 8 * i + (lane >> 3)] * (uint32_t)HD + 16 * (lane & 7));
         const uint32_t row = sidx[t0 + (lane & 31)];
         R.s = lane < 32 ? ksc[row] : vsc[row];
     };
@@ -601,20 +610,36 @@ __global__ __launch_bounds__(256, 4) void sparse_rows8_rm_kernel(SparseRows8Args
 #pragma unroll
         for (int e = 0; e < 8; e++) R.v[e] = ld8(vb + (e < 4 ? ra[e] : rb[e - 4]) * (uint32_t)HD + 8 * n);
     };
-    Raw A;
+    Raw A, Bv;   // Bv: the next step's V rows, requested a step ahead
     if (32 * w < nk) { gather_k(32 * w, A); gather_v(32 * w, A); }
     for (int t0 = 32 * w; t0 < nk; t0 += 128) {
         // scales to LDS: k scale of key j at [0][j], v scale (x 64) at [1][j]
         sks[w][lane >> 5][lane & 31] = lane < 32 ? h2f((uint16_t)A.s) : 64.0f * h2f((uint16_t)A.s);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int j = 8 * i + (lane >> 3);
+            kt[w][j][(lane & 7) ^ ((j >> 1) & 7)] = A.k[i];
+        }
+        // the K registers are free again: the next step's K and V are requested now, a step ahead
+        if (t0 + 128 < nk) {
+            gather_k(t0 + 128, A);
+            gather_v(t0 + 128, Bv);
+        }
         wave_lds_sync();
         i4_t st[2];
 #pragma unroll
         for (int t = 0; t < 2; t++) {
+            // A operands: key 16t + n, dims 64h + 16g .. + 15
+            u4_t ka[2];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int j = 16 * t + n;
+                ka[h] = kt[w][j][(4 * h + g) ^ ((j >> 1) & 7)];
+            }
             st[t] = (i4_t){0, 0, 0, 0};
-            st[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i4_t, A.k[2 * t]), qb[0], st[t], 0, 0, 0);
-            st[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i4_t, A.k[2 * t + 1]), qb[1], st[t], 0, 0, 0);
+            st[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i4_t, ka[0]), qb[0], st[t], 0, 0, 0);
+            st[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i4_t, ka[1]), qb[1], st[t], 0, 0, 0);
         }
-        if (t0 + 128 < nk) gather_k(t0 + 128, A);   // in flight during the products
         const f4_t kq0 = *(const f4_t*)(&sks[w][0][4 * g]), kq1 = *(const f4_t*)(&sks[w][0][16 + 4 * g]);
         const f4_t vq0 = *(const f4_t*)(&sks[w][1][4 * g]), vq1 = *(const f4_t*)(&sks[w][1][16 + 4 * g]);
         float x[8];
@@ -681,7 +706,8 @@ __global__ __launch_bounds__(256, 4) void sparse_rows8_rm_kernel(SparseRows8Args
             }
             O[u] = mfma16(wa, __builtin_bit_cast(h8_t, b), O[u]);
         }
-        if (t0 + 128 < nk) gather_v(t0 + 128, A);
+#pragma unroll
+        for (int e = 0; e < 8; e++) A.v[e] = Bv.v[e];
         wave_lds_sync();   // the next step's scale stores come after every lane's reads
     }
 
