@@ -42,13 +42,15 @@ typedef _Float16 h8v_t __attribute__((ext_vector_type(8)));
 // ------------------------------------------------------------------ 1. approximate scores (MFMA)
 /// Workgroup (64-row block rb, key chunk ch), 4 waves; wave w takes rows 64 rb + 16 w .. + 15 as
 /// two A tiles (8 rows × 4 index heads each) and sweeps every key of the chunk 32 at a time, so a
-/// key fragment feeds two MFMAs and the workgroup's waves read the same keys (L1 hits after the
-/// first). A tile: A row R = 4ρ + h (row ρ, index head h), lane l: R = l % 32, dims 16 s + 8 (l / 32)
+/// key fragment feeds two MFMAs; the workgroup's waves share each block's keys through an LDS
+/// tile that they load together. A tile: A row R = 4ρ + h (row ρ, index head h), lane l: R = l % 32, dims 16 s + 8 (l / 32)
 /// .. + 7 of k-step s. B: lane l: key l % 32, the same dims. D lane (key l % 32, half hh = l / 32)
 /// item e: A row 8 (e / 4) + 4 hh + e % 4, i.e. row ρ = 2 (e / 4) + hh, head e % 4: the 4 heads of
 /// a (row, key) score sit in one lane.
-// 8-row MFMA row tiles a wave (8 rows x 4 heads each): 16 rows a wave; 32 rows (4 tiles, half the
-// key loads an MFMA) measured the same, so the key loads are not what bounds this kernel
+// 8-row MFMA row tiles a wave (8 rows x 4 heads each): 16 rows a wave. What bounded this kernel
+// was the vector memory unit's address work (busy 61% of its cycles) on the key loads: each wave
+// loaded its keys in the B layout, 16 bytes of a 128-byte row a lane, every row four times; loaded
+// whole into the shared tile, each row is requested once a workgroup (90 -> 68 us a C5 chunk)
 constexpr int IXRT = 2;
 __global__ __launch_bounds__(256) void index_mfma_kernel(IndexMfmaArgs a) {
     const int rb = blockIdx.x, ch = blockIdx.y;
@@ -59,6 +61,12 @@ __global__ __launch_bounds__(256) void index_mfma_kernel(IndexMfmaArgs a) {
     // the 4 head weights of the workgroup's rows, in LDS (in registers, 16 a row tile: 148 against
     // 117 VGPRs, and 88-91 against 81-84 us a C5 chunk)
     __shared__ f4_t wl[32 * IXRT];
+    // a block's 32 key rows (128 bytes each) in a workgroup tile, double-buffered: wave w loads
+    // rows 8w .. 8w + 7 whole, 8 lanes a row (each cache line once a workgroup, where each wave's
+    // B-layout loads touched it four times, 16 bytes at a time), the next block's rows in flight
+    // during this block's products; one barrier a block. 16-byte piece p of key j sits at slot
+    // p ^ ((j >> 1) & 7), so the B-layout reads (16 lanes, 16 keys, one piece) are conflict-free.
+    __shared__ __attribute__((aligned(16))) u4_t kts[2][32][8];
     for (int i = tid; i < 32 * IXRT; i += 256) {
         const int rw = min(32 * IXRT * rb + i, a.T - 1);
         wl[i] = (f4_t){a.w[rw * 4], a.w[rw * 4 + 1], a.w[rw * 4 + 2], a.w[rw * 4 + 3]};
@@ -74,11 +82,24 @@ __global__ __launch_bounds__(256) void index_mfma_kernel(IndexMfmaArgs a) {
     const int k0 = ch * a.kchunk, k1 = min(a.ld, k0 + a.kchunk);
     const bool norms = rb == 0 && w == 0;   // one wave a chunk takes the key norms
     float nmax = 0.0f;
-    for (int kb = k0; kb < k1; kb += 32) {
+    auto load_rows = [&](int kb) {   // wave w's share of block kb: row 8w + lane / 8, piece lane % 8
+        const int kj = kb + 8 * w + (lane >> 3);
+        return kj < a.nk ? ld16(a.ki + (size_t)kj * 64 + 8 * (lane & 7)) : (u4_t){0, 0, 0, 0};
+    };
+    u4_t nx = {0, 0, 0, 0};
+    if (k0 < k1) nx = load_rows(k0);
+    int it = 0;
+    for (int kb = k0; kb < k1; kb += 32, it++) {
         const int key = kb + c;
-        u4_t kr[4];
+        u4_t kr[4];   // key c, dims 16s + 8hh .. + 7: the B operand of k-step s
+        {
+            const int j = 8 * w + (lane >> 3);
+            kts[it & 1][j][(lane & 7) ^ ((j >> 1) & 7)] = nx;
+            __syncthreads();
+            if (kb + 32 < k1) nx = load_rows(kb + 32);
 #pragma unroll
-        for (int s = 0; s < 4; s++) kr[s] = key < a.nk ? ld16(a.ki + (size_t)key * 64 + 16 * s + 8 * hh) : (u4_t){0, 0, 0, 0};
+            for (int s = 0; s < 4; s++) kr[s] = kts[it & 1][c][(2 * s + hh) ^ ((c >> 1) & 7)];
+        }
         f16_t d[IXRT] = {};
 #pragma unroll
         for (int s = 0; s < 4; s++)
