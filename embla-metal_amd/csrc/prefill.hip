@@ -592,40 +592,45 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void prefill_int8_kernel(PrefillA
 /// 8 rows a workgroup: rows (blockIdx.x * 8 + tid / 32) of head blockIdx.y.
 template <bool RELU2, bool OBF>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
-    const int lane = threadIdx.x & 31, tok = blockIdx.x * 8 + (threadIdx.x >> 5), hq = blockIdx.y;
+    // 16 lanes a (token, head): 8 dims a lane, one 16-byte load of a split's O / l record
+    const int lane = threadIdx.x & 15, tok = blockIdx.x * 16 + (threadIdx.x >> 4), hq = blockIdx.y;
     if (tok >= a.T) return;
     float M = RELU2 ? 0.0f : NEG_INF, mz[4], lz[4];
-    u2_t v[4];
+    u4_t v[4];
 #pragma unroll
     for (int z = 0; z < 4; z++) {
         if (z < a.nsplit) {
             const float* pp = a.part + (((size_t)z * a.T + tok) * a.n_q + hq) * PPH;
-            v[z] = ld8((const uint16_t*)pp + 4 * lane);   // O / l, fp16
+            v[z] = ld16((const uint16_t*)pp + 8 * lane);   // O / l, fp16
             const u2_t ml = ld8(pp + HD / 2);
             mz[z] = __uint_as_float(ml[0]);
             lz[z] = __uint_as_float(ml[1]);
             if constexpr (!RELU2) M = fmaxf(M, mz[z]);
         }
     }
-    float L = 0.0f, acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float L = 0.0f, acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int z = 0; z < 4; z++) {
         if (z < a.nsplit) {
             // split z's share: its l, rescaled to the common maximum
             const float f = lz[z] * (RELU2 ? 1.0f : (mz[z] == NEG_INF ? 0.0f : exp2f(mz[z] - M)));
             L += f;
-            acc[0] += h2f((uint16_t)(v[z][0] & 0xFFFF)) * f;
-            acc[1] += h2f((uint16_t)(v[z][0] >> 16)) * f;
-            acc[2] += h2f((uint16_t)(v[z][1] & 0xFFFF)) * f;
-            acc[3] += h2f((uint16_t)(v[z][1] >> 16)) * f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) acc[i] += h2f((uint16_t)(v[z][i / 2] >> (16 * (i & 1)))) * f;
         }
     }
     const float inv = RELU2 ? 1.0f / (11.313708498984761f + L) : 1.0f / L;
     uint16_t* orow = a.o + (size_t)tok * a.o_tok_stride + (size_t)hq * a.o_head_stride;
-    u2_t pk;
-    pk[0] = (uint32_t)f2a<OBF>(acc[0] * inv) | ((uint32_t)f2a<OBF>(acc[1] * inv) << 16);
-    pk[1] = (uint32_t)f2a<OBF>(acc[2] * inv) | ((uint32_t)f2a<OBF>(acc[3] * inv) << 16);
-    *(u2_t*)(orow + 4 * lane) = pk;
+    u4_t pk;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        pk[i] = (uint32_t)f2a<OBF>(acc[2 * i] * inv) | ((uint32_t)f2a<OBF>(acc[2 * i + 1] * inv) << 16);
+    if (((uintptr_t)orow & 15) == 0) {
+        *(u4_t*)(orow + 8 * lane) = pk;
+    } else {   // a token or head stride that breaks 16-byte alignment (4-byte aligned always)
+        *(u2_t*)(orow + 8 * lane) = (u2_t){pk[0], pk[1]};
+        *(u2_t*)(orow + 8 * lane + 4) = (u2_t){pk[2], pk[3]};
+    }
 }
 
 int launch_prefill_int8(const PrefillArgs& a, hipStream_t st) {
@@ -722,7 +727,7 @@ int launch_prefill_prestaged(const PrefillArgs& a0, uint16_t* k16, uint16_t* v16
 
 int launch_prefill_tail(const PrefillArgs& a, hipStream_t st) {
     if (a.nsplit > 1) {
-        const dim3 mg((a.T + 7) / 8, a.n_q);
+        const dim3 mg((a.T + 15) / 16, a.n_q);
         if (a.relu2) hipLaunchKernelGGL((prefill_merge_kernel<true, true>), mg, dim3(256), 0, st, a);
         else if (a.out_bf16) hipLaunchKernelGGL((prefill_merge_kernel<false, true>), mg, dim3(256), 0, st, a);
         else hipLaunchKernelGGL((prefill_merge_kernel<false, false>), mg, dim3(256), 0, st, a);
