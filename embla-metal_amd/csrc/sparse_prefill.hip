@@ -20,7 +20,7 @@
 //     is therefore the spec's. The ordered compaction then writes the indices in select_keys'
 //     order. A band too large to list (scores massed at the k-th value) is left to
 //     band_overflow_kernel, which scores it once into LDS and ranks it there.
-//  3. sparse_rows8_kernel (decode_sparse.hip): gathered attention over a row-major int8 cache.
+//  3. sparse_rows8_rm_kernel (decode_sparse.hip): gathered attention over a row-major int8 cache.
 #include "common.hpp"
 #include "embla_internal.hpp"
 
