@@ -479,17 +479,18 @@ __global__ __launch_bounds__(256) void sparse_rows8_kernel(SparseRows8Args a) {
 /// straight on the gathered K bytes, q being a 15-bit fixed point split exactly into int8 halves
 /// (hi in column n, lo in column n + GQ of the B operand; the scheme of full_decode_kernel), so the
 /// scores are exact integers times the fixed point's step. A lane (head n, group g) of the score
-/// tile holds keys {16t + 4g + i}, the A-operand slice of O += W V; it gathers those 8 keys' V
+/// tile holds keys {16t + 4g + i}, the A-operand slice of O += W V; it reads those 8 keys' V
 /// bytes for dims 8n .. 8n + 7 (8 bytes a key, a row's 128 bytes over 16 lanes) and transposes
-/// them into the fp16 B operand in registers. K goes through a per-wave LDS tile, gathered as
-/// whole rows; as soon as a step's K is in the tile, the next step's K and V rows are requested, so
-/// both are in flight through this whole step.
-// three workgroups a CU (<= 168 VGPRs): room for the next step's V rows in flight beside this
-// step's (C5 sparse layer 0.403 ms at four with the V rows requested at a step's end, 0.380 at three,
-// 0.374 with them a step ahead)
+/// them into the fp16 B operand in registers. K and V go through per-wave LDS tiles, gathered as
+/// whole rows (each cache line once a load: the gathers' address work bounds this kernel); as soon
+/// as a step's rows are in the tiles, the next step's K and V rows are requested, so they are in
+/// flight through this whole step.
+// three workgroups a CU (C5 sparse layer 0.403 ms at four with the V rows requested at a step's
+// end in the A layout, 0.380 at three, 0.374 with them a step ahead, 0.361 through the tile)
 #ifndef SPR_OCC
 #define SPR_OCC 3
 #endif
+
 template <int GQ>
 __global__ __launch_bounds__(256, SPR_OCC) void sparse_rows8_rm_kernel(SparseRows8Args a) {
     typedef int i4_t __attribute__((ext_vector_type(4)));
@@ -516,6 +517,9 @@ __global__ __launch_bounds__(256, SPR_OCC) void sparse_rows8_rm_kernel(SparseRow
     // 16-byte piece p of key j at slot p ^ ((j >> 1) & 7), so that the A-layout reads (16 lanes,
     // 16 keys, one piece) fall in distinct bank groups
     __shared__ __attribute__((aligned(16))) u4_t kt[4][32][8];
+    // V rows the same way, in 32-bit words (lane (n, g) reads its 8 bytes of a key as two of them;
+    // read as one 8-byte vector over a narrower type, the compiler has taken one word for both)
+    __shared__ __attribute__((aligned(16))) uint32_t vt[4][32][32];
 
     // the key list: every load issued before the first store (rows clamped in range)
     const uint32_t* rows = sel ? a.idx + (size_t)r * a.idx_row_stride + (size_t)kvh * a.idx_kv_stride : nullptr;
@@ -596,7 +600,7 @@ __global__ __launch_bounds__(256, SPR_OCC) void sparse_rows8_rm_kernel(SparseRow
 
     // one 32-key step's raw bytes: K[2t + h] = key 16t + n, dims 64h + 16g ..; V[e] = key
     // 16(e / 4) + 4g + e % 4, dims 8n .. 8n + 7; lanes < 32 hold key t0 + lane's two scales
-    struct Raw { u4_t k[4]; u2_t v[8]; uint32_t s; };
+    struct Raw { u4_t k[4]; u4_t v[4]; uint32_t s; };   // k, v: rows 8i + lane / 8, 16 bytes a lane
     // rows as 32-bit byte offsets from the kv head's base (< 2^31: max_s * 128 a head)
     auto gather_k = [&](int t0, Raw& R) {   // k[i]: key 8i + lane / 8, bytes 16 (lane % 8) .. + 15
 #pragma unroll
@@ -605,12 +609,12 @@ __global__ __launch_bounds__(256, SPR_OCC) void sparse_rows8_rm_kernel(SparseRow
         const uint32_t row = sidx[t0 + (lane & 31)];
         R.s = lane < 32 ? ksc[row] : vsc[row];
     };
-    auto gather_v = [&](int t0, Raw& R) {
-        const u4_t ra = *(const u4_t*)(sidx + t0 + 4 * g), rb = *(const u4_t*)(sidx + t0 + 16 + 4 * g);
+    auto gather_v = [&](int t0, Raw& R) {   // v[i]: key 8i + lane / 8, bytes 16 (lane % 8) .. + 15
 #pragma unroll
-        for (int e = 0; e < 8; e++) R.v[e] = ld8(vb + (e < 4 ? ra[e] : rb[e - 4]) * (uint32_t)HD + 8 * n);
+        for (int i = 0; i < 4; i++)
+            R.v[i] = ld16(vb + sidx[t0 + 8 * i + (lane >> 3)] * (uint32_t)HD + 16 * (lane & 7));
     };
-    Raw A, Bv;   // Bv: the next step's V rows, requested a step ahead
+    Raw A;
     if (32 * w < nk) { gather_k(32 * w, A); gather_v(32 * w, A); }
     for (int t0 = 32 * w; t0 < nk; t0 += 128) {
         // scales to LDS: k scale of key j at [0][j], v scale (x 64) at [1][j]
@@ -620,10 +624,16 @@ __global__ __launch_bounds__(256, SPR_OCC) void sparse_rows8_rm_kernel(SparseRow
             const int j = 8 * i + (lane >> 3);
             kt[w][j][(lane & 7) ^ ((j >> 1) & 7)] = A.k[i];
         }
-        // the K registers are free again: the next step's K and V are requested now, a step ahead
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int j = 8 * i + (lane >> 3), sl = (lane & 7) ^ ((j >> 1) & 7);
+#pragma unroll
+            for (int q = 0; q < 4; q++) vt[w][j][4 * sl + q] = A.v[i][q];
+        }
+        // the registers are free again: the next step's K and V are requested now, a step ahead
         if (t0 + 128 < nk) {
             gather_k(t0 + 128, A);
-            gather_v(t0 + 128, Bv);
+            gather_v(t0 + 128, A);
         }
         wave_lds_sync();
         i4_t st[2];
@@ -694,20 +704,23 @@ __global__ __launch_bounds__(256, SPR_OCC) void sparse_rows8_rm_kernel(SparseRow
         // and e + 1 (0x80 flipped) into bytes 0 and 2, zero bytes 1 and 3: the fp16 subnormal pair
         // (128 + x) 2^-24
         OB = mfma16(wa, c128, OB);
+        u2_t va[8];   // keys 4g + e and 16 + 4g + e - 4, dims 8n .. 8n + 7, with 0x80 flipped
 #pragma unroll
-        for (int e = 0; e < 8; e++) A.v[e] ^= (u2_t){0x80808080u, 0x80808080u};
+        for (int e = 0; e < 8; e++) {
+            const int j = 16 * (e >> 2) + 4 * g + (e & 3), sl = (n >> 1) ^ ((j >> 1) & 7);
+            va[e] = (u2_t){vt[w][j][4 * sl + 2 * (n & 1)], vt[w][j][4 * sl + 2 * (n & 1) + 1]} ^
+                    (u2_t){0x80808080u, 0x80808080u};
+        }
 #pragma unroll
         for (int u = 0; u < 8; u++) {
             u4_t b;
 #pragma unroll
             for (int e = 0; e < 8; e += 2) {
                 const uint32_t sel = (u & 3) | (((u & 3) + 4) << 16) | 0x0C000C00u;
-                b[e / 2] = __builtin_amdgcn_perm(A.v[e + 1][u >> 2], A.v[e][u >> 2], sel);
+                b[e / 2] = __builtin_amdgcn_perm(va[e + 1][u >> 2], va[e][u >> 2], sel);
             }
             O[u] = mfma16(wa, __builtin_bit_cast(h8_t, b), O[u]);
         }
-#pragma unroll
-        for (int e = 0; e < 8; e++) A.v[e] = Bv.v[e];
         wave_lds_sync();   // the next step's scale stores come after every lane's reads
     }
 
