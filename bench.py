@@ -746,7 +746,7 @@ def render_table(d):
         ("C5 sliding prefill attention", f"{r(sl['ms_attention'], 4)} ms", f"{r(sl['tflops_attention'], 0)} TFLOP/s",
          f"{sl['mfma_util_attention']:.3f} of bf16 MFMA"),
         ("C5 sparse prefill layer", f"{r(sp['ms_layer'], 3)} ms", f"{r(sp['tflops_layer'], 0)} TFLOP/s (indexer + attention)",
-         f"{sp['mfma_util_layer']:.3f} of bf16 MFMA (gather-bound)"),
+         f"{sp['mfma_util_layer']:.3f} of bf16 MFMA (gather address work)"),
         ("MFMA-only probe", f"{r(d['mfma_ceiling']['ms'], 3)} ms", f"{r(d['mfma_ceiling']['tflops'], 0)} TFLOP/s",
          f"{d['mfma_ceiling']['frac_of_peak']:.3f} of bf16 MFMA"),
         ("decode sub-layer step (q/k/v GEMV, decode with append, o GEMV)",
